@@ -1,0 +1,377 @@
+"""Benchmark: achieved HBM bandwidth of jinf's per-layer elementwise / reduction
+kernels on one MI355X, with the CPU oracle timed beside it.
+
+A step is one pass of the hot path over one batch of synthetic input.  The
+default workload, llama3-8b-layer, is every Llama-3-8B-shaped configuration of
+the path:
+    rope     Q [512, 32, 128] + K [512, 8, 128] fp16, positions 0..511, theta 5e5
+    norm     fused residual add + RMSNorm fp16 [2048, 4096], eps 1e-5
+    swiglu   silu(gate) * up fp16 [2048, 14336]
+    gather   Q4_0 token-embedding gather 4096 ids of 128256 x 4096 -> fp16
+`--workload llama3-70b-decode` runs config 5 (64 sequences: residual+RMSNorm,
+RoPE 64/8 heads, masked fp32 softmax over len = pos + 1, SwiGLU, residual add).
+
+value = algorithmic bytes of a step / GPU time of a step (GB/s).  Algorithmic
+bytes count every input read once and every output written once.  Inputs are
+resident in HBM before timing; each kernel rotates over enough buffer sets
+(>= 512 MiB per kernel) that no launch can be served from the 256 MB
+Infinity Cache.  Kernel times come from HIP events recorded around every
+launch on the stream the kernels run on.
+
+Prints ONE JSON line (rank 0).  `--gpus N` with N > 1 exits: this build runs
+on one GPU.
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "jetson-inference_amd"))
+
+PEAK_GBS = 8000.0
+ROTATE_BYTES = 512 << 20
+METRIC = "achieved HBM GB/s & % of 8 TB/s peak per kernel; rows/sec at Llama-8B shape"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# --------------------------------------------------------------------------
+# workloads: each kernel is (name, bytes per launch, rows per launch,
+# row unit, list of per-set launch closures)
+# --------------------------------------------------------------------------
+
+class Kernel:
+    """One kernel of a step: its launch closures over rotating buffer sets,
+    algorithmic bytes and rows per launch, and (for the CPU baseline) the
+    tensors of set 0 with the oracle call that computes the same thing."""
+
+    def __init__(self, name, nbytes, rows, row_unit, launches, hip_name, set0=(), cpu=None):
+        self.name, self.nbytes, self.rows, self.row_unit = name, nbytes, rows, row_unit
+        self.launches, self.hip_name = launches, hip_name
+        self.set0, self.cpu = set0, cpu
+        self.i = 0
+        self.ms = 0.0
+        self.n = 0
+
+    def run(self):
+        self.launches[self.i % len(self.launches)]()
+        self.i += 1
+
+
+def n_sets(bytes_per_set):
+    return max(2, -(-ROTATE_BYTES // bytes_per_set))
+
+
+def randn16(torch, shape, mu, sigma, g):
+    return (torch.randn(shape, generator=g, device="cuda", dtype=torch.float32) * sigma
+            + mu).to(torch.float16)
+
+
+def q4_0_table(torch, n_vocab, n_embd, g):
+    nb = n_embd // 32
+    t = torch.randint(0, 256, (n_vocab, nb, 18), generator=g, device="cuda",
+                      dtype=torch.int32).to(torch.uint8)
+    d = (torch.randn((n_vocab, nb), generator=g, device="cuda") * 0.02).abs().to(torch.float16)
+    t[:, :, 0:2] = d.view(torch.uint8).view(n_vocab, nb, 2)
+    return t.view(n_vocab, nb * 18)
+
+
+def build_rope(torch, jinf, g, T, nh, nkv, hd, positions, keep):
+    nbytes = T * (nh + nkv) * hd * 2 * 2 + T * 4
+    sets = []
+    for _ in range(n_sets(nbytes)):
+        q = randn16(torch, (T, nh * hd), 0.0, 1.0, g)
+        k = randn16(torch, (T, nkv * hd), 0.0, 1.0, g)
+        p = positions.clone()
+        keep.append((q, k, p))
+        sets.append(lambda q=q, k=k, p=p: jinf.rope_rows(q, k, hd, p, 0, 500000.0))
+    return Kernel("rope", nbytes, T, "token rows", sets, "rope_vec_kernel", keep[-len(sets)],
+                  lambda o, q, k, p: o.rope_rows(q, k, hd, p, 0, 500000.0))
+
+
+def build_norm(torch, jinf, g, T, H, keep):
+    nbytes = 4 * T * H * 2 + H * 2
+    sets = []
+    for _ in range(n_sets(nbytes)):
+        r = randn16(torch, (T, H), 0.0, 1.0, g)
+        x = randn16(torch, (T, H), 0.0, 1.0, g)
+        w = randn16(torch, (H,), 1.0, 0.05, g)
+        y = torch.empty_like(x)
+        keep.append((r, x, w, y))
+        sets.append(lambda r=r, x=x, w=w, y=y: jinf.residual_rmsnorm_rows(r, x, w, 1e-5, out=y))
+    return Kernel("residual_rmsnorm", nbytes, T, "token rows", sets, "rmsnorm_vec_kernel",
+                  keep[-len(sets)][:3], lambda o, r, x, w: o.residual_rmsnorm_rows(r, x, w, 1e-5))
+
+
+def build_swiglu(torch, jinf, g, T, F, keep):
+    nbytes = 3 * T * F * 2
+    sets = []
+    for _ in range(n_sets(nbytes)):
+        gt = randn16(torch, (T, F), 0.0, 2.0, g)
+        up = randn16(torch, (T, F), 0.0, 2.0, g)
+        o = torch.empty_like(gt)
+        keep.append((gt, up, o))
+        sets.append(lambda gt=gt, up=up, o=o: jinf.swiglu(gt, up, out=o))
+    return Kernel("swiglu", nbytes, T, "token rows", sets, "ew_vec_kernel",
+                  keep[-len(sets)][:2], lambda o, gt, up: o.swiglu(gt, up))
+
+
+def build_residual_add(torch, jinf, g, T, H, keep):
+    nbytes = 3 * T * H * 2
+    sets = []
+    for _ in range(n_sets(nbytes)):
+        a = randn16(torch, (T, H), 0.0, 1.0, g)
+        b = randn16(torch, (T, H), 0.0, 1.0, g)
+        keep.append((a, b))
+        sets.append(lambda a=a, b=b: jinf.residual_add(a, b))
+    return Kernel("residual_add", nbytes, T, "token rows", sets, "ew_vec_kernel",
+                  keep[-len(sets)], lambda o, a, b: o.residual_add(a, b))
+
+
+def build_gather(torch, jinf, g, n_vocab, n_embd, n_ids, keep):
+    row_bytes = n_embd // 32 * 18
+    nbytes = n_ids * row_bytes + n_ids * 4 + n_ids * n_embd * 2
+    tables = [q4_0_table(torch, n_vocab, n_embd, g) for _ in range(2)]
+    keep.append(tables)
+    sets = []
+    for i in range(n_sets(n_ids * n_embd * 2)):
+        ids = torch.randint(0, n_vocab, (n_ids,), generator=g, device="cuda", dtype=torch.int32)
+        o = torch.empty((n_ids, n_embd), dtype=torch.float16, device="cuda")
+        t = tables[i % 2]
+        keep.append((ids, o))
+        sets.append(lambda t=t, ids=ids, o=o: jinf.embed_q4_0(t, ids, n_embd, torch.float16, out=o))
+    import numpy as np
+    return Kernel("q4_0_gather", nbytes, n_ids, "token ids", sets, "embed_q4_0_kernel",
+                  (tables[0], keep[-len(sets)][0]),
+                  lambda o, t, ids: o.embed_q4_0(t, ids, n_embd, np.float16))
+
+
+def build_softmax(torch, jinf, g, n_seq, n_heads, max_len, keep):
+    pos = torch.randint(0, max_len, (n_seq,), generator=g, device="cuda", dtype=torch.int32)
+    lens = pos + 1
+    live = int(lens.sum().item())
+    nbytes = 8 * n_heads * live + n_seq * 4
+    foot = n_seq * n_heads * max_len * 4 * 2
+    sets = []
+    for _ in range(n_sets(foot)):
+        s = torch.randn((n_seq * n_heads, max_len), generator=g, device="cuda") * 3.0
+        o = torch.empty_like(s)
+        lc = lens.clone()
+        keep.append((s, o, lc))
+        sets.append(lambda s=s, o=o, lc=lc: jinf.softmax_rows(s, lc, n_heads, 1.0, out=o))
+    return Kernel("masked_softmax", nbytes, n_seq * n_heads, "score rows", sets,
+                  "softmax_vec_kernel", (keep[-len(sets)][0], lens),
+                  lambda o, s, lc: o.softmax_rows(s, lc, n_heads, 1.0))
+
+
+def workload(name, torch, jinf, seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    keep = []
+    if name == "llama3-8b-layer":
+        ks = [build_rope(torch, jinf, g, 512, 32, 8, 128,
+                         torch.arange(512, dtype=torch.int32, device="cuda"), keep),
+              build_norm(torch, jinf, g, 2048, 4096, keep),
+              build_swiglu(torch, jinf, g, 2048, 14336, keep),
+              build_gather(torch, jinf, g, 128256, 4096, 4096, keep)]
+        cfg = {"workload": name, "shapes": "Llama-3-8B: hidden 4096, 32/8 heads x 128, FFN 14336, "
+               "vocab 128256; RoPE T=512, norm/SwiGLU T=2048, 4096 token ids",
+               "storage": "f16 activations, Q4_0 table", "baseline_configs": [2, 3, 4]}
+    elif name == "llama3-70b-decode":
+        pos = torch.randint(0, 8192, (64,), generator=g, device="cuda", dtype=torch.int32)
+        ks = [build_norm(torch, jinf, g, 64, 8192, keep),
+              build_rope(torch, jinf, g, 64, 64, 8, 128, pos, keep),
+              build_softmax(torch, jinf, g, 64, 64, 8192, keep),
+              build_swiglu(torch, jinf, g, 64, 28672, keep),
+              build_residual_add(torch, jinf, g, 64, 8192, keep)]
+        cfg = {"workload": name, "shapes": "Llama-3-70B decode, 64 sequences: hidden 8192, "
+               "64/8 heads x 128, FFN 28672, score rows 4096 x stride 8192, len = pos + 1",
+               "storage": "f16 activations, f32 scores", "baseline_configs": [5]}
+    elif name in ("rope", "norm", "swiglu", "gather", "softmax"):
+        b = {"rope": lambda: build_rope(torch, jinf, g, 512, 32, 8, 128,
+                                        torch.arange(512, dtype=torch.int32, device="cuda"), keep),
+             "norm": lambda: build_norm(torch, jinf, g, 2048, 4096, keep),
+             "swiglu": lambda: build_swiglu(torch, jinf, g, 2048, 14336, keep),
+             "gather": lambda: build_gather(torch, jinf, g, 128256, 4096, 4096, keep),
+             "softmax": lambda: build_softmax(torch, jinf, g, 64, 64, 8192, keep)}[name]
+        ks = [b()]
+        cfg = {"workload": name, "shapes": "single kernel, BASELINE.json shape"}
+    else:
+        raise SystemExit(f"unknown workload {name}")
+    return ks, cfg, keep
+
+
+# --------------------------------------------------------------------------
+# CPU baseline: the oracle (a C restatement of the reference arithmetic) on
+# the host cores, same workload shapes, on a copy of buffer set 0
+# --------------------------------------------------------------------------
+
+def cpu_baseline(ks, threads, budget_s):
+    sys.path.insert(0, ROOT)
+    import oracle
+
+    oracle.set_threads(threads)
+    per = {}
+    total_s = 0.0
+    for k in ks:
+        arrays = [t.cpu().numpy() for t in k.set0]
+        fn = lambda: k.cpu(oracle, *arrays)  # noqa: E731
+        fn()  # warm-up
+        times = []
+        t_end = time.perf_counter() + budget_s / len(ks)
+        while True:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() > t_end and len(times) >= 3:
+                break
+        med = sorted(times)[len(times) // 2]
+        per[k.name] = {"GB/s": k.nbytes / med / 1e9, "runs": len(times)}
+        total_s += med
+    step_bytes = sum(k.nbytes for k in ks)
+    return {"value": round(step_bytes / total_s / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "per_kernel_GBs": {n: round(v["GB/s"], 3) for n, v in per.items()},
+            "runs": {n: v["runs"] for n, v in per.items()}, "s_per_step": round(total_s, 5)}
+
+
+# --------------------------------------------------------------------------
+# rocprof-derived traffic figure, if a committed summary exists
+# --------------------------------------------------------------------------
+
+def traffic_from_profiles(kernel):
+    path = os.path.join(ROOT, "profiles", f"{kernel}_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.]+)", open(path).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="llama3-8b-layer")
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="bounded CPU-baseline sample (0 = skip)")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, host cores)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only; the kernels are "
+                          "row-independent and shard by rows with no exchange (see DESIGN.md)",
+                          "n_gpus_requested": max(args.gpus, world)}), flush=True)
+        sys.exit(2)
+
+    import torch
+
+    import jinf_amd
+
+    jinf_amd.lib()
+    torch.cuda.set_device(0)
+    log(f"{jinf_amd.version()} on {torch.cuda.get_device_name(0)}; workload {args.workload}")
+    ks, cfg, keep = workload(args.workload, torch, jinf_amd, args.seed)
+    torch.cuda.synchronize()
+    log("buffers ready: " + ", ".join(f"{k.name} x{len(k.launches)} sets" for k in ks))
+
+    for _ in range(args.warmup):
+        for k in ks:
+            k.run()
+    torch.cuda.synchronize()
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(ks) + 1)]
+           for _ in range(args.steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for s in range(args.steps):
+        e = evs[s]
+        e[0].record()
+        for i, k in enumerate(ks):
+            k.run()
+            e[i + 1].record()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = start.elapsed_time(end)
+    for s in range(args.steps):
+        for i, k in enumerate(ks):
+            k.ms += evs[s][i].elapsed_time(evs[s][i + 1])
+            k.n += 1
+    ms_step = total_ms / args.steps
+    step_bytes = sum(k.nbytes for k in ks)
+    kern_ms = sum(k.ms for k in ks) / args.steps
+
+    per = {}
+    for k in ks:
+        us = k.ms / k.n * 1e3
+        gbs = k.nbytes / (us * 1e-6) / 1e9
+        per[k.name] = {"us": round(us, 3), "GB/s": round(gbs, 1),
+                       "frac_of_8TBs": round(gbs / PEAK_GBS, 4),
+                       "rows_per_s": round(k.rows / (us * 1e-6), 1), "row_unit": k.row_unit,
+                       "bytes": k.nbytes, "sets": len(k.launches)}
+    dom = max(ks, key=lambda k: k.ms)
+    dom_us = dom.ms / dom.n * 1e3
+    dom_gbs = dom.nbytes / (dom_us * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "kernel": dom.name, "hip_kernel": dom.hip_name,
+                "achieved": round(dom_gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom_gbs / PEAK_GBS, 4), "bytes_per_launch": dom.nbytes,
+                "avg_launch_us": round(dom_us, 3),
+                "traffic": traffic_from_profiles(dom.name)}
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        try:
+            cpu = cpu_baseline(ks, threads, args.cpu_seconds)
+            cpu["kind"] = "port"
+            cpu["sample"] = (f"every kernel of the step at full shape on a host copy of buffer "
+                             f"set 0; median of repeated runs, {args.cpu_seconds:.0f} s budget; "
+                             f"oracle C (-O3, no fast-math), {threads} OpenMP threads")
+            cpu["cpu_model"] = cpu_model()
+        except Exception as exc:  # the baseline is reported, never required
+            log(f"cpu baseline failed: {exc!r}")
+            cpu = None
+
+    out = {
+        "metric": METRIC,
+        "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 math, f16 storage",
+        "data": "synthetic: seeded torch RNG on device (N(mu, sigma), sigma = std); "
+                "Q4_0 scales fp16(|N(0,0.02)|), nibbles uniform",
+        "config": dict(cfg, step_bytes=step_bytes),
+        "frac_of_peak": round(step_bytes / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4),
+        "kernel_ms_per_step": round(kern_ms, 5),
+        "wall_s_timed": round(wall, 4),
+        "kernels": per,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    main()

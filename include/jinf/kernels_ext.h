@@ -1,0 +1,116 @@
+/*
+ * jinf MI355X kernels: batched / fp16 / fused entry points.
+ *
+ * The reference launchers (kernels.h) take one fp32 token row per call.  These
+ * entry points run the same arithmetic over many rows per launch, in fp16 or
+ * fp32 storage, and fuse the residual add into RMSNorm.  They have no
+ * one-to-one counterpart in the reference; each names the reference code
+ * whose semantics it batches.
+ *
+ * Common rules:
+ *   - pointers are DEVICE pointers; all work is asynchronous on `stream`;
+ *     nothing allocates, frees or synchronizes; no mutable global state;
+ *   - `ld_*` arguments are row strides in ELEMENTS of the storage type;
+ *   - fp16 tensors are IEEE binary16 stored as uint16_t; arithmetic is fp32
+ *     with one round-to-nearest-even to fp16 per stored value;
+ *   - return JINF_HIP_OK, JINF_HIP_ERR_INVALID (bad argument, nothing
+ *     enqueued) or JINF_HIP_ERR_DEVICE (the launch failed).  The values equal
+ *     jinf_status JINF_OK / JINF_ERR_CUDA / JINF_ERR_INVALID
+ *     (reference include/jinf/common.h:9-16);
+ *   - zero rows / zero columns is JINF_HIP_OK with nothing enqueued.
+ *
+ * This header includes no HIP or CUDA header.
+ */
+#ifndef JINF_KERNELS_EXT_H
+#define JINF_KERNELS_EXT_H
+
+#include <stdint.h>
+#include "kernels.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum jinf_hip_status {
+    JINF_HIP_OK = 0,
+    JINF_HIP_ERR_DEVICE = 3,
+    JINF_HIP_ERR_INVALID = 5
+};
+
+/* Storage types; codes equal jinf_qtype F32/F16 (reference include/jinf/quant.h:8-11). */
+enum jinf_hip_dtype {
+    JINF_HIP_F32 = 0,
+    JINF_HIP_F16 = 1
+};
+
+/* Library version string and the gfx target it was built for. */
+const char* jinf_hip_version(void);
+
+/* Per-row RMSNorm: out[r,i] = (x[r,i] * rs_r) * w[i],
+ * rs_r = 1/sqrt(sum_i x[r,i]^2 / n + eps).  act_type selects fp32/fp16
+ * storage of in/out; weight_type 0 = fp32, 1 = fp16.  out may alias in.
+ * Semantics of cuda/rmsnorm_kernel.cu:9-61, batched over rows. */
+int jinf_rmsnorm_rows(void* out, int ld_out, const void* in, int ld_in,
+                      const void* weight, int n_rows, int n, float eps,
+                      int act_type, int weight_type, hipStream_t stream);
+
+/* Fused residual add + RMSNorm, one HBM pass:
+ *   residual[r,i] = residual[r,i] + delta[r,i]   (stored, rounded to act_type)
+ *   out[r,i]      = rmsnorm(residual[r,:])[i] * w[i]
+ * The norm consumes the rounded stored residual, exactly like the reference's
+ * separate residual_add then rmsnorm launches (src/engine.cpp:466->487,
+ * 508->429).  out may alias delta (not residual). */
+int jinf_residual_rmsnorm_rows(void* out, int ld_out, void* residual, int ld_res,
+                               const void* delta, int ld_delta, const void* weight,
+                               int n_rows, int n, float eps, int act_type,
+                               int weight_type, hipStream_t stream);
+
+/* In-place interleaved RoPE over n_tokens tokens.  q is [n_tokens, ld_q] with
+ * n_heads*head_dim live elements per token, k is [n_tokens, ld_k] with
+ * n_heads_kv*head_dim.  Token t uses positions[t], or pos0 + t when
+ * positions is NULL.  head_dim even, <= 512.  Semantics of
+ * cuda/rope_kernel.cu:8-50 applied per token. */
+int jinf_rope_rows(void* q, int ld_q, void* k, int ld_k, const int32_t* positions,
+                   int pos0, int n_tokens, int head_dim, int n_heads, int n_heads_kv,
+                   float freq_base, int act_type, hipStream_t stream);
+
+/* SwiGLU: out[r,i] = silu(gate[r,i]) * up[r,i], silu(g) = g / (1 + exp(-g)).
+ * out may alias gate or up.  Semantics of cuda/silu_kernel.cu:6-18, batched. */
+int jinf_swiglu_rows(void* out, int ld_out, const void* gate, int ld_gate,
+                     const void* up, int ld_up, int n_rows, int n, int act_type,
+                     hipStream_t stream);
+
+/* Residual add a[r,i] += b[r,i] (rounded to act_type).
+ * Semantics of cuda/matmul_kernels.cu:189-194, batched. */
+int jinf_residual_add_rows(void* a, int ld_a, const void* b, int ld_b, int n_rows,
+                           int n, int act_type, hipStream_t stream);
+
+/* Masked fp32 row softmax.  Row r has live length
+ *   L_r = lens ? clamp(lens[r / rows_per_len], 0, n_cols) : n_cols
+ * and out[r, j] = exp(s_j - m) / sum_k exp(s_k - m) for j < L_r, with
+ * s_j = scale * in[r, j] and m = max_j s_j.  Elements j >= L_r are neither
+ * read nor written; L_r == 0 leaves the row untouched.  out may alias in.
+ * rows_per_len lets all query heads of one sequence share one length entry.
+ * Semantics of cuda/softmax_kernel.cu:8-42 and the attention softmax phase
+ * cuda/attention_kernel.cu:59-87 (length n_past = pos + 1). */
+int jinf_softmax_rows_f32(float* out, int ld_out, const float* in, int ld_in,
+                          int n_rows, int n_cols, const int32_t* lens,
+                          int rows_per_len, float scale, hipStream_t stream);
+
+/* GGUF Q4_0 token-embedding gather + dequant.  table holds n_vocab rows of
+ * n_embd/32 blocks (18 bytes each, any byte alignment); output row i
+ * (ld_out elements apart) is the dequantized table row ids[i], or table row i
+ * when ids is NULL.  An id outside [0, n_vocab) yields a row of +0.0 (the
+ * reference does not check ids, src/engine.cpp:311-312).  out_type fp32 or
+ * fp16; fp16 values are one RNE rounding of the exact fp32 product, so the
+ * result is bit-exact.  n_embd % 32 == 0.  Semantics of
+ * src/engine.cpp:311-317 + cuda/dequant_kernels.cu:6-21 + src/quant.cpp:49-60. */
+int jinf_embed_q4_0(void* out, int ld_out, const void* table, int n_vocab,
+                    int n_embd, const int32_t* ids, int n_ids, int out_type,
+                    hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JINF_KERNELS_EXT_H */

@@ -1,0 +1,131 @@
+// Device-side helpers shared by the jinf gfx950 kernels: binary16 <-> binary32
+// conversion, 16-byte vector access, and wave64 / workgroup reductions.
+//
+// Every reduction here is deterministic: partials are combined in a fixed
+// order, so a kernel run twice on the same input gives identical bits.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace jinf {
+
+constexpr int kWave = 64;
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// Exact binary16 -> binary32 widening (subnormals, -0, Inf, NaN preserved);
+// plays the role of half_to_float (reference cuda/cuda_utils.cuh:10-14).
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// binary32 -> binary16 with round-to-nearest-even (default MODE: RNE, fp16
+// denormals kept).  The conversion is written as an explicit instruction so
+// the compiler cannot merge it with the fp32 multiply or add that produced the
+// value (it otherwise folds them into one v_fma_mix*_f16 with a +0 addend,
+// which need not round through fp32 first and turns a -0 product into +0).
+// Every stored fp16 value is thus fl16(fl32(expression)).
+__device__ __forceinline__ uint16_t f2h(float f) {
+    uint32_t r;
+    asm("v_cvt_f16_f32 %0, %1" : "=v"(r) : "v"(f));
+    return (uint16_t)r;
+}
+
+// Two binary32 -> packed binary16 (lo in bits 0..15), RNE, same guarantee.
+__device__ __forceinline__ uint32_t f2h2(float lo, float hi) {
+    uint32_t r;
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+    return r;
+}
+
+// Storage traits: a "chunk" is one 16-byte vector of the storage type.
+template <typename T> struct Act;
+
+template <> struct Act<float> {
+    static constexpr int kElems = 4;
+    __device__ static __forceinline__ void load(const float* p, float (&v)[4]) {
+        const float4 x = *reinterpret_cast<const float4*>(p);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+    }
+    __device__ static __forceinline__ void store(float* p, const float (&v)[4]) {
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    __device__ static __forceinline__ float load1(const float* p) { return *p; }
+    __device__ static __forceinline__ void store1(float* p, float v) { *p = v; }
+    // Round an fp32 value to the storage precision (identity for fp32).
+    __device__ static __forceinline__ float round(float v) { return v; }
+};
+
+template <> struct Act<uint16_t> {
+    static constexpr int kElems = 8;
+    __device__ static __forceinline__ void load(const uint16_t* p, float (&v)[8]) {
+        const uint4 x = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = h2f((uint16_t)(w[i] & 0xFFFFu));
+            v[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
+        }
+    }
+    __device__ static __forceinline__ void store(uint16_t* p, const float (&v)[8]) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = f2h2(v[2 * i], v[2 * i + 1]);
+        *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    __device__ static __forceinline__ float load1(const uint16_t* p) { return h2f(*p); }
+    __device__ static __forceinline__ void store1(uint16_t* p, float v) { *p = f2h(v); }
+    __device__ static __forceinline__ float round(float v) { return h2f(f2h(v)); }
+};
+
+// Weight element read (fp32 or fp16 storage), widened exactly to fp32.
+__device__ __forceinline__ float wload(const float* w, int i) { return w[i]; }
+__device__ __forceinline__ float wload(const uint16_t* w, int i) { return h2f(w[i]); }
+
+// ---- wave64 reductions (butterfly: every lane ends with the full result) ----
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Workgroup reductions.  blockDim.x must be a multiple of 64 and at most 1024.
+// `lds` holds one slot per wave; each thread folds the per-wave partials in
+// wave order, so every thread returns the same value without a second
+// barrier.  A trailing barrier makes `lds` safe to reuse by the caller.
+__device__ __forceinline__ double block_sum(double v, double* lds) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    if (lane == 0) lds[wid] = v;
+    __syncthreads();
+    const int nw = blockDim.x / kWave;
+    double s = lds[0];
+    for (int i = 1; i < nw; ++i) s += lds[i];
+    __syncthreads();
+    return s;
+}
+
+__device__ __forceinline__ float block_max(float v, float* lds) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    if (lane == 0) lds[wid] = v;
+    __syncthreads();
+    const int nw = blockDim.x / kWave;
+    float m = lds[0];
+    for (int i = 1; i < nw; ++i) m = fmaxf(m, lds[i]);
+    __syncthreads();
+    return m;
+}
+
+}  // namespace jinf

@@ -1,0 +1,236 @@
+// RMSNorm and fused residual-add + RMSNorm for gfx950.
+//
+// Semantics (reference cuda/rmsnorm_kernel.cu:9-61, residual add
+// cuda/matmul_kernels.cu:189-194, sequencing src/engine.cpp:466->487):
+//   h_i  = x_i                      (plain norm), or
+//   h_i  = round_act(r_i + x_i)     (fused; stored back to the residual)
+//   ss   = sum_i h_i^2
+//   rs   = 1 / sqrt(ss / n + eps)   (ss/n and +eps in fp32)
+//   y_i  = round_act((h_i * rs) * w_i)
+//
+// Design: one workgroup per row.  The row is held in registers (up to
+// kNormCPT 16-byte chunks per thread), so every input byte is read from HBM
+// once and every output byte written once: the fused kernel moves 4 rows of
+// traffic (r, x in; r', y out) instead of the reference's 3 + 2..3 rows for
+// separate residual_add and rmsnorm launches.  The sum of squares is
+// accumulated in fp64 (h_i^2 is exact in fp64), reduced across the wave by
+// butterfly shuffles and across waves through LDS in a fixed order; 1/sqrt is
+// evaluated in fp64 and rounded once.  The result is therefore independent of
+// the launch shape and matches a sequential fp64 sum to within fp32 rounding.
+// Rows longer than the register capacity, or not 16-byte aligned, take a
+// two-pass loop kernel that re-reads the row.
+#include "jinf_device.h"
+#include "jinf_host.h"
+#include "jinf/kernels.h"
+
+namespace jinf {
+
+constexpr int kNormCPT = 4;  // 16-byte chunks per thread held in registers
+
+// E consecutive weight elements widened to fp32 (vector loads).
+template <int E> __device__ __forceinline__ void wvec(const float* w, float (&v)[E]) {
+#pragma unroll
+    for (int i = 0; i < E; i += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(w + i);
+        v[i] = x.x; v[i + 1] = x.y; v[i + 2] = x.z; v[i + 3] = x.w;
+    }
+}
+template <int E> __device__ __forceinline__ void wvec(const uint16_t* w, float (&v)[E]) {
+    if constexpr (E == 8) {
+        const uint4 x = *reinterpret_cast<const uint4*>(w);
+        const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = h2f((uint16_t)(u[i] & 0xFFFFu));
+            v[2 * i + 1] = h2f((uint16_t)(u[i] >> 16));
+        }
+    } else {
+        const uint2 x = *reinterpret_cast<const uint2*>(w);
+        const uint32_t u[2] = {x.x, x.y};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            v[2 * i] = h2f((uint16_t)(u[i] & 0xFFFFu));
+            v[2 * i + 1] = h2f((uint16_t)(u[i] >> 16));
+        }
+    }
+}
+
+// rs = 1/sqrt(fl32(fl32(ss)/n) + eps), the sqrt and divide in fp64 and
+// rounded once to fp32.
+__device__ __forceinline__ float rms_scale(double ss, int n, float eps) {
+#pragma clang fp contract(off)
+    const float m = (float)ss / (float)n;
+    const float t = m + eps;
+    return (float)(1.0 / sqrt((double)t));
+}
+
+template <typename TA, typename TW, bool FUSED>
+__global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(
+    TA* out, int ld_out, TA* res, int ld_res, const TA* in, int ld_in,
+    const TW* __restrict__ w, int n, float eps) {
+#pragma clang fp contract(off)
+    using A = Act<TA>;
+    constexpr int E = A::kElems;
+    __shared__ double red[16];
+    const int64_t row = blockIdx.x;
+    const int nch = n / E;
+    const int bs = blockDim.x;
+    const TA* x = in + row * ld_in;
+    TA* r = FUSED ? res + row * ld_res : nullptr;
+
+    float h[kNormCPT][E];
+    float d[kNormCPT][E];
+    // Issue every load of the row before any store (out may alias in).
+#pragma unroll
+    for (int j = 0; j < kNormCPT; ++j) {
+        const int c = threadIdx.x + j * bs;
+        if (c < nch) {
+            A::load(x + (int64_t)c * E, h[j]);
+            if constexpr (FUSED) A::load(r + (int64_t)c * E, d[j]);
+        }
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < kNormCPT; ++j) {
+        const int c = threadIdx.x + j * bs;
+        if (c < nch) {
+            if constexpr (FUSED) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) h[j][e] = A::round(d[j][e] + h[j][e]);
+                A::store(r + (int64_t)c * E, h[j]);
+            }
+#pragma unroll
+            for (int e = 0; e < E; ++e) ss = fma((double)h[j][e], (double)h[j][e], ss);
+        }
+    }
+    ss = block_sum(ss, red);
+    const float rs = rms_scale(ss, n, eps);
+    TA* y = out + row * ld_out;
+#pragma unroll
+    for (int j = 0; j < kNormCPT; ++j) {
+        const int c = threadIdx.x + j * bs;
+        if (c < nch) {
+            float wv[E];
+            wvec<E>(w + c * E, wv);
+            float o[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) o[e] = (h[j][e] * rs) * wv[e];
+            A::store(y + (int64_t)c * E, o);
+        }
+    }
+}
+
+// Any length / alignment: pass 1 forms (and for the fused form stores) h and
+// its sum of squares, pass 2 re-reads h and writes y.  Each element is read
+// and written by the same thread in both passes, so in-place use is safe.
+template <typename TA, typename TW, bool FUSED>
+__global__ __launch_bounds__(1024) void rmsnorm_loop_kernel(
+    TA* out, int ld_out, TA* res, int ld_res, const TA* in, int ld_in,
+    const TW* __restrict__ w, int n, float eps) {
+#pragma clang fp contract(off)
+    using A = Act<TA>;
+    __shared__ double red[16];
+    const int64_t row = blockIdx.x;
+    const TA* x = in + row * ld_in;
+    TA* r = FUSED ? res + row * ld_res : nullptr;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = A::load1(x + i);
+        if constexpr (FUSED) {
+            v = A::round(A::load1(r + i) + v);
+            A::store1(r + i, v);
+        }
+        ss = fma((double)v, (double)v, ss);
+    }
+    ss = block_sum(ss, red);
+    const float rs = rms_scale(ss, n, eps);
+    TA* y = out + row * ld_out;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = FUSED ? A::load1(r + i) : A::load1(x + i);
+        A::store1(y + i, (v * rs) * wload(w, i));
+    }
+}
+
+template <typename TA, typename TW, bool FUSED>
+static int rmsnorm_launch(void* out, int ld_out, void* res, int ld_res, const void* in,
+                          int ld_in, const void* w, int n_rows, int n, float eps,
+                          hipStream_t stream) {
+    constexpr int E = Act<TA>::kElems;
+    constexpr int kVec = 16;
+    const bool vec = (n % E == 0) && aligned(out, kVec) && aligned(in, kVec) &&
+                     aligned(w, kVec) && ((int64_t)ld_out * sizeof(TA)) % kVec == 0 &&
+                     ((int64_t)ld_in * sizeof(TA)) % kVec == 0 &&
+                     (!FUSED || (aligned(res, kVec) && ((int64_t)ld_res * sizeof(TA)) % kVec == 0));
+    const int nch = n / E;
+    int bs = round_up((nch + kNormCPT - 1) / kNormCPT, kWave);
+    // Few rows cannot fill 256 CUs: spread each row over more lanes so the
+    // row's loads are all in flight at once.
+    if (n_rows < 1024) bs = bs > round_up(nch, kWave) ? bs : round_up(nch, kWave);
+    if (bs > 1024) bs = round_up((nch + kNormCPT - 1) / kNormCPT, kWave);
+    if (bs < kWave) bs = kWave;
+    TA* o = static_cast<TA*>(out);
+    TA* r = static_cast<TA*>(res);
+    const TA* x = static_cast<const TA*>(in);
+    const TW* wt = static_cast<const TW*>(w);
+    if (vec && bs <= 1024)
+        return launch(rmsnorm_vec_kernel<TA, TW, FUSED>, dim3(n_rows), dim3(bs), 0, stream,
+                      o, ld_out, r, ld_res, x, ld_in, wt, n, eps);
+    const int lbs = n >= 1024 ? 1024 : round_up(n, kWave);
+    return launch(rmsnorm_loop_kernel<TA, TW, FUSED>, dim3(n_rows), dim3(lbs), 0, stream,
+                  o, ld_out, r, ld_res, x, ld_in, wt, n, eps);
+}
+
+template <bool FUSED>
+static int rmsnorm_dispatch(void* out, int ld_out, void* res, int ld_res, const void* in,
+                            int ld_in, const void* w, int n_rows, int n, float eps,
+                            int act_type, int weight_type, hipStream_t stream) {
+    if (n_rows < 0 || n < 0) return JINF_HIP_ERR_INVALID;
+    if (n_rows == 0 || n == 0) return JINF_HIP_OK;
+    if (!out || !in || !w || (FUSED && !res)) return JINF_HIP_ERR_INVALID;
+    if (ld_out < n || ld_in < n || (FUSED && ld_res < n)) return JINF_HIP_ERR_INVALID;
+    if (FUSED && res == out) return JINF_HIP_ERR_INVALID;
+    if (act_type == JINF_HIP_F32) {
+        if (weight_type == JINF_HIP_F32)
+            return rmsnorm_launch<float, float, FUSED>(out, ld_out, res, ld_res, in, ld_in, w,
+                                                       n_rows, n, eps, stream);
+        if (weight_type == JINF_HIP_F16)
+            return rmsnorm_launch<float, uint16_t, FUSED>(out, ld_out, res, ld_res, in, ld_in,
+                                                          w, n_rows, n, eps, stream);
+    } else if (act_type == JINF_HIP_F16) {
+        if (weight_type == JINF_HIP_F32)
+            return rmsnorm_launch<uint16_t, float, FUSED>(out, ld_out, res, ld_res, in, ld_in,
+                                                          w, n_rows, n, eps, stream);
+        if (weight_type == JINF_HIP_F16)
+            return rmsnorm_launch<uint16_t, uint16_t, FUSED>(out, ld_out, res, ld_res, in,
+                                                             ld_in, w, n_rows, n, eps, stream);
+    }
+    return JINF_HIP_ERR_INVALID;
+}
+
+}  // namespace jinf
+
+extern "C" int jinf_rmsnorm_rows(void* out, int ld_out, const void* in, int ld_in,
+                                 const void* weight, int n_rows, int n, float eps,
+                                 int act_type, int weight_type, hipStream_t stream) {
+    return jinf::rmsnorm_dispatch<false>(out, ld_out, nullptr, 0, in, ld_in, weight, n_rows, n,
+                                         eps, act_type, weight_type, stream);
+}
+
+extern "C" int jinf_residual_rmsnorm_rows(void* out, int ld_out, void* residual, int ld_res,
+                                          const void* delta, int ld_delta, const void* weight,
+                                          int n_rows, int n, float eps, int act_type,
+                                          int weight_type, hipStream_t stream) {
+    return jinf::rmsnorm_dispatch<true>(out, ld_out, residual, ld_res, delta, ld_delta, weight,
+                                        n_rows, n, eps, act_type, weight_type, stream);
+}
+
+// Drop-in for the reference launcher (cuda/rmsnorm_kernel.cu:65-85): one fp32
+// row; weight_type 1 = fp16 weight, every other value = fp32 weight.
+extern "C" void jinf_cuda_rmsnorm(float* output, const float* input, const void* weight, int n,
+                                  float eps, int weight_type, hipStream_t stream) {
+    if (n <= 0) return;
+    const int wt = weight_type == JINF_HIP_F16 ? JINF_HIP_F16 : JINF_HIP_F32;
+    const int st = jinf::rmsnorm_dispatch<false>(output, n, nullptr, 0, input, n, weight, 1, n,
+                                                 eps, JINF_HIP_F32, wt, stream);
+    if (st == JINF_HIP_ERR_INVALID) JINF_LOG("jinf_cuda_rmsnorm: invalid argument (n=%d)", n);
+}

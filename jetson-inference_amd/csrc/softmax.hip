@@ -1,0 +1,160 @@
+// Masked fp32 row softmax for gfx950.
+//
+// Semantics (reference cuda/softmax_kernel.cu:8-42; the live masked form is the
+// softmax phase of cuda/attention_kernel.cu:59-87 over n_past = pos + 1
+// scores):
+//   s_j = scale * x_j                 for j < L (L = live length of the row)
+//   m   = max_j s_j
+//   e_j = exp(s_j - m)
+//   y_j = e_j * (1 / sum_j e_j)
+// Elements j >= L are neither read nor written.
+//
+// Design: one workgroup per row.  The live part of the row is loaded once into
+// registers (kSmCPT float4 chunks per thread, so up to 32 KiB per row with
+// 256 lanes), exponentiated once, and written once: one HBM read and one write
+// per element, against the reference's three reads and two exp evaluations.
+// Max and sum are wave64 butterflies plus one LDS exchange; the sum is
+// accumulated in fp64 so its rounding does not depend on the launch shape.
+// Rows longer than the register capacity (or unaligned rows) take a two-pass
+// kernel that keeps an online (max, sum) pair per thread and re-reads the row
+// for the write pass.
+#include <math.h>
+
+#include "jinf_device.h"
+#include "jinf_host.h"
+#include "jinf/kernels.h"
+
+namespace jinf {
+
+constexpr int kSmCPT = 8;  // float4 chunks per thread kept in registers
+
+__device__ __forceinline__ int live_len(const int32_t* lens, int rows_per_len, int n_cols,
+                                        int64_t row) {
+    if (!lens) return n_cols;
+    int L = lens[row / rows_per_len];
+    L = L < 0 ? 0 : L;
+    return L > n_cols ? n_cols : L;
+}
+
+__global__ __launch_bounds__(1024) void softmax_vec_kernel(
+    float* out, int ld_out, const float* in, int ld_in, int n_cols, const int32_t* lens,
+    int rows_per_len, float scale) {
+#pragma clang fp contract(off)
+    __shared__ float redf[16];
+    __shared__ double redd[16];
+    const int64_t row = blockIdx.x;
+    const int L = live_len(lens, rows_per_len, n_cols, row);
+    if (L == 0) return;  // uniform over the workgroup
+    const float* x = in + row * ld_in;
+    float* y = out + row * ld_out;
+    const int bs = blockDim.x;
+    const int nfull = L >> 2;  // whole float4 chunks
+    const float ninf = -INFINITY;
+
+    float v[kSmCPT][4];
+#pragma unroll
+    for (int j = 0; j < kSmCPT; ++j) {
+        const int c = threadIdx.x + j * bs;
+        if (c < nfull) {
+            const float4 t = *reinterpret_cast<const float4*>(x + 4 * c);
+            v[j][0] = t.x; v[j][1] = t.y; v[j][2] = t.z; v[j][3] = t.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[j][e] = (4 * c + e < L) ? x[4 * c + e] : ninf;
+        }
+    }
+    float mx = ninf;
+#pragma unroll
+    for (int j = 0; j < kSmCPT; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[j][e] = v[j][e] * scale;  // -inf * scale stays -inf for scale > 0
+            mx = fmaxf(mx, v[j][e]);
+        }
+    mx = block_max(mx, redf);
+    double sum = 0.0;
+#pragma unroll
+    for (int j = 0; j < kSmCPT; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int idx = 4 * (threadIdx.x + j * bs) + e;
+            const float ex = idx < L ? expf(v[j][e] - mx) : 0.0f;
+            v[j][e] = ex;
+            sum += (double)ex;
+        }
+    sum = block_sum(sum, redd);
+    const float inv = 1.0f / (float)sum;
+#pragma unroll
+    for (int j = 0; j < kSmCPT; ++j) {
+        const int c = threadIdx.x + j * bs;
+        if (c < nfull) {
+            *reinterpret_cast<float4*>(y + 4 * c) =
+                make_float4(v[j][0] * inv, v[j][1] * inv, v[j][2] * inv, v[j][3] * inv);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (4 * c + e < L) y[4 * c + e] = v[j][e] * inv;
+        }
+    }
+}
+
+// Any length / alignment.  Pass 1: per-thread online (max, sum); the pairs
+// are merged across the workgroup.  Pass 2 re-reads and writes.
+__global__ __launch_bounds__(1024) void softmax_loop_kernel(
+    float* out, int ld_out, const float* in, int ld_in, int n_cols, const int32_t* lens,
+    int rows_per_len, float scale) {
+#pragma clang fp contract(off)
+    __shared__ float redf[16];
+    __shared__ double redd[16];
+    const int64_t row = blockIdx.x;
+    const int L = live_len(lens, rows_per_len, n_cols, row);
+    if (L == 0) return;
+    const float* x = in + row * ld_in;
+    float* y = out + row * ld_out;
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < L; i += blockDim.x) m = fmaxf(m, x[i] * scale);
+    m = block_max(m, redf);
+    double sum = 0.0;
+    for (int i = threadIdx.x; i < L; i += blockDim.x) sum += (double)expf(x[i] * scale - m);
+    sum = block_sum(sum, redd);
+    const float inv = 1.0f / (float)sum;
+    for (int i = threadIdx.x; i < L; i += blockDim.x) y[i] = expf(x[i] * scale - m) * inv;
+}
+
+static int softmax_dispatch(float* out, int ld_out, const float* in, int ld_in, int n_rows,
+                            int n_cols, const int32_t* lens, int rows_per_len, float scale,
+                            hipStream_t stream) {
+    if (n_rows < 0 || n_cols < 0) return JINF_HIP_ERR_INVALID;
+    if (n_rows == 0 || n_cols == 0) return JINF_HIP_OK;
+    if (!out || !in || ld_out < n_cols || ld_in < n_cols) return JINF_HIP_ERR_INVALID;
+    if (lens && rows_per_len <= 0) return JINF_HIP_ERR_INVALID;
+    if (!(scale > 0.0f) || !isfinite(scale)) return JINF_HIP_ERR_INVALID;
+    const bool vec = aligned(out, 16) && aligned(in, 16) && ld_out % 4 == 0 && ld_in % 4 == 0;
+    const int nch = (n_cols + 3) / 4;
+    int bs = round_up((nch + kSmCPT - 1) / kSmCPT, kWave);
+    if (bs < 256 && n_cols > 256) bs = 256;
+    if (bs < kWave) bs = kWave;
+    if (vec && bs <= 1024)
+        return launch(softmax_vec_kernel, dim3(n_rows), dim3(bs), 0, stream, out, ld_out, in,
+                      ld_in, n_cols, lens, rows_per_len, scale);
+    const int lbs = n_cols >= 1024 ? 1024 : round_up(n_cols, kWave);
+    return launch(softmax_loop_kernel, dim3(n_rows), dim3(lbs), 0, stream, out, ld_out, in,
+                  ld_in, n_cols, lens, rows_per_len, scale);
+}
+
+}  // namespace jinf
+
+extern "C" int jinf_softmax_rows_f32(float* out, int ld_out, const float* in, int ld_in,
+                                     int n_rows, int n_cols, const int32_t* lens,
+                                     int rows_per_len, float scale, hipStream_t stream) {
+    return jinf::softmax_dispatch(out, ld_out, in, ld_in, n_rows, n_cols, lens, rows_per_len,
+                                  scale, stream);
+}
+
+// Drop-in for cuda/softmax_kernel.cu:46-51 (one fp32 row; output may alias input).
+extern "C" void jinf_cuda_softmax(float* output, const float* input, int n, hipStream_t stream) {
+    if (n <= 0) return;
+    if (jinf::softmax_dispatch(output, n, input, n, 1, n, nullptr, 1, 1.0f, stream) ==
+        JINF_HIP_ERR_INVALID)
+        JINF_LOG("jinf_cuda_softmax: invalid argument (n=%d)", n);
+}

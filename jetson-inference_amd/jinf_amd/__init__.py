@@ -1,0 +1,24 @@
+"""jinf_amd: MI355X (gfx950) kernels for jinf's per-layer elementwise and
+reduction path -- RMSNorm (+ fused residual add), interleaved GQA RoPE,
+SwiGLU, masked row softmax and the GGUF Q4_0 token-embedding gather.
+
+The kernels live in libjinf_hip.so behind the C-ABI of include/jinf/*.h;
+this package is a thin ctypes/torch front end used by tests and bench.py.
+"""
+from ._lib import F16, F32, LIB_PATH, lib, version  # noqa: F401
+from .ops import (  # noqa: F401
+    JinfError,
+    cuda_dequantize_q4_0,
+    cuda_residual_add,
+    cuda_rmsnorm,
+    cuda_rope,
+    cuda_silu_mul,
+    cuda_softmax,
+    embed_q4_0,
+    residual_add,
+    residual_rmsnorm_rows,
+    rmsnorm_rows,
+    rope_rows,
+    softmax_rows,
+    swiglu,
+)

@@ -1,0 +1,72 @@
+"""ctypes binding of libjinf_hip.so, the C-ABI declared in include/jinf/kernels.h
+and include/jinf/kernels_ext.h.
+
+The library links the HIP runtime by soname (libamdhip64.so.7).  PyTorch ships
+its own copy with the same soname, so torch is imported first: the dynamic
+loader then resolves the library's HIP dependency to the runtime torch already
+loaded, and device pointers and streams from torch are valid in both.
+
+There is no fallback: if the shared library is missing, `lib()` raises.
+"""
+import ctypes
+import os
+
+_PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_DIR, "libjinf_hip.so")
+
+JINF_HIP_OK = 0
+JINF_HIP_ERR_DEVICE = 3
+JINF_HIP_ERR_INVALID = 5
+
+F32 = 0
+F16 = 1
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> (restype, argtypes); the parameter lists of the C declarations.
+SIGNATURES = {
+    # drop-ins (include/jinf/kernels.h)
+    "jinf_cuda_rmsnorm": (None, [_P, _P, _P, _I, _F, _I, _P]),
+    "jinf_cuda_rope": (None, [_P, _P, _I, _I, _I, _I, _F, _P]),
+    "jinf_cuda_silu_mul": (None, [_P, _P, _P, _I, _P]),
+    "jinf_cuda_softmax": (None, [_P, _P, _I, _P]),
+    "jinf_cuda_residual_add": (None, [_P, _P, _I, _P]),
+    "jinf_cuda_dequantize_q4_0": (None, [_P, _P, _I, _P]),
+    # extensions (include/jinf/kernels_ext.h)
+    "jinf_hip_version": (ctypes.c_char_p, []),
+    "jinf_rmsnorm_rows": (_I, [_P, _I, _P, _I, _P, _I, _I, _F, _I, _I, _P]),
+    "jinf_residual_rmsnorm_rows": (_I, [_P, _I, _P, _I, _P, _I, _P, _I, _I, _F, _I, _I, _P]),
+    "jinf_rope_rows": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _F, _I, _P]),
+    "jinf_swiglu_rows": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P]),
+    "jinf_residual_add_rows": (_I, [_P, _I, _P, _I, _I, _I, _I, _P]),
+    "jinf_softmax_rows_f32": (_I, [_P, _I, _P, _I, _I, _I, _P, _I, _F, _P]),
+    "jinf_embed_q4_0": (_I, [_P, _I, _P, _I, _I, _P, _I, _I, _P]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libjinf_hip.so (after torch) and declare every entry point."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    import torch  # noqa: F401  (must precede the load; see module docstring)
+
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+            "or `make -C jetson-inference_amd`")
+    handle = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_LOCAL)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = handle
+    return _lib
+
+
+def version():
+    return lib().jinf_hip_version().decode()

@@ -1,0 +1,188 @@
+"""Torch-tensor front end over the jinf C-ABI (libjinf_hip.so).
+
+Tensors must live on the current HIP device; every call is enqueued on torch's
+current stream, and nothing synchronizes.  Shapes follow the reference engine:
+rows are tokens (or (sequence, head) pairs for softmax), the last dimension is
+contiguous, and the row stride is passed as the C-ABI `ld_*` argument.
+
+Each function raises JinfError when the library rejects its arguments; there
+is no CPU or PyTorch fallback.
+"""
+import ctypes
+
+import torch
+
+from ._lib import F16, F32, JINF_HIP_OK, lib
+
+
+class JinfError(RuntimeError):
+    pass
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _act(t):
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.float16:
+        return F16
+    raise JinfError(f"unsupported dtype {t.dtype}")
+
+
+def _rows(t):
+    """(n_rows, n, ld) of a tensor viewed as rows over its last dimension."""
+    if t.dim() == 1:
+        return 1, t.shape[0], t.shape[0]
+    if t.stride(-1) != 1:
+        raise JinfError("last dimension must be contiguous")
+    n = t.shape[-1]
+    lead = t.shape[:-1]
+    rows = 1
+    for s in lead:
+        rows *= s
+    # leading dims must collapse onto one row stride
+    ld = t.stride(-2)
+    expect = ld
+    for d in range(t.dim() - 2, -1, -1):
+        if t.shape[d] != 1 and t.stride(d) != expect:
+            raise JinfError("leading dimensions must form a single row stride")
+        expect *= t.shape[d]
+    return rows, n, ld
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _check(rc, name):
+    if rc != JINF_HIP_OK:
+        raise JinfError(f"{name} returned status {rc}")
+
+
+def rmsnorm_rows(x, weight, eps=1e-5, out=None):
+    """out[r] = rmsnorm(x[r]) * weight (x fp32 or fp16; weight fp32 or fp16)."""
+    out = torch.empty_like(x) if out is None else out
+    rows, n, ld_in = _rows(x)
+    _, _, ld_out = _rows(out)
+    _check(lib().jinf_rmsnorm_rows(_ptr(out), ld_out, _ptr(x), ld_in, _ptr(weight), rows, n,
+                                   float(eps), _act(x), _act(weight), _stream()),
+           "jinf_rmsnorm_rows")
+    return out
+
+
+def residual_rmsnorm_rows(residual, delta, weight, eps=1e-5, out=None):
+    """residual += delta (in place, rounded to its dtype); returns rmsnorm(residual)*w."""
+    out = torch.empty_like(residual) if out is None else out
+    rows, n, ld_res = _rows(residual)
+    _, _, ld_d = _rows(delta)
+    _, _, ld_out = _rows(out)
+    _check(lib().jinf_residual_rmsnorm_rows(_ptr(out), ld_out, _ptr(residual), ld_res,
+                                            _ptr(delta), ld_d, _ptr(weight), rows, n,
+                                            float(eps), _act(residual), _act(weight),
+                                            _stream()),
+           "jinf_residual_rmsnorm_rows")
+    return out
+
+
+def rope_rows(q, k, head_dim, positions=None, pos0=0, freq_base=10000.0):
+    """In-place interleaved RoPE.  q: [T, n_heads*head_dim] (or [T, n_heads,
+    head_dim]), k: [T, n_heads_kv*head_dim]; positions: int32 [T] or None."""
+    T = q.shape[0]
+    q2 = q.reshape(T, -1) if q.is_contiguous() else q
+    k2 = k.reshape(T, -1) if k.is_contiguous() else k
+    nh = q2.shape[1] // head_dim
+    nkv = k2.shape[1] // head_dim
+    if positions is not None and positions.dtype != torch.int32:
+        raise JinfError("positions must be int32")
+    _check(lib().jinf_rope_rows(_ptr(q2), q2.stride(0), _ptr(k2), k2.stride(0),
+                                _ptr(positions), int(pos0), T, head_dim, nh, nkv,
+                                float(freq_base), _act(q), _stream()),
+           "jinf_rope_rows")
+    return q, k
+
+
+def swiglu(gate, up, out=None):
+    """out = silu(gate) * up (out may be gate or up)."""
+    out = torch.empty_like(gate) if out is None else out
+    rows, n, ld_g = _rows(gate)
+    _, _, ld_u = _rows(up)
+    _, _, ld_o = _rows(out)
+    _check(lib().jinf_swiglu_rows(_ptr(out), ld_o, _ptr(gate), ld_g, _ptr(up), ld_u, rows, n,
+                                  _act(gate), _stream()),
+           "jinf_swiglu_rows")
+    return out
+
+
+def residual_add(a, b):
+    """a += b in place."""
+    rows, n, ld_a = _rows(a)
+    _, _, ld_b = _rows(b)
+    _check(lib().jinf_residual_add_rows(_ptr(a), ld_a, _ptr(b), ld_b, rows, n, _act(a),
+                                        _stream()),
+           "jinf_residual_add_rows")
+    return a
+
+
+def softmax_rows(x, lens=None, rows_per_len=1, scale=1.0, out=None):
+    """Masked fp32 row softmax; rows j >= len are left untouched in `out`."""
+    out = torch.empty_like(x) if out is None else out
+    rows, n, ld_in = _rows(x)
+    _, _, ld_out = _rows(out)
+    if lens is not None and lens.dtype != torch.int32:
+        raise JinfError("lens must be int32")
+    _check(lib().jinf_softmax_rows_f32(_ptr(out), ld_out, _ptr(x), ld_in, rows, n, _ptr(lens),
+                                       int(rows_per_len), float(scale), _stream()),
+           "jinf_softmax_rows_f32")
+    return out
+
+
+def embed_q4_0(table, ids, n_embd, out_dtype=torch.float16, out=None):
+    """Gather + dequantize rows of a Q4_0 table (uint8 [n_vocab, n_embd/32*18])."""
+    n_vocab = table.shape[0]
+    n_ids = ids.shape[0] if ids is not None else n_vocab
+    if out is None:
+        out = torch.empty((n_ids, n_embd), dtype=out_dtype, device=table.device)
+    if ids is not None and ids.dtype != torch.int32:
+        raise JinfError("ids must be int32")
+    _check(lib().jinf_embed_q4_0(_ptr(out), out.stride(0), _ptr(table), n_vocab, n_embd,
+                                 _ptr(ids), n_ids, _act(out), _stream()),
+           "jinf_embed_q4_0")
+    return out
+
+
+# ---- drop-in entry points (reference signatures; fp32, one row) ----
+
+def cuda_rmsnorm(out, x, weight, eps=1e-5):
+    wt = F16 if weight.dtype == torch.float16 else F32
+    lib().jinf_cuda_rmsnorm(_ptr(out), _ptr(x), _ptr(weight), x.numel(), float(eps), wt,
+                            _stream())
+    return out
+
+
+def cuda_rope(q, k, head_dim, n_heads, n_heads_kv, pos, freq_base):
+    lib().jinf_cuda_rope(_ptr(q), _ptr(k), head_dim, n_heads, n_heads_kv, int(pos),
+                         float(freq_base), _stream())
+    return q, k
+
+
+def cuda_silu_mul(out, gate, up):
+    lib().jinf_cuda_silu_mul(_ptr(out), _ptr(gate), _ptr(up), gate.numel(), _stream())
+    return out
+
+
+def cuda_softmax(out, x):
+    lib().jinf_cuda_softmax(_ptr(out), _ptr(x), x.numel(), _stream())
+    return out
+
+
+def cuda_residual_add(a, b):
+    lib().jinf_cuda_residual_add(_ptr(a), _ptr(b), a.numel(), _stream())
+    return a
+
+
+def cuda_dequantize_q4_0(data, out, n_blocks, byte_offset=0):
+    ptr = ctypes.c_void_p(data.data_ptr() + byte_offset)
+    lib().jinf_cuda_dequantize_q4_0(ptr, _ptr(out), int(n_blocks), _stream())
+    return out

@@ -1,0 +1,320 @@
+/*
+ * CPU oracle for the jinf per-layer elementwise / reduction kernels.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker the GPU kernels are
+ * compared against (tests/, __graft_entry__.smoke(), and the cpu_baseline leg
+ * of bench.py); the product path never calls it.
+ *
+ * It restates the reference's arithmetic for each kernel in plain C, with the
+ * rounding points of the reference source and transcendentals evaluated in
+ * fp64 (glibc) and rounded once to fp32 where the reference rounds:
+ *   fp16 <-> fp32          cuda/cuda_utils.cuh:10-14, src/quant.cpp:7-45
+ *   Q4_0 dequant / gather  src/quant.cpp:49-60, cuda/dequant_kernels.cu:6-21,
+ *                          src/engine.cpp:170-178, 311-317
+ *   RMSNorm                cuda/rmsnorm_kernel.cu:9-61
+ *   residual add           cuda/matmul_kernels.cu:189-194
+ *   residual -> RMSNorm    src/engine.cpp:466->487, 508->429
+ *   RoPE                   cuda/rope_kernel.cu:8-50
+ *   SiLU * up              cuda/silu_kernel.cu:6-18
+ *   softmax                cuda/softmax_kernel.cu:8-42, cuda/attention_kernel.cu:59-87
+ * Build with -ffp-contract=off (no FMA contraction) and without fast-math.
+ *
+ * fp16 storage: every stored value is fl16(fl32(expression)) with
+ * round-to-nearest-even and subnormals kept.
+ *
+ * Rows are split over OpenMP threads only for the CPU baseline timing; each
+ * row's arithmetic is sequential and identical for any thread count.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define JO_F32 0
+#define JO_F16 1
+
+static int jo_threads = 1;
+
+void jo_set_threads(int n) { jo_threads = n < 1 ? 1 : n; }
+int jo_get_threads(void) { return jo_threads; }
+
+/* ---- binary16 <-> binary32 (IEEE 754 definitions) ---- */
+
+/* Exact widening; same results as src/quant.cpp:7-45. */
+float jo_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1Fu;
+    const uint32_t m = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0) {
+        const float v = ldexpf((float)m, -24); /* m * 2^-24, exact */
+        return sign ? -v : v;
+    }
+    if (e == 31)
+        bits = sign | 0x7F800000u | (m << 13);
+    else
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* Round-to-nearest-even narrowing, subnormals kept, overflow to Inf,
+ * NaN stays NaN (quiet, top payload bits kept). */
+uint16_t jo_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((ax >> 13) & 0x3FFu));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u); /* >= 65520 */
+    if (ax >= 0x38800000u) {                                 /* >= 2^-14: normal */
+        const uint32_t m = ax - 0x38000000u;                 /* rebias 127 -> 15 */
+        return (uint16_t)(sign | ((m + 0x0FFFu + ((m >> 13) & 1u)) >> 13));
+    }
+    const uint32_t e = ax >> 23;
+    if (e < 102) return sign; /* below 2^-25: rounds to zero */
+    const uint32_t mant = (ax & 0x7FFFFFu) | 0x800000u;
+    const uint32_t shift = 126u - e; /* units of 2^-24 */
+    uint32_t q = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+}
+
+void jo_f16_to_f32_n(const uint16_t* in, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = jo_f16_to_f32(in[i]);
+}
+
+void jo_f32_to_f16_n(const float* in, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = jo_f32_to_f16(in[i]);
+}
+
+static inline float ld_act(const void* p, int type, int64_t i) {
+    return type == JO_F16 ? jo_f16_to_f32(((const uint16_t*)p)[i]) : ((const float*)p)[i];
+}
+
+static inline void st_act(void* p, int type, int64_t i, float v) {
+    if (type == JO_F16)
+        ((uint16_t*)p)[i] = jo_f32_to_f16(v);
+    else
+        ((float*)p)[i] = v;
+}
+
+static inline float round_act(int type, float v) {
+    return type == JO_F16 ? jo_f16_to_f32(jo_f32_to_f16(v)) : v;
+}
+
+/* ---- Q4_0 (src/quant.cpp:49-60; block layout include/jinf/quant.h:30-36) ---- */
+
+static void q4_0_block(const uint8_t* blk, int type, void* out, int64_t o) {
+    const uint16_t dbits = (uint16_t)(blk[0] | (blk[1] << 8)); /* little-endian */
+    const float d = jo_f16_to_f32(dbits);
+    for (int j = 0; j < 16; ++j) {
+        const uint8_t b = blk[2 + j];
+        const int v0 = (int)(b & 0x0F) - 8;
+        const int v1 = (int)(b >> 4) - 8;
+        st_act(out, type, o + 2 * j, (float)v0 * d);
+        st_act(out, type, o + 2 * j + 1, (float)v1 * d);
+    }
+}
+
+/* Contiguous blocks to fp32: the reference CPU path jinf_dequantize_q4_0. */
+void jo_dequant_q4_0(const uint8_t* blocks, float* out, int n_blocks) {
+    for (int b = 0; b < n_blocks; ++b) q4_0_block(blocks + 18 * (int64_t)b, JO_F32, out, 32 * (int64_t)b);
+}
+
+/* Token-embedding gather (src/engine.cpp:311-317): row ids[i] of a table of
+ * n_vocab rows of n_embd/32 blocks.  ids == NULL means row i.  Out-of-range ids
+ * give a +0.0 row (the GPU contract; the reference does not check). */
+void jo_embed_q4_0(void* out, int out_type, int64_t ld_out, const uint8_t* table, int n_vocab,
+                   int n_embd, const int32_t* ids, int n_ids) {
+    const int nb = n_embd / 32;
+    const int64_t row_bytes = (int64_t)nb * 18;
+#pragma omp parallel for num_threads(jo_threads) schedule(static)
+    for (int i = 0; i < n_ids; ++i) {
+        const int id = ids ? ids[i] : i;
+        const int64_t o = (int64_t)i * ld_out;
+        if (id < 0 || id >= n_vocab) {
+            for (int e = 0; e < n_embd; ++e) st_act(out, out_type, o + e, 0.0f);
+            continue;
+        }
+        const uint8_t* row = table + (int64_t)id * row_bytes;
+        for (int b = 0; b < nb; ++b) q4_0_block(row + 18 * (int64_t)b, out_type, out, o + 32 * (int64_t)b);
+    }
+}
+
+/* ---- RMSNorm (cuda/rmsnorm_kernel.cu:9-61) ---- */
+
+/* rs = 1/sqrt(fl32(fl32(ss)/n) + eps), sqrt and divide in fp64, rounded once. */
+static float rms_scale(double ss, int n, float eps) {
+    const float m = (float)ss / (float)n;
+    const float t = m + eps;
+    return (float)(1.0 / sqrt((double)t));
+}
+
+static void norm_row(void* out, int64_t oo, const float* h, const void* w, int wt, int n,
+                     float eps, int act) {
+    double ss = 0.0;
+    for (int i = 0; i < n; ++i) ss += (double)h[i] * (double)h[i];
+    const float rs = rms_scale(ss, n, eps);
+    for (int i = 0; i < n; ++i) st_act(out, act, oo + i, (h[i] * rs) * ld_act(w, wt, i));
+}
+
+/* out[r] = rmsnorm(in[r]) * w.  Sum of squares sequential in fp64. */
+void jo_rmsnorm_rows(void* out, int64_t ld_out, const void* in, int64_t ld_in, const void* w,
+                     int n_rows, int n, float eps, int act, int wt) {
+#pragma omp parallel num_threads(jo_threads)
+    {
+        float hbuf[65536];
+#pragma omp for schedule(static)
+        for (int r = 0; r < n_rows; ++r) {
+            for (int i = 0; i < n; ++i) hbuf[i] = ld_act(in, act, (int64_t)r * ld_in + i);
+            norm_row(out, (int64_t)r * ld_out, hbuf, w, wt, n, eps, act);
+        }
+    }
+}
+
+/* residual[r] = round(residual[r] + delta[r]) (stored); out[r] = rmsnorm(residual[r]) * w. */
+void jo_residual_rmsnorm_rows(void* out, int64_t ld_out, void* res, int64_t ld_res,
+                              const void* delta, int64_t ld_delta, const void* w, int n_rows,
+                              int n, float eps, int act, int wt) {
+#pragma omp parallel num_threads(jo_threads)
+    {
+        float hbuf[65536];
+#pragma omp for schedule(static)
+        for (int r = 0; r < n_rows; ++r) {
+            for (int i = 0; i < n; ++i) {
+                const float v = ld_act(res, act, (int64_t)r * ld_res + i) +
+                                ld_act(delta, act, (int64_t)r * ld_delta + i);
+                st_act(res, act, (int64_t)r * ld_res + i, v);
+                hbuf[i] = round_act(act, v);
+            }
+            norm_row(out, (int64_t)r * ld_out, hbuf, w, wt, n, eps, act);
+        }
+    }
+}
+
+/* The reference kernel's own fp32 summation order for one row: per-thread
+ * strided partials over T = min(n,1024) rounded up to 32 threads, each
+ * accumulated as fma(v, v, acc) (nvcc contracts sum += v*v), then the 32-lane
+ * shfl_down tree per warp and the same tree over the warp partials
+ * (cuda/cuda_utils.cuh:18-49, cuda/rmsnorm_kernel.cu:16-22,67-69).
+ * Returns the fp32 sum of squares; used to bound how far the reference's
+ * rounding of ss can sit from the fp64 sum used above. */
+float jo_ref_order_sumsq(const float* x, int n) {
+    int T = n < 1024 ? n : 1024;
+    T = (T + 31) / 32 * 32;
+    if (T > 1024) T = 1024;
+    float part[1024];
+    for (int t = 0; t < T; ++t) {
+        float acc = 0.0f;
+        for (int i = t; i < n; i += T) acc = fmaf(x[i], x[i], acc);
+        part[t] = acc;
+    }
+    const int nw = (T + 31) / 32;
+    float warp[32];
+    for (int w = 0; w < nw; ++w) {
+        float v[32];
+        for (int l = 0; l < 32; ++l) v[l] = part[32 * w + l];
+        for (int off = 16; off > 0; off >>= 1)
+            for (int l = 0; l < 32; ++l) v[l] = v[l] + (l + off < 32 ? v[l + off] : 0.0f);
+        warp[w] = v[0];
+    }
+    float v[32];
+    for (int l = 0; l < 32; ++l) v[l] = l < nw ? warp[l] : 0.0f;
+    for (int off = 16; off > 0; off >>= 1)
+        for (int l = 0; l < 32; ++l) v[l] = v[l] + (l + off < 32 ? v[l + off] : 0.0f);
+    return v[0];
+}
+
+/* ---- residual add (cuda/matmul_kernels.cu:189-194) ---- */
+
+void jo_residual_add(void* a, const void* b, int64_t n, int act) {
+#pragma omp parallel for num_threads(jo_threads) schedule(static)
+    for (int64_t i = 0; i < n; ++i) st_act(a, act, i, ld_act(a, act, i) + ld_act(b, act, i));
+}
+
+/* ---- RoPE (cuda/rope_kernel.cu:8-50) ---- */
+
+/* theta_i = fl32(base^e), e = fl32(fl32(-2*i)/hd) as the reference forms it. */
+float jo_rope_theta(float base, int i, int head_dim) {
+    volatile float e = -2.0f * (float)i;
+    e = e / (float)head_dim;
+    return (float)pow((double)base, (double)e);
+}
+
+static void rope_head(void* p, int act, int64_t o, int head_dim, const float* c, const float* s) {
+    for (int i = 0; i < head_dim / 2; ++i) {
+        const float x0 = ld_act(p, act, o + 2 * i);
+        const float x1 = ld_act(p, act, o + 2 * i + 1);
+        st_act(p, act, o + 2 * i, x0 * c[i] - x1 * s[i]);
+        st_act(p, act, o + 2 * i + 1, x0 * s[i] + x1 * c[i]);
+    }
+}
+
+/* In place over n_tokens tokens; token t uses positions[t] (or pos0 + t). */
+void jo_rope_rows(void* q, int64_t ld_q, void* k, int64_t ld_k, const int32_t* positions,
+                  int pos0, int n_tokens, int head_dim, int n_heads, int n_heads_kv, float base,
+                  int act) {
+    float theta[4096];
+    for (int i = 0; i < head_dim / 2; ++i) theta[i] = jo_rope_theta(base, i, head_dim);
+#pragma omp parallel num_threads(jo_threads)
+    {
+        float c[4096], s[4096];
+#pragma omp for schedule(static)
+        for (int t = 0; t < n_tokens; ++t) {
+            const int pos = positions ? positions[t] : pos0 + t;
+            for (int i = 0; i < head_dim / 2; ++i) {
+                const float a = (float)pos * theta[i];
+                c[i] = (float)cos((double)a);
+                s[i] = (float)sin((double)a);
+            }
+            for (int h = 0; h < n_heads; ++h)
+                rope_head(q, act, (int64_t)t * ld_q + (int64_t)h * head_dim, head_dim, c, s);
+            for (int h = 0; h < n_heads_kv; ++h)
+                rope_head(k, act, (int64_t)t * ld_k + (int64_t)h * head_dim, head_dim, c, s);
+        }
+    }
+}
+
+/* ---- SiLU(gate) * up (cuda/silu_kernel.cu:6-18) ---- */
+
+void jo_swiglu(void* out, const void* gate, const void* up, int64_t n, int act) {
+#pragma omp parallel for num_threads(jo_threads) schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        const float g = ld_act(gate, act, i);
+        const float e = (float)exp(-(double)g);
+        const float silu = g / (1.0f + e);
+        st_act(out, act, i, silu * ld_act(up, act, i));
+    }
+}
+
+/* ---- softmax (cuda/softmax_kernel.cu:8-42, cuda/attention_kernel.cu:59-87) ---- */
+
+/* Row r has live length L = lens ? clamp(lens[r / rows_per_len], 0, n_cols)
+ * : n_cols.  s = scale * x; y_j = fl32(exp(s_j - m)) * fl32(1 / sum), with the
+ * sum of the rounded exponentials accumulated in fp64.  j >= L untouched. */
+void jo_softmax_rows(float* out, int64_t ld_out, const float* in, int64_t ld_in, int n_rows,
+                     int n_cols, const int32_t* lens, int rows_per_len, float scale) {
+#pragma omp parallel for num_threads(jo_threads) schedule(dynamic, 16)
+    for (int r = 0; r < n_rows; ++r) {
+        int L = n_cols;
+        if (lens) {
+            L = lens[r / rows_per_len];
+            L = L < 0 ? 0 : (L > n_cols ? n_cols : L);
+        }
+        if (L == 0) continue;
+        const float* x = in + (int64_t)r * ld_in;
+        float* y = out + (int64_t)r * ld_out;
+        float m = -INFINITY;
+        for (int j = 0; j < L; ++j) m = fmaxf(m, x[j] * scale);
+        double sum = 0.0;
+        for (int j = 0; j < L; ++j) sum += (double)(float)exp((double)(x[j] * scale - m));
+        const float inv = 1.0f / (float)sum;
+        for (int j = 0; j < L; ++j) y[j] = (float)exp((double)(x[j] * scale - m)) * inv;
+    }
+}

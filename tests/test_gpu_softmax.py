@@ -1,0 +1,91 @@
+"""GPU parity: masked fp32 row softmax (attention-score rows) and the
+single-row drop-in.
+
+Bar: within 1e-5 relative of the oracle (floor 1e-30 for values that underflow
+towards fp32 subnormals), masked tails never written (poisoned with NaN), rows
+sum to 1 at the full config-5 size.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import jinf_amd
+import oracle
+import testutil as tu
+from gpu_util import dev as to_dev
+from gpu_util import host, say
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def test_config5_ragged_rows(dev):
+    say("config 5: 64 seqs x 64 heads, stride 8192, len = pos + 1, logits ~ N(0, 3)")
+    r = tu.rng(5)
+    pos = r.integers(0, 8192, size=64)
+    lens = (pos + 1).astype(np.int32)
+    x = tu.normal(r, (4096, 8192), 0.0, 3.0, np.float32)
+    oracle.set_threads(8)
+    ref = oracle.softmax_rows(x, lens, 64, 1.0, out=np.full_like(x, np.nan))
+    oracle.set_threads(1)
+    xd = to_dev(x)
+    out = torch.full_like(xd, float("nan"))
+    jinf_amd.softmax_rows(xd, to_dev(lens), 64, 1.0, out=out)
+    got = host(out)
+    live = ~np.isnan(ref)
+    assert np.array_equal(np.isnan(got), ~live)  # tails untouched
+    tu.assert_f32_close(got[live], ref[live], 1e-5, 1e-30, "config 5")
+    sums = np.nansum(got.astype(np.float64), axis=1)
+    assert np.max(np.abs(sums - 1.0)) < 1e-5
+    assert tu.bits_equal(host(xd), x)  # input untouched
+
+
+def test_fixture(dev):
+    g = np.load(os.path.join(HERE, "golden", "kernels.npz"))
+    xd = to_dev(g["sm_x"])
+    out = torch.full_like(xd, float("nan"))
+    jinf_amd.softmax_rows(xd, to_dev(g["sm_lens"]), 4, 1.0, out=out)
+    got, ref = host(out), g["sm_y"]
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    live = ~np.isnan(ref)
+    tu.assert_f32_close(got[live], ref[live], 1e-5, 1e-30, "fixture")
+
+
+@pytest.mark.parametrize("n", [1, 3, 100, 1024, 8192, 32768, 40000, 100003])
+def test_drop_in_single_row(dev, n):
+    say(f"drop-in jinf_cuda_softmax n={n} (in place)")
+    r = tu.rng(n)
+    x = tu.normal(r, (1, n), 0.0, 3.0, np.float32)
+    ref = oracle.softmax_rows(x)
+    xd = to_dev(x[0])
+    jinf_amd.cuda_softmax(xd, xd)
+    tu.assert_f32_close(host(xd), ref[0], 1e-5, 1e-30, f"n={n}")
+
+
+def test_scale_lengths_and_unaligned_rows(dev):
+    say("scale 1/sqrt(128), per-row lens incl. 0 and > n, row stride 1001")
+    r = tu.rng(77)
+    x = tu.normal(r, (40, 1001), 0.0, 3.0, np.float32)
+    lens = r.integers(-3, 1100, size=40).astype(np.int32)
+    scale = float(np.float32(1.0 / np.sqrt(128.0)))
+    ref = oracle.softmax_rows(x, lens, 1, scale, out=np.full_like(x, np.nan))
+    xd = to_dev(x)
+    out = torch.full_like(xd, float("nan"))
+    jinf_amd.softmax_rows(xd, to_dev(lens), 1, scale, out=out)
+    got = host(out)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    live = ~np.isnan(ref)
+    tu.assert_f32_close(got[live], ref[live], 1e-5, 1e-30, "scaled")
+
+
+def test_all_masked_rows_noop_and_length_one(dev):
+    x = np.random.default_rng(3).normal(0, 3, size=(4, 64)).astype(np.float32)
+    lens = np.array([0, 1, 1, 0], np.int32)
+    xd = to_dev(x)
+    out = torch.full_like(xd, 7.0)
+    jinf_amd.softmax_rows(xd, to_dev(lens), 1, 1.0, out=out)
+    got = host(out)
+    assert np.all(got[0] == 7.0) and np.all(got[3] == 7.0)
+    assert got[1, 0] == 1.0 and got[2, 0] == 1.0 and np.all(got[1:3, 1:] == 7.0)
