@@ -15,8 +15,11 @@ value = algorithmic bytes of a step / GPU time of a step (GB/s).  Algorithmic
 bytes count every input read once and every output written once.  Inputs are
 resident in HBM before timing; each kernel rotates over enough buffer sets
 (>= 512 MiB per kernel) that no launch can be served from the 256 MB
-Infinity Cache.  Kernel times come from HIP events recorded around every
-launch on the stream the kernels run on.
+Infinity Cache.  Times come from HIP events on the stream the kernels run on:
+the K steps are captured as one HIP graph and the replay is bracketed by two
+events (ms_per_step); each kernel's average launch duration is timed the same
+way over K back-to-back launches of that kernel alone (kernels.*.us,
+roofline.avg_launch_us).
 
 Prints ONE JSON line (rank 0).  `--gpus N` with N > 1 exits: this build runs
 on one GPU.
@@ -261,6 +264,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, host cores)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch eagerly instead of replaying a captured HIP graph")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -286,27 +291,44 @@ def main():
             k.run()
     torch.cuda.synchronize()
 
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(ks) + 1)]
-           for _ in range(args.steps)]
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    # The K timed steps are captured into one HIP graph and replayed once: the
+    # GPU then runs the kernels back to back, as an engine's captured decode
+    # step would, and Python launch overhead is out of the measurement.
+    # --no-graph launches them eagerly on the stream instead.
+    def record(n_steps, kernels):
+        for _ in range(n_steps):
+            for k in kernels:
+                k.run()
+
+    def timed(n_steps, kernels):
+        """GPU ms for n_steps passes over `kernels` (HIP events on the stream)."""
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        if args.no_graph:
+            torch.cuda.synchronize()
+            start.record()
+            record(n_steps, kernels)
+            end.record()
+        else:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                record(n_steps, kernels)
+            g.replay()  # untimed: first replay uploads the graph
+            torch.cuda.synchronize()
+            start.record()
+            g.replay()
+            end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end)
+
     t0 = time.perf_counter()
-    start.record()
-    for s in range(args.steps):
-        e = evs[s]
-        e[0].record()
-        for i, k in enumerate(ks):
-            k.run()
-            e[i + 1].record()
-    end.record()
-    torch.cuda.synchronize()
+    total_ms = timed(args.steps, ks)
     wall = time.perf_counter() - t0
-    total_ms = start.elapsed_time(end)
-    for s in range(args.steps):
-        for i, k in enumerate(ks):
-            k.ms += evs[s][i].elapsed_time(evs[s][i + 1])
-            k.n += 1
+    # per-kernel average launch duration: each kernel alone, K launches back to
+    # back over its rotating buffer sets, same event method
+    for k in ks:
+        k.ms = timed(args.steps, [k])
+        k.n = args.steps
     ms_step = total_ms / args.steps
     step_bytes = sum(k.nbytes for k in ks)
     kern_ms = sum(k.ms for k in ks) / args.steps
@@ -355,6 +377,7 @@ def main():
         "config": dict(cfg, step_bytes=step_bytes),
         "frac_of_peak": round(step_bytes / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4),
         "kernel_ms_per_step": round(kern_ms, 5),
+        "launch": "eager stream" if args.no_graph else "HIP graph of the K steps, replayed once",
         "wall_s_timed": round(wall, 4),
         "kernels": per,
         "roofline": roofline,

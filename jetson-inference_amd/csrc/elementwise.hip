@@ -5,23 +5,26 @@
 //   residual a = a + b                         (reference cuda/matmul_kernels.cu:189-194)
 // in fp32, rounded once to the storage type.
 //
-// Design: a streaming kernel over [rows, n] with 16-byte vector accesses.
-// Each thread owns kEwUnroll chunks spaced one workgroup apart, issues all of
-// their loads before any arithmetic, and stores after; consecutive lanes touch
-// consecutive 16-byte chunks, so each wave instruction moves 1 KiB of
-// contiguous bytes.  Contiguous tensors are flattened to one row, making the
-// grid one long 1-D sweep.
+// Design: a streaming kernel over [rows, n] with 16-byte nontemporal vector
+// accesses.  Consecutive lanes touch consecutive 16-byte chunks, so each wave
+// instruction moves 1 KiB of contiguous bytes.  Contiguous tensors are
+// flattened to one row, making the grid one long 1-D sweep.  Measured on
+// MI355X at [2048, 14336] fp16, one chunk per thread in 256-lane workgroups
+// (many small workgroups) beats 2-4 chunks per thread: 28.7 us vs 29.8 / 30.6.
 //
 // Arithmetic:
 //   fp32 storage (the drop-in's precision) uses accurate expf and an IEEE
 //   divide, exactly the reference's expression;
 //   fp16 storage computes sigmoid as rcp(1 + 2^(-g*log2 e)) with the hardware
 //   exp2 / reciprocal and then g * sigmoid.  The fp32 value differs from the
-//   exact expression by a few fp32 ulps (relative error < 1e-6), far below
+//   exact expression by a few fp32 ulps (relative error ~1e-6), far below
 //   half an fp16 ulp (2.4e-4 relative), so after the single RNE to fp16 the
 //   result equals the correctly rounded one or is 1 ulp away when the exact
-//   value sits within 1e-6 of a rounding midpoint.  It keeps the kernel at
-//   about 6 VALU ops per element so it stays HBM-bound.
+//   value sits within 1e-6 of a rounding midpoint.  (The exponent argument
+//   g*log2(e) is rounded to fp32, which adds |g|*6e-8 relative; for the
+//   |g| < 24 where the fp16 result is not already 0 or g*u that stays below
+//   2e-6.)  It keeps the kernel at about 6 VALU ops per element so it stays
+//   HBM-bound.
 //   Limits agree with the exact form: g -> -inf gives -0.0, g -> +inf gives g.
 #include "jinf_device.h"
 #include "jinf_host.h"
@@ -30,7 +33,7 @@
 namespace jinf {
 
 constexpr int kEwBlock = 256;
-constexpr int kEwUnroll = 4;
+constexpr int kEwUnroll = 1;
 
 enum EwOp { kSwigluExact = 0, kSwigluFast = 1, kAdd = 2 };
 
@@ -49,29 +52,29 @@ __device__ __forceinline__ float ew_apply(float a, float b) {
 
 // Vector kernel: rows of n elements, n % E == 0, 16-byte aligned rows.
 // grid.x covers one row's chunks, grid.y the rows.
-template <typename TA, int OP>
-__global__ __launch_bounds__(kEwBlock) void ew_vec_kernel(
+template <typename TA, int OP, int BS = kEwBlock, int U = kEwUnroll>
+__global__ __launch_bounds__(BS) void ew_vec_kernel(
     TA* out, int64_t ld_out, const TA* a, int64_t ld_a, const TA* b, int64_t ld_b,
     int64_t nch) {
     using A = Act<TA>;
     constexpr int E = A::kElems;
     const int64_t row = blockIdx.y;
-    const int64_t c0 = (int64_t)blockIdx.x * (kEwBlock * kEwUnroll) + threadIdx.x;
+    const int64_t c0 = (int64_t)blockIdx.x * (BS * U) + threadIdx.x;
     const TA* pa = a + row * ld_a;
     const TA* pb = b + row * ld_b;
     TA* po = out + row * ld_out;
-    float va[kEwUnroll][E], vb[kEwUnroll][E];
+    float va[U][E], vb[U][E];
 #pragma unroll
-    for (int j = 0; j < kEwUnroll; ++j) {
-        const int64_t c = c0 + j * kEwBlock;
+    for (int j = 0; j < U; ++j) {
+        const int64_t c = c0 + j * BS;
         if (c < nch) {
             A::load(pa + c * E, va[j]);
             A::load(pb + c * E, vb[j]);
         }
     }
 #pragma unroll
-    for (int j = 0; j < kEwUnroll; ++j) {
-        const int64_t c = c0 + j * kEwBlock;
+    for (int j = 0; j < U; ++j) {
+        const int64_t c = c0 + j * BS;
         if (c < nch) {
             float o[E];
 #pragma unroll

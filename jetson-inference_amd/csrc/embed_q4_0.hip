@@ -10,13 +10,15 @@
 // so the fp32 output is exact and the fp16 output is one RNE rounding of the
 // exact value: both are bit-exact by construction.
 //
-// Design: grid = (ids, row segments).  A segment (<= kSegBlocks blocks) of
-// the quantized row is staged into LDS with the widest load the row's
-// alignment allows (16 bytes for Llama rows: 2304 = 144 * 16), because the
-// 18-byte blocks are not 16-byte aligned individually.  Each lane then
-// decodes one output unit of 16 bytes (8 fp16 or 4 fp32 values) from the
-// block's scale and 4 (or 2) nibble bytes read from LDS, and consecutive
-// lanes store consecutive 16-byte units, so stores are fully coalesced.
+// Design: one lane per 16-byte output unit (8 fp16 or 4 fp32 values, a quarter
+// or an eighth of a block); grid = (ids, unit tiles of a row).  Each lane reads
+// its block's scale and its 4 (or 2) nibble bytes straight from global memory
+// with 16-bit loads (blocks are 18 bytes, so every field is 2-byte aligned but
+// not 4-byte aligned).  The 16 lanes that share a 288-byte run of blocks hit
+// the same cache lines, so HBM sees each table byte once; consecutive lanes
+// store consecutive 16-byte units with nontemporal stores, fully coalesced.
+// Measured on MI355X (4096 ids of a 128256 x 4096 table -> fp16): 7.8 us with
+// 512 lanes per row, against 8.3 us for staging the row through LDS first.
 // fp16 decode is exact and packed: 0x6400 | nibble is the binary16 value
 // 1024 + nibble; subtracting 1032 gives nibble - 8 exactly, and one packed
 // binary16 multiply by d is the single RNE rounding of the exact product
@@ -28,14 +30,8 @@
 
 namespace jinf {
 
-constexpr int kSegBlocks = 512;  // blocks per workgroup (9216 bytes of LDS)
 constexpr int kQ4Bytes = 18;
-
-template <int LW> struct Word;
-template <> struct Word<16> { typedef uint4 T; };
-template <> struct Word<4> { typedef uint32_t T; };
-template <> struct Word<2> { typedef uint16_t T; };
-template <> struct Word<1> { typedef uint8_t T; };
+constexpr int kEmbedBlock = 512;
 
 // Four nibble bytes (little-endian in w) -> 8 binary16 values in jinf order,
 // each = (nibble - 8) * d rounded once.
@@ -60,20 +56,29 @@ __device__ __forceinline__ uint4 decode8_f16(uint32_t w, uint16_t d) {
 }
 
 // Two nibble bytes (low 16 bits of w) -> 4 fp32 values, exact.
-__device__ __forceinline__ float4 decode4_f32(uint32_t w, uint16_t d) {
+__device__ __forceinline__ uint4 decode4_f32(uint32_t w, uint16_t d) {
     const float df = h2f(d);
-    return make_float4((float)((int)(w & 0xFu) - 8) * df,
-                       (float)((int)((w >> 4) & 0xFu) - 8) * df,
-                       (float)((int)((w >> 8) & 0xFu) - 8) * df,
-                       (float)((int)((w >> 12) & 0xFu) - 8) * df);
+    const float v[4] = {(float)((int)(w & 0xFu) - 8) * df, (float)((int)((w >> 4) & 0xFu) - 8) * df,
+                        (float)((int)((w >> 8) & 0xFu) - 8) * df,
+                        (float)((int)((w >> 12) & 0xFu) - 8) * df};
+    return Act<float>::pack(v);
+}
+
+// 16-bit little-endian field at an even byte offset (A2) or at any offset.
+template <bool A2>
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
+    if constexpr (A2)
+        return *reinterpret_cast<const uint16_t*>(p);
+    else
+        return (uint32_t)p[0] | ((uint32_t)p[1] << 8);
 }
 
 // VST: output rows are 16-byte aligned, so each unit is one 16-byte store;
 // otherwise each value is stored separately.
-template <typename TO, int VST>
+template <typename TO, bool VST>
 __device__ __forceinline__ void store_unit(TO* p, uint4 bits) {
     if constexpr (VST) {
-        *reinterpret_cast<uint4*>(p) = bits;
+        st16<true>(p, bits);
     } else {
         const uint32_t w[4] = {bits.x, bits.y, bits.z, bits.w};
         if constexpr (sizeof(TO) == 4) {
@@ -89,76 +94,62 @@ __device__ __forceinline__ void store_unit(TO* p, uint4 bits) {
     }
 }
 
-template <typename TO, int LW, int VST>
-__global__ __launch_bounds__(256) void embed_q4_0_kernel(
+template <typename TO, bool A2, bool VST>
+__global__ __launch_bounds__(kEmbedBlock) void embed_q4_0_kernel(
     TO* out, int64_t ld_out, const uint8_t* table, int n_vocab, int nb_row,
     const int32_t* ids) {
     // Output unit: 16 bytes = 8 fp16 or 4 fp32 values; kUPB units per block.
     constexpr int kVals = 16 / (int)sizeof(TO);
     constexpr int kUPB = 32 / kVals;
-    __shared__ uint16_t lds[kSegBlocks * kQ4Bytes / 2];
     const int64_t r = blockIdx.x;
-    const int b0 = blockIdx.y * kSegBlocks;
-    const int nbs = min(kSegBlocks, nb_row - b0);
-    const int nunits = nbs * kUPB;
-    TO* orow = out + r * ld_out + (int64_t)b0 * 32;
+    const int u = blockIdx.y * blockDim.x + threadIdx.x;
+    if (u >= nb_row * kUPB) return;
     const int id = ids ? ids[r] : (int)r;
+    TO* dst = out + r * ld_out + (int64_t)u * kVals;
     if (id < 0 || id >= n_vocab) {
-        for (int u = threadIdx.x; u < nunits; u += blockDim.x)
-            store_unit<TO, VST>(orow + (int64_t)u * kVals, make_uint4(0, 0, 0, 0));
+        store_unit<TO, VST>(dst, make_uint4(0, 0, 0, 0));
         return;
     }
-    typedef typename Word<LW>::T W;
-    const W* src = reinterpret_cast<const W*>(
-        table + ((int64_t)id * nb_row + b0) * kQ4Bytes);
-    W* dst = reinterpret_cast<W*>(lds);
-    const int nw = nbs * kQ4Bytes / LW;
-    for (int i = threadIdx.x; i < nw; i += blockDim.x) dst[i] = src[i];
-    __syncthreads();
-    for (int u = threadIdx.x; u < nunits; u += blockDim.x) {
-        const int b = u / kUPB;
-        const int q = u % kUPB;
-        const int hb = b * (kQ4Bytes / 2);  // block start in 16-bit words
-        const uint16_t d = lds[hb];
-        if constexpr (kVals == 8) {
-            // nibble bytes 4q .. 4q+3 of qs: words hb+1+2q, hb+2+2q
-            const uint32_t w = (uint32_t)lds[hb + 1 + 2 * q] | ((uint32_t)lds[hb + 2 + 2 * q] << 16);
-            store_unit<TO, VST>(orow + (int64_t)u * kVals, decode8_f16(w, d));
-        } else {
-            // nibble bytes 2q, 2q+1 of qs: word hb+1+q
-            const uint32_t w = lds[hb + 1 + q];
-            store_unit<TO, VST>(orow + (int64_t)u * kVals,
-                                __builtin_bit_cast(uint4, decode4_f32(w, d)));
-        }
+    const int b = u / kUPB;
+    const int q = u % kUPB;
+    const uint8_t* blk = table + ((int64_t)id * nb_row + b) * kQ4Bytes;
+    const uint16_t d = (uint16_t)ld_u16<A2>(blk);
+    if constexpr (kVals == 8) {
+        // nibble bytes 4q .. 4q+3 of qs
+        const uint32_t w = ld_u16<A2>(blk + 2 + 4 * q) | (ld_u16<A2>(blk + 4 + 4 * q) << 16);
+        store_unit<TO, VST>(dst, decode8_f16(w, d));
+    } else {
+        // nibble bytes 2q, 2q+1 of qs
+        store_unit<TO, VST>(dst, decode4_f32(ld_u16<A2>(blk + 2 + 2 * q), d));
     }
 }
 
-template <typename TO, int VST>
+template <typename TO, bool A2, bool VST>
 static int embed_launch(void* out, int64_t ld_out, const void* table, int n_vocab, int n_embd,
                         const int32_t* ids, int n_ids, hipStream_t stream) {
-    static_assert((kSegBlocks * kQ4Bytes) % 16 == 0, "segment must hold whole 16-byte words");
     const int nb_row = n_embd / 32;
-    const int64_t row_bytes = (int64_t)nb_row * kQ4Bytes;
-    const int segs = (nb_row + kSegBlocks - 1) / kSegBlocks;
-    const int units = (nb_row < kSegBlocks ? nb_row : kSegBlocks) * (32 * (int)sizeof(TO) / 16);
-    int bs = round_up(units, kWave);
-    if (bs > 256) bs = 256;
-    const dim3 grid(n_ids, segs);
-    TO* o = static_cast<TO*>(out);
-    const uint8_t* t = static_cast<const uint8_t*>(table);
-    // Widest staging word that keeps every segment start aligned (segment
-    // starts are multiples of 512 blocks = 9216 bytes).
-    if (aligned(table, 16) && row_bytes % 16 == 0)
-        return launch(embed_q4_0_kernel<TO, 16, VST>, grid, dim3(bs), 0, stream, o, ld_out, t,
-                      n_vocab, nb_row, ids);
-    if (aligned(table, 4) && row_bytes % 4 == 0)
-        return launch(embed_q4_0_kernel<TO, 4, VST>, grid, dim3(bs), 0, stream, o, ld_out, t,
-                      n_vocab, nb_row, ids);
-    if (aligned(table, 2))
-        return launch(embed_q4_0_kernel<TO, 2, VST>, grid, dim3(bs), 0, stream, o, ld_out, t,
-                      n_vocab, nb_row, ids);
-    return launch(embed_q4_0_kernel<TO, 1, VST>, grid, dim3(bs), 0, stream, o, ld_out, t,
-                  n_vocab, nb_row, ids);
+    const int units = nb_row * (32 * (int)sizeof(TO) / 16);
+    const int bs = units < kEmbedBlock ? round_up(units, kWave) : kEmbedBlock;
+    const dim3 grid(n_ids, (units + bs - 1) / bs);
+    return launch(embed_q4_0_kernel<TO, A2, VST>, grid, dim3(bs), 0, stream,
+                  static_cast<TO*>(out), ld_out, static_cast<const uint8_t*>(table), n_vocab,
+                  nb_row, ids);
+}
+
+template <typename TO>
+static int embed_pick(void* out, int64_t ld_out, const void* table, int n_vocab, int n_embd,
+                      const int32_t* ids, int n_ids, hipStream_t stream) {
+    const bool vst = aligned(out, 16) && (ld_out * (int64_t)sizeof(TO)) % 16 == 0;
+    const bool a2 = aligned(table, 2);
+    if (vst)
+        return a2 ? embed_launch<TO, true, true>(out, ld_out, table, n_vocab, n_embd, ids, n_ids,
+                                                 stream)
+                  : embed_launch<TO, false, true>(out, ld_out, table, n_vocab, n_embd, ids,
+                                                  n_ids, stream);
+    return a2 ? embed_launch<TO, true, false>(out, ld_out, table, n_vocab, n_embd, ids, n_ids,
+                                              stream)
+              : embed_launch<TO, false, false>(out, ld_out, table, n_vocab, n_embd, ids, n_ids,
+                                               stream);
 }
 
 static int embed_dispatch(void* out, int64_t ld_out, const void* table, int n_vocab, int n_embd,
@@ -170,15 +161,11 @@ static int embed_dispatch(void* out, int64_t ld_out, const void* table, int n_vo
     if (out_type != JINF_HIP_F16 && out_type != JINF_HIP_F32) return JINF_HIP_ERR_INVALID;
     const int64_t osz = out_type == JINF_HIP_F16 ? 2 : 4;
     if (!aligned(out, osz)) return JINF_HIP_ERR_INVALID;
-    if ((n_embd + kSegBlocks * 32 - 1) / (kSegBlocks * 32) > 65535) return JINF_HIP_ERR_INVALID;
-    const bool vst = aligned(out, 16) && (ld_out * osz) % 16 == 0;
+    // grid.y = unit tiles of one row (<= 65535)
+    if ((int64_t)n_embd * osz / 16 > 65535LL * kEmbedBlock) return JINF_HIP_ERR_INVALID;
     if (out_type == JINF_HIP_F16)
-        return vst ? embed_launch<uint16_t, 1>(out, ld_out, table, n_vocab, n_embd, ids, n_ids,
-                                               stream)
-                   : embed_launch<uint16_t, 0>(out, ld_out, table, n_vocab, n_embd, ids, n_ids,
-                                               stream);
-    return vst ? embed_launch<float, 1>(out, ld_out, table, n_vocab, n_embd, ids, n_ids, stream)
-               : embed_launch<float, 0>(out, ld_out, table, n_vocab, n_embd, ids, n_ids, stream);
+        return embed_pick<uint16_t>(out, ld_out, table, n_vocab, n_embd, ids, n_ids, stream);
+    return embed_pick<float>(out, ld_out, table, n_vocab, n_embd, ids, n_ids, stream);
 }
 
 }  // namespace jinf

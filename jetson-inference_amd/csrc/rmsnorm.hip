@@ -64,7 +64,7 @@ __device__ __forceinline__ float rms_scale(double ss, int n, float eps) {
     return (float)(1.0 / sqrt((double)t));
 }
 
-template <typename TA, typename TW, bool FUSED>
+template <typename TA, typename TW, bool FUSED, int CPT = kNormCPT>
 __global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(
     TA* out, int ld_out, TA* res, int ld_res, const TA* in, int ld_in,
     const TW* __restrict__ w, int n, float eps) {
@@ -78,44 +78,55 @@ __global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(
     const TA* x = in + row * ld_in;
     TA* r = FUSED ? res + row * ld_res : nullptr;
 
-    float h[kNormCPT][E];
-    float d[kNormCPT][E];
-    // Issue every load of the row before any store (out may alias in).
+    // The row stays in registers in its storage format (16-byte chunks); every
+    // load is issued before any store (out may alias in).
+    uint4 hv[CPT];
+    uint4 dv[CPT];
 #pragma unroll
-    for (int j = 0; j < kNormCPT; ++j) {
+    for (int j = 0; j < CPT; ++j) {
         const int c = threadIdx.x + j * bs;
         if (c < nch) {
-            A::load(x + (int64_t)c * E, h[j]);
-            if constexpr (FUSED) A::load(r + (int64_t)c * E, d[j]);
+            if constexpr (FUSED) {
+                hv[j] = ld16<true>(r + (int64_t)c * E);
+                dv[j] = ld16<true>(x + (int64_t)c * E);
+            } else {
+                hv[j] = ld16<true>(x + (int64_t)c * E);
+            }
         }
     }
     double ss = 0.0;
 #pragma unroll
-    for (int j = 0; j < kNormCPT; ++j) {
+    for (int j = 0; j < CPT; ++j) {
         const int c = threadIdx.x + j * bs;
         if (c < nch) {
+            float h[E];
+            A::unpack(hv[j], h);
             if constexpr (FUSED) {
+                float d[E];
+                A::unpack(dv[j], d);
 #pragma unroll
-                for (int e = 0; e < E; ++e) h[j][e] = A::round(d[j][e] + h[j][e]);
-                A::store(r + (int64_t)c * E, h[j]);
+                for (int e = 0; e < E; ++e) h[e] = h[e] + d[e];
+                hv[j] = A::pack(h);  // the stored residual, rounded once
+                st16<true>(r + (int64_t)c * E, hv[j]);
+                A::unpack(hv[j], h);
             }
 #pragma unroll
-            for (int e = 0; e < E; ++e) ss = fma((double)h[j][e], (double)h[j][e], ss);
+            for (int e = 0; e < E; ++e) ss = fma((double)h[e], (double)h[e], ss);
         }
     }
     ss = block_sum(ss, red);
     const float rs = rms_scale(ss, n, eps);
     TA* y = out + row * ld_out;
 #pragma unroll
-    for (int j = 0; j < kNormCPT; ++j) {
+    for (int j = 0; j < CPT; ++j) {
         const int c = threadIdx.x + j * bs;
         if (c < nch) {
-            float wv[E];
+            float h[E], wv[E], o[E];
+            A::unpack(hv[j], h);
             wvec<E>(w + c * E, wv);
-            float o[E];
 #pragma unroll
-            for (int e = 0; e < E; ++e) o[e] = (h[j][e] * rs) * wv[e];
-            A::store(y + (int64_t)c * E, o);
+            for (int e = 0; e < E; ++e) o[e] = (h[e] * rs) * wv[e];
+            st16<true>(y + (int64_t)c * E, A::pack(o));
         }
     }
 }

@@ -58,7 +58,8 @@ __device__ __forceinline__ void rope_table(float2* cs, int half, int pos,
     __syncthreads();
 }
 
-template <typename TA>
+// UPT units per thread, spaced one workgroup apart.
+template <typename TA, int UPT = 1>
 __global__ __launch_bounds__(kRopeBlock) void rope_vec_kernel(
     TA* q, int ld_q, TA* k, int ld_k, const int32_t* positions, int pos0, int head_dim,
     int units_q, int units_tok, RopeTheta th) {
@@ -66,25 +67,35 @@ __global__ __launch_bounds__(kRopeBlock) void rope_vec_kernel(
     constexpr int E = A::kElems;
     __shared__ float2 cs[kRopeMaxHalf];
     const int64_t t = blockIdx.x;
-    const int u = blockIdx.y * kRopeBlock + threadIdx.x;
-    TA* p = nullptr;
-    int i0 = 0;
-    float v[E];
-    if (u < units_tok) {
-        const int uu = u < units_q ? u : u - units_q;
-        p = u < units_q ? q + t * ld_q + (int64_t)uu * E : k + t * ld_k + (int64_t)uu * E;
-        i0 = (uu * E % head_dim) / 2;
-        A::load(p, v);
+    TA* p[UPT];
+    int i0[UPT];
+    uint4 raw[UPT];
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) {
+        const int u = (blockIdx.y * UPT + j) * kRopeBlock + threadIdx.x;
+        p[j] = nullptr;
+        i0[j] = 0;
+        if (u < units_tok) {
+            const int uu = u < units_q ? u : u - units_q;
+            p[j] = u < units_q ? q + t * ld_q + (int64_t)uu * E : k + t * ld_k + (int64_t)uu * E;
+            i0[j] = (uu * E % head_dim) / 2;
+            raw[j] = ld16<true>(p[j]);
+        }
     }
     const int pos = positions ? positions[t] : pos0 + (int)t;
     rope_table(cs, head_dim / 2, pos, th);
-    if (u < units_tok) {
 #pragma unroll
-        for (int e = 0; e < E / 2; ++e) {
-            const float2 c = cs[i0 + e];
-            rot(v[2 * e], v[2 * e + 1], c.x, c.y);
+    for (int j = 0; j < UPT; ++j) {
+        if (p[j]) {
+            float v[E];
+            A::unpack(raw[j], v);
+#pragma unroll
+            for (int e = 0; e < E / 2; ++e) {
+                const float2 c = cs[i0[j] + e];
+                rot(v[2 * e], v[2 * e + 1], c.x, c.y);
+            }
+            st16<true>(p[j], A::pack(v));
         }
-        A::store(p, v);
     }
 }
 

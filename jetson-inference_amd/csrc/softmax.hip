@@ -13,11 +13,12 @@
 // registers (kSmCPT float4 chunks per thread, so up to 32 KiB per row with
 // 256 lanes), exponentiated once, and written once: one HBM read and one write
 // per element, against the reference's three reads and two exp evaluations.
-// Max and sum are wave64 butterflies plus one LDS exchange; the sum is
-// accumulated in fp64 so its rounding does not depend on the launch shape.
-// Rows longer than the register capacity (or unaligned rows) take a two-pass
-// kernel that keeps an online (max, sum) pair per thread and re-reads the row
-// for the write pass.
+// Max and sum are wave64 butterflies plus one LDS exchange; each aligned group
+// of 4 exponentials is summed in fp32 and the group sums in fp64.  Chunks past
+// the row's live length do no arithmetic (whole waves branch over them), so
+// the VALU cost follows the live length, not the padded stride.
+// Rows longer than the register capacity (or unaligned rows) take a loop
+// kernel that reads the row three times (max, sum, write) like the reference.
 #include <math.h>
 
 #include "jinf_device.h"
@@ -36,6 +37,27 @@ __device__ __forceinline__ int live_len(const int32_t* lens, int rows_per_len, i
     return L > n_cols ? n_cols : L;
 }
 
+// exp(a) for the softmax argument a = s - m <= 0, accurate to ~2 ulp:
+// Cody-Waite splitting of a*log2(e) into hi + lo (hi the rounded product, lo its
+// exact rounding error plus a times the tail of log2(e)), then
+// 2^hi (v_exp_f32) * (1 + lo*ln2).  |lo| <= 2^-24 |hi| + tiny, so the
+// dropped second-order term is below 1e-13.  Six VALU ops against ~12 for the
+// library expf.  a < -104 (including -inf) returns +0: the true value is below
+// the smallest fp32 subnormal there.  Arguments below about -87.3 give fp32
+// subnormals, which the hardware exp2 may return as 0 (absolute error < 1.2e-38).
+__device__ __forceinline__ float exp_neg(float a) {
+    constexpr float kL2E = 1.44269502162933349609375f;        // fl32(log2 e)
+    constexpr float kL2ELo = 1.925963033500011079e-08f;       // log2 e - kL2E
+    constexpr float kLn2 = 0.693147180559945309f;
+    const float hi = a * kL2E;
+    float lo = fmaf(a, kL2E, -hi);
+    lo = fmaf(a, kL2ELo, lo);
+    const float e = __builtin_amdgcn_exp2f(hi);
+    const float r = fmaf(e, lo * kLn2, e);
+    return a < -104.0f ? 0.0f : r;
+}
+
+template <int CPT = kSmCPT>
 __global__ __launch_bounds__(1024) void softmax_vec_kernel(
     float* out, int ld_out, const float* in, int ld_in, int n_cols, const int32_t* lens,
     int rows_per_len, float scale) {
@@ -51,46 +73,51 @@ __global__ __launch_bounds__(1024) void softmax_vec_kernel(
     const int nfull = L >> 2;  // whole float4 chunks
     const float ninf = -INFINITY;
 
-    float v[kSmCPT][4];
+    // Chunks at or past L do no arithmetic: whole waves skip them.
+    float v[CPT][4];
+    float mx = ninf;
 #pragma unroll
-    for (int j = 0; j < kSmCPT; ++j) {
+    for (int j = 0; j < CPT; ++j) {
         const int c = threadIdx.x + j * bs;
         if (c < nfull) {
-            const float4 t = *reinterpret_cast<const float4*>(x + 4 * c);
-            v[j][0] = t.x; v[j][1] = t.y; v[j][2] = t.z; v[j][3] = t.w;
+            Act<float>::load(x + 4 * c, v[j]);
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[j][e] = (4 * c + e < L) ? x[4 * c + e] : ninf;
         }
-    }
-    float mx = ninf;
+        if (4 * c < L) {
 #pragma unroll
-    for (int j = 0; j < kSmCPT; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            v[j][e] = v[j][e] * scale;  // -inf * scale stays -inf for scale > 0
-            mx = fmaxf(mx, v[j][e]);
+            for (int e = 0; e < 4; ++e) {
+                v[j][e] = v[j][e] * scale;  // -inf * scale stays -inf for scale > 0
+                mx = fmaxf(mx, v[j][e]);
+            }
         }
+    }
     mx = block_max(mx, redf);
     double sum = 0.0;
 #pragma unroll
-    for (int j = 0; j < kSmCPT; ++j)
+    for (int j = 0; j < CPT; ++j) {
+        const int c = threadIdx.x + j * bs;
+        if (4 * c < L) {
+            float part = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int idx = 4 * (threadIdx.x + j * bs) + e;
-            const float ex = idx < L ? expf(v[j][e] - mx) : 0.0f;
-            v[j][e] = ex;
-            sum += (double)ex;
+            for (int e = 0; e < 4; ++e) {
+                const float ex = 4 * c + e < L ? exp_neg(v[j][e] - mx) : 0.0f;
+                v[j][e] = ex;
+                part += ex;
+            }
+            sum += (double)part;
         }
+    }
     sum = block_sum(sum, redd);
     const float inv = 1.0f / (float)sum;
 #pragma unroll
-    for (int j = 0; j < kSmCPT; ++j) {
+    for (int j = 0; j < CPT; ++j) {
         const int c = threadIdx.x + j * bs;
         if (c < nfull) {
-            *reinterpret_cast<float4*>(y + 4 * c) =
-                make_float4(v[j][0] * inv, v[j][1] * inv, v[j][2] * inv, v[j][3] * inv);
-        } else {
+            const float o[4] = {v[j][0] * inv, v[j][1] * inv, v[j][2] * inv, v[j][3] * inv};
+            Act<float>::store(y + 4 * c, o);
+        } else if (4 * c < L) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 if (4 * c + e < L) y[4 * c + e] = v[j][e] * inv;
@@ -98,8 +125,8 @@ __global__ __launch_bounds__(1024) void softmax_vec_kernel(
     }
 }
 
-// Any length / alignment.  Pass 1: per-thread online (max, sum); the pairs
-// are merged across the workgroup.  Pass 2 re-reads and writes.
+// Any length / alignment: pass 1 max, pass 2 sum of exponentials, pass 3
+// write; each pass re-reads the row.
 __global__ __launch_bounds__(1024) void softmax_loop_kernel(
     float* out, int ld_out, const float* in, int ld_in, int n_cols, const int32_t* lens,
     int rows_per_len, float scale) {
@@ -115,10 +142,10 @@ __global__ __launch_bounds__(1024) void softmax_loop_kernel(
     for (int i = threadIdx.x; i < L; i += blockDim.x) m = fmaxf(m, x[i] * scale);
     m = block_max(m, redf);
     double sum = 0.0;
-    for (int i = threadIdx.x; i < L; i += blockDim.x) sum += (double)expf(x[i] * scale - m);
+    for (int i = threadIdx.x; i < L; i += blockDim.x) sum += (double)exp_neg(x[i] * scale - m);
     sum = block_sum(sum, redd);
     const float inv = 1.0f / (float)sum;
-    for (int i = threadIdx.x; i < L; i += blockDim.x) y[i] = expf(x[i] * scale - m) * inv;
+    for (int i = threadIdx.x; i < L; i += blockDim.x) y[i] = exp_neg(x[i] * scale - m) * inv;
 }
 
 static int softmax_dispatch(float* out, int ld_out, const float* in, int ld_in, int n_rows,
@@ -135,8 +162,8 @@ static int softmax_dispatch(float* out, int ld_out, const float* in, int ld_in, 
     if (bs < 256 && n_cols > 256) bs = 256;
     if (bs < kWave) bs = kWave;
     if (vec && bs <= 1024)
-        return launch(softmax_vec_kernel, dim3(n_rows), dim3(bs), 0, stream, out, ld_out, in,
-                      ld_in, n_cols, lens, rows_per_len, scale);
+        return launch(softmax_vec_kernel<kSmCPT>, dim3(n_rows), dim3(bs), 0, stream, out, ld_out,
+                      in, ld_in, n_cols, lens, rows_per_len, scale);
     const int lbs = n_cols >= 1024 ? 1024 : round_up(n_cols, kWave);
     return launch(softmax_loop_kernel, dim3(n_rows), dim3(lbs), 0, stream, out, ld_out, in,
                   ld_in, n_cols, lens, rows_per_len, scale);
