@@ -246,12 +246,103 @@ def cpu_baseline(ks, threads, budget_s):
 # rocprof-derived traffic figure, if a committed summary exists
 # --------------------------------------------------------------------------
 
-def traffic_from_profiles(kernel):
-    path = os.path.join(ROOT, "profiles", f"{kernel}_pmc.txt")
+def traffic_from_profiles(kernel, workload):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary of `workload` (profiles/<workload>_pmc.txt), if there is one."""
+    path = os.path.join(ROOT, "profiles", f"{workload}_pmc.txt")
     if not os.path.exists(path):
         return None
-    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.]+)", open(path).read(), re.M)
+    m = re.search(rf"^{re.escape(kernel)}_traffic_bytes_per_launch:\s*([0-9.]+)",
+                  open(path).read(), re.M)
     return float(m.group(1)) if m else None
+
+
+CALIB_BYTES = 256 << 20  # plain D2D copy used to scale the FETCH/WRITE counters
+
+
+def calibrate_copy(torch, reps=5):
+    """A plain device copy of known size (CALIB_BYTES read + written)."""
+    src = torch.empty(CALIB_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def rocprof_summary(dbs, bytes_per_kernel):
+    """Text summary of rocprofv3 databases: per-kernel dispatch durations and,
+    for --pmc runs, per-dispatch FETCH_SIZE / WRITE_SIZE (KiB), the copy
+    calibration factors, and the resulting HBM bytes per launch."""
+    import sqlite3
+
+    lines = []
+    durs, ctrs = {}, {}
+    for db in dbs:
+        c = sqlite3.connect(db)
+        # the copy calibration is the largest-grid blit; torch's small copies share its name
+        big = c.execute("select max(grid_x * grid_y * grid_z) from kernels "
+                        "where name like '%copyBuffer%'").fetchone()[0] or 0
+        for name, n, avg, mn, mx in c.execute(
+                "select name, count(*), avg(duration), min(duration), max(duration) from kernels "
+                "where name not like '%copyBuffer%' or grid_x * grid_y * grid_z = ? "
+                "group by name", (big,)):
+            key = short_kernel(name)
+            if key:
+                durs.setdefault(key, (n, avg, mn, mx))
+        try:
+            rows = c.execute("select kernel_name, counter_name, avg(value), count(*) from "
+                             "counters_collection where kernel_name not like '%copyBuffer%' "
+                             "or grid_size = ? group by kernel_name, counter_name",
+                             (big,)).fetchall()
+        except sqlite3.OperationalError:
+            rows = []
+        for name, cn, v, n in rows:
+            key = short_kernel(name)
+            if key:
+                ctrs[(key, cn)] = (v, n)
+    lines.append("kernel durations (rocprofv3 --kernel-trace), microseconds:")
+    lines.append(f"  {'kernel':44s} {'calls':>6s} {'avg':>9s} {'min':>9s} {'max':>9s}")
+    for k, (n, avg, mn, mx) in sorted(durs.items()):
+        lines.append(f"  {k:44s} {n:6d} {avg / 1e3:9.3f} {mn / 1e3:9.3f} {mx / 1e3:9.3f}")
+    if ctrs:
+        lines.append("counters per dispatch (rocprofv3 --pmc), KiB:")
+        for (k, cn), (v, n) in sorted(ctrs.items()):
+            lines.append(f"  {k:44s} {cn:12s} {v:14.1f}  ({n} dispatches)")
+        cal_f = ctrs.get(("copy_calibration", "FETCH_SIZE"))
+        cal_w = ctrs.get(("copy_calibration", "WRITE_SIZE"))
+        if cal_f and cal_w:
+            ff = CALIB_BYTES / 1024 / cal_f[0]
+            fw = CALIB_BYTES / 1024 / cal_w[0]
+            lines.append(f"copy calibration ({CALIB_BYTES >> 20} MiB read + written): "
+                         f"FETCH factor {ff:.4f}, WRITE factor {fw:.4f}")
+            for k, nb in bytes_per_kernel.items():
+                f = ctrs.get((k, "FETCH_SIZE"))
+                w = ctrs.get((k, "WRITE_SIZE"))
+                if f and w:
+                    t = (f[0] * ff + w[0] * fw) * 1024
+                    lines.append(f"{k}: traffic {t:.0f} B/launch vs algorithmic {nb} B "
+                                 f"(ratio {t / nb:.3f})")
+                    lines.append(f"{k}_traffic_bytes_per_launch: {t:.0f}")
+    return "\n".join(lines)
+
+
+_KERNEL_KEYS = [("ew_vec_kernel<unsigned short, 1", "swiglu"),
+                ("ew_vec_kernel<unsigned short, 2", "residual_add_f16"),
+                ("rmsnorm_vec_kernel<unsigned short, unsigned short, true", "residual_rmsnorm"),
+                ("rmsnorm_vec_kernel", "rmsnorm"),
+                ("embed_q4_0_kernel", "q4_0_gather"),
+                ("rope_vec_kernel", "rope"),
+                ("softmax_vec_kernel", "masked_softmax"),
+                ("softmax_loop_kernel", "softmax_loop"),
+                ("copyBuffer", "copy_calibration")]
+
+
+def short_kernel(name):
+    for pat, key in _KERNEL_KEYS:
+        if pat in name:
+            return key
+    return None
 
 
 def main():
@@ -266,7 +357,17 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, host cores)")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch eagerly instead of replaying a captured HIP graph")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 256 MiB device copy (PMC scaling reference)")
+    ap.add_argument("--rocprof-summary", nargs="+", metavar="DB",
+                    help="summarize rocprofv3 result databases and exit (no GPU use)")
     args = ap.parse_args()
+
+    if args.rocprof_summary:
+        nb = {"rope": 10487808, "residual_rmsnorm": 67117056, "swiglu": 176160768,
+              "q4_0_gather": 43008000}
+        print(rocprof_summary(args.rocprof_summary, nb))
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -348,7 +449,10 @@ def main():
                 "achieved": round(dom_gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom_gbs / PEAK_GBS, 4), "bytes_per_launch": dom.nbytes,
                 "avg_launch_us": round(dom_us, 3),
-                "traffic": traffic_from_profiles(dom.name)}
+                "traffic": traffic_from_profiles(dom.name, args.workload)}
+
+    if args.calibrate_copy:
+        calibrate_copy(torch)
 
     cpu = None
     if args.cpu_seconds > 0:

@@ -90,7 +90,9 @@ int jinf_residual_add_rows(void* a, int ld_a, const void* b, int ld_b, int n_row
  * and out[r, j] = exp(s_j - m) / sum_k exp(s_k - m) for j < L_r, with
  * s_j = scale * in[r, j] and m = max_j s_j.  Elements j >= L_r are neither
  * read nor written; L_r == 0 leaves the row untouched.  out may alias in.
- * rows_per_len lets all query heads of one sequence share one length entry.
+ * rows_per_len (> 0) lets all query heads of one sequence share one length
+ * entry; lens then holds ceil(n_rows / rows_per_len) values.  scale must be
+ * finite and > 0 (1 for pre-scaled scores).
  * Semantics of cuda/softmax_kernel.cu:8-42 and the attention softmax phase
  * cuda/attention_kernel.cu:59-87 (length n_past = pos + 1). */
 int jinf_softmax_rows_f32(float* out, int ld_out, const float* in, int ld_in,
