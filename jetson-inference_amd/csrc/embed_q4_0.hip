@@ -17,8 +17,9 @@
 // not 4-byte aligned).  The 16 lanes that share a 288-byte run of blocks hit
 // the same cache lines, so HBM sees each table byte once; consecutive lanes
 // store consecutive 16-byte units with nontemporal stores, fully coalesced.
-// Measured on MI355X (4096 ids of a 128256 x 4096 table -> fp16): 7.8 us with
-// 512 lanes per row, against 8.3 us for staging the row through LDS first.
+// Measured on MI355X (4096 ids of a 128256 x 4096 table -> fp16): 7.86 us with
+// 256-lane workgroups (two per 4096-wide row), 8.1 us with 512 lanes, 8.3 us for
+// staging the row through LDS first; 2 or 4 units per lane gain nothing.
 // fp16 decode is exact and packed: 0x6400 | nibble is the binary16 value
 // 1024 + nibble; subtracting 1032 gives nibble - 8 exactly, and one packed
 // binary16 multiply by d is the single RNE rounding of the exact product
@@ -31,7 +32,7 @@
 namespace jinf {
 
 constexpr int kQ4Bytes = 18;
-constexpr int kEmbedBlock = 512;
+constexpr int kEmbedBlock = 256;
 
 // Four nibble bytes (little-endian in w) -> 8 binary16 values in jinf order,
 // each = (nibble - 8) * d rounded once.

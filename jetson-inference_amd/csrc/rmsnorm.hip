@@ -27,31 +27,43 @@ namespace jinf {
 
 constexpr int kNormCPT = 4;  // 16-byte chunks per thread held in registers
 
-// E consecutive weight elements widened to fp32 (vector loads).
-template <int E> __device__ __forceinline__ void wvec(const float* w, float (&v)[E]) {
+// E consecutive weight elements: raw bits loaded with the row (normal cached
+// loads: every row re-reads the weight), widened to fp32 after the reduction.
+template <typename TW, int E> struct WRaw {
+    static constexpr int kWords = (E * (int)sizeof(TW) + 15) / 16;  // 16-byte words
+    uint4 w[kWords];
+};
+
+template <int E>
+__device__ __forceinline__ void wload_raw(const float* w, WRaw<float, E>& r) {
 #pragma unroll
-    for (int i = 0; i < E; i += 4) {
-        const float4 x = *reinterpret_cast<const float4*>(w + i);
-        v[i] = x.x; v[i + 1] = x.y; v[i + 2] = x.z; v[i + 3] = x.w;
-    }
+    for (int i = 0; i < WRaw<float, E>::kWords; ++i) r.w[i] = ld16<false>(w + 4 * i);
 }
-template <int E> __device__ __forceinline__ void wvec(const uint16_t* w, float (&v)[E]) {
+template <int E>
+__device__ __forceinline__ void wload_raw(const uint16_t* w, WRaw<uint16_t, E>& r) {
     if constexpr (E == 8) {
-        const uint4 x = *reinterpret_cast<const uint4*>(w);
-        const uint32_t u[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            v[2 * i] = h2f((uint16_t)(u[i] & 0xFFFFu));
-            v[2 * i + 1] = h2f((uint16_t)(u[i] >> 16));
-        }
+        r.w[0] = ld16<false>(w);
     } else {
         const uint2 x = *reinterpret_cast<const uint2*>(w);
-        const uint32_t u[2] = {x.x, x.y};
+        r.w[0] = make_uint4(x.x, x.y, 0, 0);
+    }
+}
+template <int E>
+__device__ __forceinline__ void wunpack(const WRaw<float, E>& r, float (&v)[E]) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            v[2 * i] = h2f((uint16_t)(u[i] & 0xFFFFu));
-            v[2 * i + 1] = h2f((uint16_t)(u[i] >> 16));
-        }
+    for (int i = 0; i < E; ++i) {
+        const uint4 q = r.w[i / 4];
+        const uint32_t u = (i % 4 == 0) ? q.x : (i % 4 == 1) ? q.y : (i % 4 == 2) ? q.z : q.w;
+        v[i] = __builtin_bit_cast(float, u);
+    }
+}
+template <int E>
+__device__ __forceinline__ void wunpack(const WRaw<uint16_t, E>& r, float (&v)[E]) {
+    const uint32_t u[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) {
+        v[2 * i] = h2f((uint16_t)(u[i] & 0xFFFFu));
+        v[2 * i + 1] = h2f((uint16_t)(u[i] >> 16));
     }
 }
 
@@ -80,8 +92,11 @@ __global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(
 
     // The row stays in registers in its storage format (16-byte chunks); every
     // load is issued before any store (out may alias in).
+    // The weight chunks are fetched with the row, so their latency is not
+    // paid again after the reduction.
     uint4 hv[CPT];
     uint4 dv[CPT];
+    WRaw<TW, E> wr[CPT];
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
         const int c = threadIdx.x + j * bs;
@@ -92,6 +107,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(
             } else {
                 hv[j] = ld16<true>(x + (int64_t)c * E);
             }
+            wload_raw<E>(w + c * E, wr[j]);
         }
     }
     double ss = 0.0;
@@ -123,7 +139,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(
         if (c < nch) {
             float h[E], wv[E], o[E];
             A::unpack(hv[j], h);
-            wvec<E>(w + c * E, wv);
+            wunpack<E>(wr[j], wv);
 #pragma unroll
             for (int e = 0; e < E; ++e) o[e] = (h[e] * rs) * wv[e];
             st16<true>(y + (int64_t)c * E, A::pack(o));
