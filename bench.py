@@ -172,6 +172,20 @@ def build_softmax(torch, jinf, g, n_seq, n_heads, max_len, keep):
                   lambda o, s, lc: o.softmax_rows(s, lc, n_heads, 1.0))
 
 
+def build_matvec(torch, jinf, g, name, rows, cols, keep):
+    """Q4_0 dequant-GEMV y = W x at batch 1 (fp32 x, y)."""
+    nbytes = rows * (cols // 32) * 18 + cols * 4 + rows * 4
+    sets = []
+    for _ in range(n_sets(nbytes)):
+        W = q4_0_table(torch, rows, cols, g)
+        x = torch.randn(cols, generator=g, device="cuda")
+        y = torch.empty(rows, dtype=torch.float32, device="cuda")
+        keep.append((W, x, y))
+        sets.append(lambda W=W, x=x, y=y: jinf.matvec_q4_0(W, x, y))
+    return Kernel(name, nbytes, rows, "output rows", sets, "matvec_q4_0_kernel",
+                  keep[-len(sets)][:2], lambda o, W, x: o.matvec_q4_0(W, x))
+
+
 def workload(name, torch, jinf, seed):
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
@@ -195,6 +209,19 @@ def workload(name, torch, jinf, seed):
         cfg = {"workload": name, "shapes": "Llama-3-70B decode, 64 sequences: hidden 8192, "
                "64/8 heads x 128, FFN 28672, score rows 4096 x stride 8192, len = pos + 1",
                "storage": "f16 activations, f32 scores", "baseline_configs": [5]}
+    elif name == "llama3-8b-gemv":
+        H, F, KV = 4096, 14336, 1024
+        ks = [build_matvec(torch, jinf, g, "gemv_q", H, H, keep),
+              build_matvec(torch, jinf, g, "gemv_k", KV, H, keep),
+              build_matvec(torch, jinf, g, "gemv_v", KV, H, keep),
+              build_matvec(torch, jinf, g, "gemv_o", H, H, keep),
+              build_matvec(torch, jinf, g, "gemv_gate", F, H, keep),
+              build_matvec(torch, jinf, g, "gemv_up", F, H, keep),
+              build_matvec(torch, jinf, g, "gemv_down", H, F, keep)]
+        cfg = {"workload": name, "shapes": "Llama-3-8B layer projections at batch 1 (decode): "
+               "q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096, down 4096x14336, Q4_0 "
+               "weights, fp32 x/y", "storage": "Q4_0 weights, f32 vectors",
+               "baseline_configs": [], "note": "SURVEY 8(f) f1, next component"}
     elif name in ("rope", "norm", "swiglu", "gather", "softmax"):
         b = {"rope": lambda: build_rope(torch, jinf, g, 512, 32, 8, 128,
                                         torch.arange(512, dtype=torch.int32, device="cuda"), keep),

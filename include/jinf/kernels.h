@@ -69,6 +69,15 @@ void jinf_cuda_residual_add(float* a, const float* b, int n, hipStream_t stream)
 void jinf_cuda_dequantize_q4_0(const void* data, float* output, int n_blocks,
                                hipStream_t stream);
 
+/* y[row] = sum_j W[row, j] * x[j] for a [rows, cols] matrix stored as GGUF
+ * Q4_0 blocks along the columns (cols % 32 == 0; jinf's interleaved nibble
+ * order), fp32 x and y.  qtype 2 (Q4_0) is served; any other qtype prints one
+ * stderr line and enqueues nothing.  W 2-byte aligned, x and y 4-byte aligned.
+ * Replaces jinf_cuda_dequant_matvec, cuda/matmul_kernels.cu:198-225 (Q4_0
+ * kernel :8-43). */
+void jinf_cuda_dequant_matvec(const void* weight, const float* input, float* output,
+                              int rows, int cols, int qtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -111,6 +111,12 @@ int jinf_embed_q4_0(void* out, int ld_out, const void* table, int n_vocab,
                     int n_embd, const int32_t* ids, int n_ids, int out_type,
                     hipStream_t stream);
 
+/* Q4_0 dequant-GEMV, y = W x (W [rows, cols] in Q4_0 blocks, x/y fp32), with
+ * a status return.  Same arithmetic as jinf_cuda_dequant_matvec (Q4_0).
+ * Fast path: cols % 256 == 0, W and x 16-byte aligned. */
+int jinf_matvec_q4_0(const void* weight, const float* x, float* y, int rows, int cols,
+                     hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

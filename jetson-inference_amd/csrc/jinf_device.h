@@ -137,6 +137,28 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// fp32 wave sum without LDS round trips: four DPP steps (quad swaps, then
+// rotations by 4 and 8 lanes within each row of 16) leave every lane with its
+// row's sum; the four row sums are read into scalars and added in row order.
+// Returns the same value in every lane.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f32<0x124>(v);  // row_ror:4
+    v += dpp_f32<0x128>(v);  // row_ror:8
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return ((r0 + r1) + r2) + r3;
+}
+
 // Workgroup reductions.  blockDim.x must be a multiple of 64 and at most 1024.
 // `lds` holds one slot per wave; each thread folds the per-wave partials in
 // wave order, so every thread returns the same value without a second

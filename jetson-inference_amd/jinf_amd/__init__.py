@@ -1,6 +1,7 @@
 """jinf_amd: MI355X (gfx950) kernels for jinf's per-layer elementwise and
 reduction path -- RMSNorm (+ fused residual add), interleaved GQA RoPE,
-SwiGLU, masked row softmax and the GGUF Q4_0 token-embedding gather.
+SwiGLU, masked row softmax and the GGUF Q4_0 token-embedding gather -- and the
+Q4_0 dequant-GEMV beside them.
 
 The kernels live in libjinf_hip.so behind the C-ABI of include/jinf/*.h;
 this package is a thin ctypes/torch front end used by tests and bench.py.
@@ -8,6 +9,7 @@ this package is a thin ctypes/torch front end used by tests and bench.py.
 from ._lib import F16, F32, LIB_PATH, lib, version  # noqa: F401
 from .ops import (  # noqa: F401
     JinfError,
+    cuda_dequant_matvec,
     cuda_dequantize_q4_0,
     cuda_residual_add,
     cuda_rmsnorm,
@@ -15,6 +17,7 @@ from .ops import (  # noqa: F401
     cuda_silu_mul,
     cuda_softmax,
     embed_q4_0,
+    matvec_q4_0,
     residual_add,
     residual_rmsnorm_rows,
     rmsnorm_rows,

@@ -34,6 +34,7 @@ SIGNATURES = {
     "jinf_cuda_softmax": (None, [_P, _P, _I, _P]),
     "jinf_cuda_residual_add": (None, [_P, _P, _I, _P]),
     "jinf_cuda_dequantize_q4_0": (None, [_P, _P, _I, _P]),
+    "jinf_cuda_dequant_matvec": (None, [_P, _P, _P, _I, _I, _I, _P]),
     # extensions (include/jinf/kernels_ext.h)
     "jinf_hip_version": (ctypes.c_char_p, []),
     "jinf_rmsnorm_rows": (_I, [_P, _I, _P, _I, _P, _I, _I, _F, _I, _I, _P]),
@@ -43,6 +44,7 @@ SIGNATURES = {
     "jinf_residual_add_rows": (_I, [_P, _I, _P, _I, _I, _I, _I, _P]),
     "jinf_softmax_rows_f32": (_I, [_P, _I, _P, _I, _I, _I, _P, _I, _F, _P]),
     "jinf_embed_q4_0": (_I, [_P, _I, _P, _I, _I, _P, _I, _I, _P]),
+    "jinf_matvec_q4_0": (_I, [_P, _P, _P, _I, _I, _P]),
 }
 
 _lib = None

@@ -152,6 +152,18 @@ def embed_q4_0(table, ids, n_embd, out_dtype=torch.float16, out=None):
     return out
 
 
+def matvec_q4_0(weight, x, y=None):
+    """y = W x: weight uint8 [rows, cols/32*18] (Q4_0 blocks), x fp32 [cols]."""
+    rows = weight.shape[0]
+    cols = x.shape[0]
+    if weight.shape[1] != cols // 32 * 18:
+        raise JinfError("weight row bytes do not match cols")
+    y = torch.empty(rows, dtype=torch.float32, device=x.device) if y is None else y
+    _check(lib().jinf_matvec_q4_0(_ptr(weight), _ptr(x), _ptr(y), rows, cols, _stream()),
+           "jinf_matvec_q4_0")
+    return y
+
+
 # ---- drop-in entry points (reference signatures; fp32, one row) ----
 
 def cuda_rmsnorm(out, x, weight, eps=1e-5):
@@ -180,6 +192,12 @@ def cuda_softmax(out, x):
 def cuda_residual_add(a, b):
     lib().jinf_cuda_residual_add(_ptr(a), _ptr(b), a.numel(), _stream())
     return a
+
+
+def cuda_dequant_matvec(weight, x, y, rows, cols, qtype=2):
+    lib().jinf_cuda_dequant_matvec(_ptr(weight), _ptr(x), _ptr(y), int(rows), int(cols),
+                                   int(qtype), _stream())
+    return y
 
 
 def cuda_dequantize_q4_0(data, out, n_blocks, byte_offset=0):

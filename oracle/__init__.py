@@ -39,6 +39,7 @@ _SIG = {
     "jo_rope_rows": (None, [_P, _L, _P, _L, _P, _I, _I, _I, _I, _I, _F, _I]),
     "jo_swiglu": (None, [_P, _P, _P, _L, _I]),
     "jo_softmax_rows": (None, [_P, _L, _P, _L, _I, _I, _P, _I, _F]),
+    "jo_matvec_q4_0": (None, [_P, _P, _P, _P, _I, _I]),
 }
 
 _lib = None
@@ -225,3 +226,19 @@ def softmax_rows(x, lens=None, rows_per_len=1, scale=1.0, out=None):
     lib().jo_softmax_rows(_p(out), n, _p(x), n, rows, n, _p(l_a), int(rows_per_len),
                           float(scale))
     return out
+
+
+# ---- Q4_0 dequant-GEMV ----
+
+def matvec_q4_0(W_u8, x):
+    """W uint8 [rows, cols/32*18] Q4_0, x fp32 [cols] -> (y fp32 [rows],
+    sum_j |w_j x_j| fp64 [rows])."""
+    W = _c(np.asarray(W_u8, dtype=np.uint8))
+    x = _c(np.asarray(x, dtype=np.float32))
+    rows = W.shape[0]
+    cols = x.shape[0]
+    assert W.shape[1] == cols // 32 * 18
+    y = np.empty(rows, np.float32)
+    a = np.empty(rows, np.float64)
+    lib().jo_matvec_q4_0(_p(W), _p(x), _p(y), _p(a), rows, cols)
+    return y, a

@@ -17,6 +17,7 @@
  *   RoPE                   cuda/rope_kernel.cu:8-50
  *   SiLU * up              cuda/silu_kernel.cu:6-18
  *   softmax                cuda/softmax_kernel.cu:8-42, cuda/attention_kernel.cu:59-87
+ *   Q4_0 dequant-GEMV      cuda/matmul_kernels.cu:8-43, 198-225
  * Build with -ffp-contract=off (no FMA contraction) and without fast-math.
  *
  * fp16 storage: every stored value is fl16(fl32(expression)) with
@@ -316,5 +317,35 @@ void jo_softmax_rows(float* out, int64_t ld_out, const float* in, int64_t ld_in,
         for (int j = 0; j < L; ++j) sum += (double)(float)exp((double)(x[j] * scale - m));
         const float inv = 1.0f / (float)sum;
         for (int j = 0; j < L; ++j) y[j] = (float)exp((double)(x[j] * scale - m)) * inv;
+    }
+}
+
+/* ---- Q4_0 dequant-GEMV (cuda/matmul_kernels.cu:8-43, :198-225) ---- */
+
+/* y[r] = sum_j ((q_j - 8) * d) * x[j]; every product is exact in fp64 (a
+ * 15-bit weight times a 24-bit x) and the sum is accumulated in fp64 in
+ * column order, then rounded once.  abs_y (optional) receives
+ * sum_j |w_j * x_j|, the scale of the dot product's rounding error. */
+void jo_matvec_q4_0(const uint8_t* W, const float* x, float* y, double* abs_y, int rows,
+                    int cols) {
+    const int nb = cols / 32;
+    const int64_t row_bytes = (int64_t)nb * 18;
+#pragma omp parallel for num_threads(jo_threads) schedule(static)
+    for (int r = 0; r < rows; ++r) {
+        double acc = 0.0, aabs = 0.0;
+        const uint8_t* row = W + (int64_t)r * row_bytes;
+        for (int b = 0; b < nb; ++b) {
+            const uint8_t* blk = row + 18 * (int64_t)b;
+            const double d = (double)jo_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+            for (int j = 0; j < 16; ++j) {
+                const uint8_t byte = blk[2 + j];
+                const double t0 = (double)((int)(byte & 0x0F) - 8) * d * (double)x[32 * b + 2 * j];
+                const double t1 = (double)((int)(byte >> 4) - 8) * d * (double)x[32 * b + 2 * j + 1];
+                acc += t0 + t1;
+                aabs += fabs(t0) + fabs(t1);
+            }
+        }
+        y[r] = (float)acc;
+        if (abs_y) abs_y[r] = aabs;
     }
 }

@@ -37,7 +37,7 @@ def test_headers_include_no_gpu_runtime_header():
 
 def test_every_declared_symbol_is_exported_with_declared_arity():
     decl = declared()
-    assert len(decl) == 14
+    assert len(decl) == 16
     lib = jinf_amd.lib()
     for name, n in decl.items():
         assert hasattr(lib, name), name
@@ -72,6 +72,9 @@ FAKE = P(0x1000)  # never dereferenced: every call below is rejected on the host
     lambda L: L.jinf_embed_q4_0(FAKE, 100, FAKE, 10, 100, FAKE, 4, 1, None),
     lambda L: L.jinf_embed_q4_0(FAKE, 128, FAKE, 10, 128, FAKE, 4, 2, None),
     lambda L: L.jinf_embed_q4_0(FAKE, 128, FAKE, 10, 128, None, 11, 1, None),
+    lambda L: L.jinf_matvec_q4_0(FAKE, FAKE, FAKE, 16, 100, None),
+    lambda L: L.jinf_matvec_q4_0(FAKE, FAKE, FAKE, -1, 128, None),
+    lambda L: L.jinf_matvec_q4_0(None, FAKE, FAKE, 16, 128, None),
 ])
 def test_invalid_arguments_rejected_on_host(call):
     assert call(jinf_amd.lib()) == _lib.JINF_HIP_ERR_INVALID
@@ -83,6 +86,7 @@ def test_invalid_arguments_rejected_on_host(call):
     lambda L: L.jinf_rope_rows(FAKE, 256, FAKE, 128, None, 0, 0, 128, 2, 1, 1e4, 1, None),
     lambda L: L.jinf_softmax_rows_f32(FAKE, 64, FAKE, 64, 0, 64, None, 1, 1.0, None),
     lambda L: L.jinf_embed_q4_0(FAKE, 128, FAKE, 10, 128, FAKE, 0, 1, None),
+    lambda L: L.jinf_matvec_q4_0(FAKE, FAKE, FAKE, 0, 128, None),
 ])
 def test_empty_work_is_ok_and_enqueues_nothing(call):
     assert call(jinf_amd.lib()) == _lib.JINF_HIP_OK
@@ -96,3 +100,5 @@ def test_drop_ins_are_noops_for_empty_sizes():
     L.jinf_cuda_residual_add(FAKE, FAKE, 0, None)
     L.jinf_cuda_dequantize_q4_0(FAKE, FAKE, 0, None)
     L.jinf_cuda_rope(FAKE, FAKE, 128, 0, 0, 5, 1e4, None)
+    L.jinf_cuda_dequant_matvec(FAKE, FAKE, FAKE, 0, 128, 2, None)
+    L.jinf_cuda_dequant_matvec(FAKE, FAKE, FAKE, 16, 128, 12, None)  # unsupported qtype: no-op
