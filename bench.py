@@ -218,7 +218,8 @@ def workload(name, torch, jinf, seed):
               build_matvec(torch, jinf, g, "gemv_gate", F, H, keep),
               build_matvec(torch, jinf, g, "gemv_up", F, H, keep),
               build_matvec(torch, jinf, g, "gemv_down", H, F, keep)]
-        cfg = {"workload": name, "shapes": "Llama-3-8B layer projections at batch 1 (decode): "
+        cfg = {"workload": name, "dtype": "f32 math, Q4_0 weights (fp16 scales), f32 x and y",
+               "shapes": "Llama-3-8B layer projections at batch 1 (decode): "
                "q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096, down 4096x14336, Q4_0 "
                "weights, fp32 x/y", "storage": "Q4_0 weights, f32 vectors",
                "baseline_configs": [], "note": "SURVEY 8(f) f1, next component"}
@@ -362,6 +363,9 @@ _KERNEL_KEYS = [("ew_vec_kernel<unsigned short, 1", "swiglu"),
                 ("rope_vec_kernel", "rope"),
                 ("softmax_vec_kernel", "masked_softmax"),
                 ("softmax_loop_kernel", "softmax_loop"),
+                ("matvec_q4_0_kernel<2, true>", "gemv_one_tile (q,k,v,o,gate,up)"),
+                ("matvec_q4_0_kernel<2, false>", "gemv_down"),
+                ("matvec_q4_0_any_kernel", "gemv_generic"),
                 ("copyBuffer", "copy_calibration")]
 
 
@@ -392,14 +396,14 @@ def main():
 
     if args.rocprof_summary:
         nb = {"rope": 10487808, "residual_rmsnorm": 67117056, "swiglu": 176160768,
-              "q4_0_gather": 43008000}
+              "q4_0_gather": 43008000, "gemv_down": 33103872}
         print(rocprof_summary(args.rocprof_summary, nb))
         return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build measures one GPU only; the kernels are "
-                          "row-independent and shard by rows with no exchange (see DESIGN.md)",
+                          "row-independent and shard by rows with no exchange",
                           "n_gpus_requested": max(args.gpus, world)}), flush=True)
         sys.exit(2)
 
@@ -502,7 +506,7 @@ def main():
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32 math, f16 storage",
+        "dtype": cfg.pop("dtype", "f32 math, f16 storage"),
         "data": "synthetic: seeded torch RNG on device (N(mu, sigma), sigma = std); "
                 "Q4_0 scales fp16(|N(0,0.02)|), nibbles uniform",
         "config": dict(cfg, step_bytes=step_bytes),
