@@ -172,18 +172,39 @@ def build_softmax(torch, jinf, g, n_seq, n_heads, max_len, keep):
                   lambda o, s, lc: o.softmax_rows(s, lc, n_heads, 1.0))
 
 
-def build_matvec(torch, jinf, g, name, rows, cols, keep):
-    """Q4_0 dequant-GEMV y = W x at batch 1 (fp32 x, y)."""
-    nbytes = rows * (cols // 32) * 18 + cols * 4 + rows * 4
+# GGUF block geometry (values, bytes) and where each format keeps its binary16
+# scales (byte offsets within the block).
+QGEOM = {2: (32, 18, (0,)), 8: (32, 34, (0,)), 12: (256, 144, (0, 2)), 14: (256, 210, (208,))}
+
+
+def quant_table(torch, qtype, rows, cols, g):
+    """Random weight rows of a GGUF block type: every byte uniform, then the
+    binary16 scales set to fp16(|N(0, 0.02)|)."""
+    if qtype == 2:
+        return q4_0_table(torch, rows, cols, g)
+    elems, nbytes, scale_offs = QGEOM[qtype]
+    nb = cols // elems
+    t = torch.randint(0, 256, (rows, nb, nbytes), generator=g, device="cuda",
+                      dtype=torch.int32).to(torch.uint8)
+    for off in scale_offs:
+        d = (torch.randn((rows, nb), generator=g, device="cuda") * 0.02).abs().to(torch.float16)
+        t[:, :, off:off + 2] = d.view(torch.uint8).view(rows, nb, 2)
+    return t.view(rows, nb * nbytes)
+
+
+def build_matvec(torch, jinf, g, name, rows, cols, keep, qtype=2):
+    """Dequant-GEMV y = W x at batch 1 (fp32 x, y), W in qtype blocks."""
+    elems, nbytes_blk, _ = QGEOM[qtype]
+    nbytes = rows * (cols // elems) * nbytes_blk + cols * 4 + rows * 4
     sets = []
     for _ in range(n_sets(nbytes)):
-        W = q4_0_table(torch, rows, cols, g)
+        W = quant_table(torch, qtype, rows, cols, g)
         x = torch.randn(cols, generator=g, device="cuda")
         y = torch.empty(rows, dtype=torch.float32, device="cuda")
         keep.append((W, x, y))
-        sets.append(lambda W=W, x=x, y=y: jinf.matvec_q4_0(W, x, y))
-    return Kernel(name, nbytes, rows, "output rows", sets, "matvec_q4_0_kernel",
-                  keep[-len(sets)][:2], lambda o, W, x: o.matvec_q4_0(W, x))
+        sets.append(lambda W=W, x=x, y=y: jinf.matvec(W, x, qtype, y))
+    return Kernel(name, nbytes, rows, "output rows", sets, f"matvec_kernel<{qtype}",
+                  keep[-len(sets)][:2], lambda o, W, x: o.matvec(qtype, W, x))
 
 
 def workload(name, torch, jinf, seed):
@@ -223,6 +244,23 @@ def workload(name, torch, jinf, seed):
                "q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096, down 4096x14336, Q4_0 "
                "weights, fp32 x/y", "storage": "Q4_0 weights, f32 vectors",
                "baseline_configs": [], "note": "SURVEY 8(f) f1, next component"}
+    elif name in ("llama3-8b-gemv-q4_k_m", "llama3-8b-gemv-q8_0"):
+        H, F, KV = 4096, 14336, 1024
+        if name.endswith("q8_0"):
+            qt = dict.fromkeys(("q", "k", "v", "o", "gate", "up", "down"), 8)
+            desc = "Q8_0 weights"
+        else:  # Q4_K_M: Q4_K, with Q6_K for attn_v and ffn_down
+            qt = dict(q=12, k=12, v=14, o=12, gate=12, up=12, down=14)
+            desc = "Q4_K weights, Q6_K for v and down (Q4_K_M)"
+        shapes = dict(q=(H, H), k=(KV, H), v=(KV, H), o=(H, H), gate=(F, H), up=(F, H),
+                      down=(H, F))
+        ks = [build_matvec(torch, jinf, g, "gemv_" + p, rows, cols, keep, qt[p])
+              for p, (rows, cols) in shapes.items()]
+        cfg = {"workload": name, "dtype": f"f32 math, {desc} (fp16 scales), f32 x and y",
+               "shapes": "Llama-3-8B layer projections at batch 1 (decode): "
+               "q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096, down 4096x14336, " + desc,
+               "storage": desc + ", f32 vectors", "baseline_configs": [],
+               "note": "SURVEY 8(f) f1, next component"}
     elif name in ("rope", "norm", "swiglu", "gather", "softmax"):
         b = {"rope": lambda: build_rope(torch, jinf, g, 512, 32, 8, 128,
                                         torch.arange(512, dtype=torch.int32, device="cuda"), keep),
@@ -363,9 +401,17 @@ _KERNEL_KEYS = [("ew_vec_kernel<unsigned short, 1", "swiglu"),
                 ("rope_vec_kernel", "rope"),
                 ("softmax_vec_kernel", "masked_softmax"),
                 ("softmax_loop_kernel", "softmax_loop"),
-                ("matvec_q4_0_kernel<2, true>", "gemv_one_tile (q,k,v,o,gate,up)"),
-                ("matvec_q4_0_kernel<2, false>", "gemv_down"),
-                ("matvec_q4_0_any_kernel", "gemv_generic"),
+                # the one-tile kernels serve q, k, v, o, gate, up; the multi-tile
+                # kernels only down (14336 columns) in the GEMV workloads
+                ("matvec_kernel<2, true>", "gemv_one_tile (q,k,v,o,gate,up)"),
+                ("matvec_kernel<8, true>", "gemv_one_tile (q,k,v,o,gate,up)"),
+                ("matvec_kernel<12, true>", "gemv_one_tile Q4_K (q,k,o,gate,up)"),
+                ("matvec_kernel<14, true>", "gemv_one_tile Q6_K (v)"),
+                ("matvec_kernel<2, false>", "gemv_down"),
+                ("matvec_kernel<8, false>", "gemv_down"),
+                ("matvec_kernel<12, false>", "gemv_down"),
+                ("matvec_kernel<14, false>", "gemv_down"),
+                ("matvec_any_kernel", "gemv_generic"),
                 ("copyBuffer", "copy_calibration")]
 
 

@@ -69,12 +69,32 @@ void jinf_cuda_residual_add(float* a, const float* b, int n, hipStream_t stream)
 void jinf_cuda_dequantize_q4_0(const void* data, float* output, int n_blocks,
                                hipStream_t stream);
 
+/* Dequantize n_blocks consecutive Q4_K super-blocks (144 bytes, 256 values:
+ * d, dmin, 12 packed 6-bit scale/min bytes in the reference's own packing,
+ * 128 bytes of nibbles) to fp32, bit-identical to the reference.
+ * Replaces jinf_cuda_dequantize_q4_K, cuda/dequant_kernels.cu:124-129. */
+void jinf_cuda_dequantize_q4_K(const void* data, float* output, int n_blocks,
+                               hipStream_t stream);
+
+/* Dequantize n_blocks consecutive Q8_0 blocks (34 bytes: d, 32 int8).
+ * Replaces jinf_cuda_dequantize_q8_0, cuda/dequant_kernels.cu:131-137. */
+void jinf_cuda_dequantize_q8_0(const void* data, float* output, int n_blocks,
+                               hipStream_t stream);
+
+/* Dequantize n_blocks consecutive Q6_K super-blocks (210 bytes: ql[128],
+ * qh[64], int8 scales[16], d) to fp32, bit-identical to the reference.
+ * Replaces jinf_cuda_dequantize_q6_K, cuda/dequant_kernels.cu:139-146. */
+void jinf_cuda_dequantize_q6_K(const void* data, float* output, int n_blocks,
+                               hipStream_t stream);
+
 /* y[row] = sum_j W[row, j] * x[j] for a [rows, cols] matrix stored as GGUF
- * Q4_0 blocks along the columns (cols % 32 == 0; jinf's interleaved nibble
- * order), fp32 x and y.  qtype 2 (Q4_0) is served; any other qtype prints one
- * stderr line and enqueues nothing.  W 2-byte aligned, x and y 4-byte aligned.
- * Replaces jinf_cuda_dequant_matvec, cuda/matmul_kernels.cu:198-225 (Q4_0
- * kernel :8-43). */
+ * blocks along the columns, fp32 x and y (4-byte aligned).  qtype 2 (Q4_0),
+ * 8 (Q8_0), 12 (Q4_K) and 14 (Q6_K) are served, as in the reference, with its
+ * element orders and dequantized weights; cols must be a multiple of the
+ * block size (32, or 256 for the K formats).  Any other qtype prints one
+ * stderr line and enqueues nothing.
+ * Replaces jinf_cuda_dequant_matvec, cuda/matmul_kernels.cu:198-225 (kernels
+ * :8-185). */
 void jinf_cuda_dequant_matvec(const void* weight, const float* input, float* output,
                               int rows, int cols, int qtype, hipStream_t stream);
 

@@ -111,11 +111,38 @@ int jinf_embed_q4_0(void* out, int ld_out, const void* table, int n_vocab,
                     int n_embd, const int32_t* ids, int n_ids, int out_type,
                     hipStream_t stream);
 
-/* Q4_0 dequant-GEMV, y = W x (W [rows, cols] in Q4_0 blocks, x/y fp32), with
- * a status return.  Same arithmetic as jinf_cuda_dequant_matvec (Q4_0).
- * Fast path: cols % 256 == 0, W and x 16-byte aligned. */
+/* GGUF block codes (values of jinf_qtype, reference include/jinf/quant.h:8-24)
+ * served by jinf_matvec, jinf_dequant_rows and jinf_cuda_dequant_matvec. */
+enum jinf_hip_qtype {
+    JINF_HIP_Q4_0 = 2,
+    JINF_HIP_Q8_0 = 8,
+    JINF_HIP_Q4_K = 12,
+    JINF_HIP_Q6_K = 14
+};
+
+/* Dequant-GEMV y = W x with a status return: W [rows, cols] stored as qtype
+ * blocks along the columns (any byte alignment), x and y fp32 (4-byte
+ * aligned); cols a multiple of the block size (32 or 256).  Same arithmetic as
+ * jinf_cuda_dequant_matvec.  Fast path: W and x 16-byte aligned, cols a
+ * multiple of 256 (2048 for Q6_K) and at most 28672.  Semantics of
+ * cuda/matmul_kernels.cu:8-185. */
+int jinf_matvec(const void* weight, int qtype, const float* x, float* y, int rows, int cols,
+                hipStream_t stream);
+
+/* jinf_matvec with qtype = JINF_HIP_Q4_0. */
 int jinf_matvec_q4_0(const void* weight, const float* x, float* y, int rows, int cols,
                      hipStream_t stream);
+
+/* Gather + dequant of table rows for any qtype above (the engine's embedding
+ * dispatch by table type, src/engine.cpp:311-334): output row i (ld_out
+ * elements apart) is table row ids[i] (row i when ids is NULL), n_embd values
+ * from n_embd / block_size blocks; an id outside [0, n_vocab) gives +0.0.
+ * Weights are bit-identical to the reference's dequantizers
+ * (cuda/dequant_kernels.cu:6-110); fp16 output is one RNE rounding of them.
+ * Q4_0 runs jinf_embed_q4_0. */
+int jinf_dequant_rows(void* out, int ld_out, const void* table, int qtype, int n_vocab,
+                      int n_embd, const int32_t* ids, int n_ids, int out_type,
+                      hipStream_t stream);
 
 #ifdef __cplusplus
 }

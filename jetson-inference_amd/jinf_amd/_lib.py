@@ -21,6 +21,9 @@ JINF_HIP_ERR_INVALID = 5
 F32 = 0
 F16 = 1
 
+# GGUF block codes (jinf_qtype values)
+Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
@@ -35,6 +38,9 @@ SIGNATURES = {
     "jinf_cuda_residual_add": (None, [_P, _P, _I, _P]),
     "jinf_cuda_dequantize_q4_0": (None, [_P, _P, _I, _P]),
     "jinf_cuda_dequant_matvec": (None, [_P, _P, _P, _I, _I, _I, _P]),
+    "jinf_cuda_dequantize_q4_K": (None, [_P, _P, _I, _P]),
+    "jinf_cuda_dequantize_q8_0": (None, [_P, _P, _I, _P]),
+    "jinf_cuda_dequantize_q6_K": (None, [_P, _P, _I, _P]),
     # extensions (include/jinf/kernels_ext.h)
     "jinf_hip_version": (ctypes.c_char_p, []),
     "jinf_rmsnorm_rows": (_I, [_P, _I, _P, _I, _P, _I, _I, _F, _I, _I, _P]),
@@ -45,6 +51,8 @@ SIGNATURES = {
     "jinf_softmax_rows_f32": (_I, [_P, _I, _P, _I, _I, _I, _P, _I, _F, _P]),
     "jinf_embed_q4_0": (_I, [_P, _I, _P, _I, _I, _P, _I, _I, _P]),
     "jinf_matvec_q4_0": (_I, [_P, _P, _P, _I, _I, _P]),
+    "jinf_matvec": (_I, [_P, _I, _P, _P, _I, _I, _P]),
+    "jinf_dequant_rows": (_I, [_P, _I, _P, _I, _I, _I, _P, _I, _I, _P]),
 }
 
 _lib = None

@@ -12,7 +12,7 @@ import ctypes
 
 import torch
 
-from ._lib import F16, F32, JINF_HIP_OK, lib
+from ._lib import F16, F32, JINF_HIP_OK, Q4_0, Q4_K, Q6_K, Q8_0, lib
 
 
 class JinfError(RuntimeError):
@@ -152,16 +152,41 @@ def embed_q4_0(table, ids, n_embd, out_dtype=torch.float16, out=None):
     return out
 
 
+_GEOM = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+
+
 def matvec_q4_0(weight, x, y=None):
     """y = W x: weight uint8 [rows, cols/32*18] (Q4_0 blocks), x fp32 [cols]."""
+    return matvec(weight, x, Q4_0, y)
+
+
+def matvec(weight, x, qtype, y=None):
+    """y = W x: weight uint8 [rows, cols/elems*bytes] of qtype blocks, x fp32 [cols]."""
+    if qtype not in _GEOM:
+        raise JinfError(f"unsupported qtype {qtype}")
+    elems, nbytes = _GEOM[qtype]
     rows = weight.shape[0]
     cols = x.shape[0]
-    if weight.shape[1] != cols // 32 * 18:
+    if weight.shape[1] != cols // elems * nbytes:
         raise JinfError("weight row bytes do not match cols")
     y = torch.empty(rows, dtype=torch.float32, device=x.device) if y is None else y
-    _check(lib().jinf_matvec_q4_0(_ptr(weight), _ptr(x), _ptr(y), rows, cols, _stream()),
-           "jinf_matvec_q4_0")
+    _check(lib().jinf_matvec(_ptr(weight), int(qtype), _ptr(x), _ptr(y), rows, cols, _stream()),
+           "jinf_matvec")
     return y
+
+
+def dequant_rows(table, qtype, n_embd, ids=None, out_dtype=torch.float32, out=None):
+    """Gather + dequantize rows of a qtype table (uint8 [n_vocab, row bytes])."""
+    n_vocab = table.shape[0]
+    n_ids = ids.shape[0] if ids is not None else n_vocab
+    if out is None:
+        out = torch.empty((n_ids, n_embd), dtype=out_dtype, device=table.device)
+    if ids is not None and ids.dtype != torch.int32:
+        raise JinfError("ids must be int32")
+    _check(lib().jinf_dequant_rows(_ptr(out), out.stride(0), _ptr(table), int(qtype), n_vocab,
+                                   n_embd, _ptr(ids), n_ids, _act(out), _stream()),
+           "jinf_dequant_rows")
+    return out
 
 
 # ---- drop-in entry points (reference signatures; fp32, one row) ----
@@ -203,4 +228,13 @@ def cuda_dequant_matvec(weight, x, y, rows, cols, qtype=2):
 def cuda_dequantize_q4_0(data, out, n_blocks, byte_offset=0):
     ptr = ctypes.c_void_p(data.data_ptr() + byte_offset)
     lib().jinf_cuda_dequantize_q4_0(ptr, _ptr(out), int(n_blocks), _stream())
+    return out
+
+
+def cuda_dequantize(qtype, data, out, n_blocks, byte_offset=0):
+    """The reference's per-row launchers jinf_cuda_dequantize_{q4_0,q8_0,q4_K,q6_K}."""
+    name = {Q4_0: "jinf_cuda_dequantize_q4_0", Q8_0: "jinf_cuda_dequantize_q8_0",
+            Q4_K: "jinf_cuda_dequantize_q4_K", Q6_K: "jinf_cuda_dequantize_q6_K"}[qtype]
+    ptr = ctypes.c_void_p(data.data_ptr() + byte_offset)
+    getattr(lib(), name)(ptr, _ptr(out), int(n_blocks), _stream())
     return out

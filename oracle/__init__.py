@@ -40,7 +40,13 @@ _SIG = {
     "jo_swiglu": (None, [_P, _P, _P, _L, _I]),
     "jo_softmax_rows": (None, [_P, _L, _P, _L, _I, _I, _P, _I, _F]),
     "jo_matvec_q4_0": (None, [_P, _P, _P, _P, _I, _I]),
+    "jo_qtype_geometry": (_I, [_I, ctypes.POINTER(_I)]),
+    "jo_dequant": (None, [_I, _P, _P, _I]),
+    "jo_matvec": (None, [_I, _P, _P, _P, _P, _I, _I]),
 }
+
+# qtype codes (include/jinf/quant.h:8-24)
+Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
 
 _lib = None
 _ref = None
@@ -72,6 +78,9 @@ def ref():
         h.jref_dequantize_q4_0.argtypes = [_P, _P, _I]
         h.jref_f16_to_f32.restype = None
         h.jref_f16_to_f32.argtypes = [_P, _P, ctypes.c_longlong]
+        for n in ("jref_dequantize_q4_K", "jref_dequantize_q8_0"):
+            getattr(h, n).restype = None
+            getattr(h, n).argtypes = [_P, _P, _I]
         _ref = h
     return _ref
 
@@ -241,4 +250,50 @@ def matvec_q4_0(W_u8, x):
     y = np.empty(rows, np.float32)
     a = np.empty(rows, np.float64)
     lib().jo_matvec_q4_0(_p(W), _p(x), _p(y), _p(a), rows, cols)
+    return y, a
+
+
+# ---- Q8_0 / Q4_K / Q6_K ----
+
+def qtype_geometry(qtype):
+    """(values per block, bytes per block) of a supported qtype, else (0, 0)."""
+    b = _I(0)
+    e = lib().jo_qtype_geometry(int(qtype), ctypes.byref(b))
+    return e, b.value
+
+
+def dequant(qtype, blocks_u8):
+    """Contiguous blocks of qtype (uint8) -> fp32 values."""
+    e, nbytes = qtype_geometry(qtype)
+    b = _c(np.asarray(blocks_u8, dtype=np.uint8)).reshape(-1)
+    nb = b.size // nbytes
+    out = np.empty(nb * e, np.float32)
+    lib().jo_dequant(int(qtype), _p(b), _p(out), nb)
+    return out
+
+
+def ref_dequant(qtype, blocks_u8):
+    """Same through the reference's compiled src/quant.cpp (Q4_K and Q8_0 only:
+    it has no CPU Q6_K routine)."""
+    e, nbytes = qtype_geometry(qtype)
+    b = _c(np.asarray(blocks_u8, dtype=np.uint8)).reshape(-1)
+    nb = b.size // nbytes
+    out = np.empty(nb * e, np.float32)
+    fn = {Q4_K: "jref_dequantize_q4_K", Q8_0: "jref_dequantize_q8_0",
+          Q4_0: "jref_dequantize_q4_0"}[qtype]
+    getattr(ref(), fn)(_p(b), _p(out), nb)
+    return out
+
+
+def matvec(qtype, W_u8, x):
+    """W uint8 [rows, cols/elems*bytes] of qtype, x fp32 [cols] -> (y fp32 [rows],
+    sum_j |w_j x_j| fp64 [rows])."""
+    e, nbytes = qtype_geometry(qtype)
+    W = _c(np.asarray(W_u8, dtype=np.uint8))
+    x = _c(np.asarray(x, dtype=np.float32))
+    rows, cols = W.shape[0], x.shape[0]
+    assert cols % e == 0 and W.shape[1] == cols // e * nbytes
+    y = np.empty(rows, np.float32)
+    a = np.empty(rows, np.float64)
+    lib().jo_matvec(int(qtype), _p(W), _p(x), _p(y), _p(a), rows, cols)
     return y, a

@@ -18,6 +18,8 @@
  *   SiLU * up              cuda/silu_kernel.cu:6-18
  *   softmax                cuda/softmax_kernel.cu:8-42, cuda/attention_kernel.cu:59-87
  *   Q4_0 dequant-GEMV      cuda/matmul_kernels.cu:8-43, 198-225
+ *   Q4_K / Q8_0 / Q6_K     src/quant.cpp:64-105, cuda/dequant_kernels.cu:25-110,
+ *   dequant and GEMV       cuda/matmul_kernels.cu:47-185
  * Build with -ffp-contract=off (no FMA contraction) and without fast-math.
  *
  * fp16 storage: every stored value is fl16(fl32(expression)) with
@@ -347,5 +349,129 @@ void jo_matvec_q4_0(const uint8_t* W, const float* x, float* y, double* abs_y, i
         }
         y[r] = (float)acc;
         if (abs_y) abs_y[r] = aabs;
+    }
+}
+
+/* ---- Q4_K, Q8_0, Q6_K (block layouts include/jinf/quant.h:38-68) ---- */
+
+/* The reference's own 6-bit unpacking of the 12 scale bytes into 8 scales and
+ * 8 mins (src/quant.cpp:70-75, cuda/matmul_kernels.cu:65-70): sub-blocks 0-3
+ * take the low 6 bits of bytes 0-3 (scales) and 4-7 (mins); sub-blocks 4-7
+ * take a nibble of bytes 8-11 as their HIGH four bits and the top two bits of
+ * bytes 0-3 / 4-7 as their low two. */
+static void q4_K_scales(const uint8_t* s, int sc[8], int mn[8]) {
+    for (int i = 0; i < 4; ++i) {
+        sc[i] = s[i] & 0x3F;
+        mn[i] = s[i + 4] & 0x3F;
+        sc[i + 4] = ((s[i + 8] & 0x0F) << 2) | (s[i] >> 6);
+        mn[i + 4] = ((s[i + 8] >> 4) << 2) | (s[i + 4] >> 6);
+    }
+}
+
+/* One 144-byte Q4_K super-block (256 values): d, dmin (binary16), scales[12],
+ * qs[128]; element 2i of sub-block sb is the low nibble of qs[16 sb + i], 2i+1
+ * the high nibble.  w = sub_d * q - sub_min with sub_d = d * sc and
+ * sub_min = dmin * mn; both products and sub_d * q are exact in fp32, so the
+ * subtraction is the only rounding (with or without FMA contraction). */
+static void q4_K_block(const uint8_t* blk, float* out) {
+    const float d = jo_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+    const float dmin = jo_f16_to_f32((uint16_t)(blk[2] | (blk[3] << 8)));
+    int sc[8], mn[8];
+    q4_K_scales(blk + 4, sc, mn);
+    for (int sb = 0; sb < 8; ++sb) {
+        const float sub_d = d * (float)sc[sb];
+        const float sub_min = dmin * (float)mn[sb];
+        for (int i = 0; i < 16; ++i) {
+            const uint8_t b = blk[16 + 16 * sb + i];
+            out[32 * sb + 2 * i] = sub_d * (float)(b & 0x0F) - sub_min;
+            out[32 * sb + 2 * i + 1] = sub_d * (float)(b >> 4) - sub_min;
+        }
+    }
+}
+
+/* One 34-byte Q8_0 block: d (binary16), 32 int8; w = q * d, exact. */
+static void q8_0_block(const uint8_t* blk, float* out) {
+    const float d = jo_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+    for (int i = 0; i < 32; ++i) out[i] = (float)(int8_t)blk[2 + i] * d;
+}
+
+/* One 210-byte Q6_K super-block (cuda/dequant_kernels.cu:82-110): ql[128],
+ * qh[64], int8 scales[16], then d (binary16) at byte 208.  Element e:
+ * low four bits from ql[e/2] (low nibble for even e), high two bits from
+ * qh[e/4] at bit 2*(e%4); w = (d * scales[e/16]) * (q6 - 32).  d * scale has
+ * at most 18 significant bits and |q6 - 32| <= 32, so both products are exact. */
+static void q6_K_block(const uint8_t* blk, float* out) {
+    const float d = jo_f16_to_f32((uint16_t)(blk[208] | (blk[209] << 8)));
+    for (int e = 0; e < 256; ++e) {
+        const uint8_t l = blk[e / 2];
+        const int lo = (e & 1) ? (l >> 4) : (l & 0x0F);
+        const int hi = (blk[128 + e / 4] >> (2 * (e % 4))) & 0x03;
+        const int q6 = lo | (hi << 4);
+        out[e] = d * (float)(int8_t)blk[192 + e / 16] * (float)(q6 - 32);
+    }
+}
+
+/* Block geometry of a supported qtype (include/jinf/quant.h:8-24 codes):
+ * returns values per block and sets *bytes, or 0 for an unsupported type. */
+int jo_qtype_geometry(int qtype, int* bytes) {
+    switch (qtype) {
+        case 2: *bytes = 18; return 32;    /* Q4_0 */
+        case 8: *bytes = 34; return 32;    /* Q8_0 */
+        case 12: *bytes = 144; return 256; /* Q4_K */
+        case 14: *bytes = 210; return 256; /* Q6_K */
+        default: *bytes = 0; return 0;
+    }
+}
+
+static void dequant_block(int qtype, const uint8_t* blk, float* out) {
+    switch (qtype) {
+        case 2: q4_0_block(blk, JO_F32, out, 0); break;
+        case 8: q8_0_block(blk, out); break;
+        case 12: q4_K_block(blk, out); break;
+        case 14: q6_K_block(blk, out); break;
+        default: break;
+    }
+}
+
+/* n_blocks contiguous blocks of qtype to fp32 (the reference's
+ * jinf_dequantize_q4_K / _q8_0 and the GPU launchers
+ * jinf_cuda_dequantize_q4_K / _q8_0 / _q6_K). */
+void jo_dequant(int qtype, const uint8_t* blocks, float* out, int n_blocks) {
+    int bytes;
+    const int elems = jo_qtype_geometry(qtype, &bytes);
+    if (!elems) return;
+    for (int b = 0; b < n_blocks; ++b)
+        dequant_block(qtype, blocks + (int64_t)bytes * b, out + (int64_t)elems * b);
+}
+
+/* y[r] = sum_j w[r, j] * x[j] for any supported qtype (cuda/matmul_kernels.cu
+ * :8-185): each row is dequantized exactly as above, the products are formed
+ * and summed in fp64 in column order and rounded once; abs_y (optional)
+ * receives sum_j |w_j x_j|. */
+void jo_matvec(int qtype, const uint8_t* W, const float* x, float* y, double* abs_y, int rows,
+               int cols) {
+    int bytes;
+    const int elems = jo_qtype_geometry(qtype, &bytes);
+    if (!elems || cols % elems) return;
+    const int nb = cols / elems;
+    const int64_t row_bytes = (int64_t)nb * bytes;
+#pragma omp parallel num_threads(jo_threads)
+    {
+        float wblk[256];
+#pragma omp for schedule(static)
+        for (int r = 0; r < rows; ++r) {
+            double acc = 0.0, aabs = 0.0;
+            const uint8_t* row = W + (int64_t)r * row_bytes;
+            for (int b = 0; b < nb; ++b) {
+                dequant_block(qtype, row + (int64_t)bytes * b, wblk);
+                for (int j = 0; j < elems; ++j) {
+                    const double t = (double)wblk[j] * (double)x[(int64_t)elems * b + j];
+                    acc += t;
+                    aabs += fabs(t);
+                }
+            }
+            y[r] = (float)acc;
+            if (abs_y) abs_y[r] = aabs;
+        }
     }
 }

@@ -12,3 +12,11 @@ extern "C" void jref_dequantize_q4_0(const void* blocks, float* out, int n_block
 extern "C" void jref_f16_to_f32(const void* halfs, float* out, long long n) {
     jinf_dequantize(halfs, JINF_TYPE_F16, out, (int64_t)n);
 }
+
+extern "C" void jref_dequantize_q4_K(const void* blocks, float* out, int n_blocks) {
+    jinf_dequantize_q4_K(static_cast<const jinf_block_q4_K*>(blocks), out, n_blocks);
+}
+
+extern "C" void jref_dequantize_q8_0(const void* blocks, float* out, int n_blocks) {
+    jinf_dequantize_q8_0(static_cast<const jinf_block_q8_0*>(blocks), out, n_blocks);
+}

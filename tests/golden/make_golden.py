@@ -4,12 +4,14 @@
                  own CPU dequantizer (src/quant.cpp:49-60, compiled where it
                  lies by `make -C oracle ref`); plus the reference's fp16->fp32
                  conversion of every binary16 bit pattern.
+  kquants_ref.npz  Q4_K and Q8_0 blocks and the reference's own CPU
+                 dequantization of them (src/quant.cpp:64-105).
   kernels.npz    seeded inputs and oracle outputs for each kernel at small
                  shapes (the oracle is pinned by tests/test_oracle_*.py); GPU
                  tests compare against these committed values.
 
 Run from the repository root after `make -C oracle` (with the reference tree
-present for q4_0_ref.npz):  python tests/golden/make_golden.py
+present for the *_ref.npz files):  python tests/golden/make_golden.py [q4_0 kquants kernels]
 """
 import os
 import sys
@@ -52,6 +54,27 @@ def q4_0_fixture():
     np.savez_compressed(os.path.join(HERE, "q4_0_ref.npz"), blocks=blocks, out=out,
                         f16_bits=all_h.view(np.uint16), f16_to_f32=f16_ref)
     print("q4_0_ref.npz:", blocks.size // 18, "blocks")
+
+
+def kquants_fixture():
+    """Q4_K and Q8_0 blocks and the reference's own CPU dequantization of them
+    (src/quant.cpp:64-105 via oracle/_ref)."""
+    if not oracle.ref_available():
+        raise SystemExit("oracle/_ref/libjinf_ref.so missing: run `make -C oracle ref` first")
+    r = tu.rng(41)
+    fx = {}
+    for qtype, key in ((oracle.Q4_K, "q4_K"), (oracle.Q8_0, "q8_0")):
+        e, nbytes = oracle.qtype_geometry(qtype)
+        rand = tu.quant_table(r, qtype, 1, e * 96, 0.05).reshape(-1, nbytes)
+        special = np.repeat(rand[:len(SPECIAL_D)], 1, axis=0).copy()
+        special[:, 0:2] = np.array(SPECIAL_D, np.uint16).view(np.uint8).reshape(-1, 2)
+        if qtype == oracle.Q4_K:  # dmin through the same special values, reversed
+            special[:, 2:4] = np.array(SPECIAL_D[::-1], np.uint16).view(np.uint8).reshape(-1, 2)
+        blocks = np.concatenate([rand, special]).reshape(-1)
+        fx[key + "_blocks"] = blocks
+        fx[key + "_out"] = oracle.ref_dequant(qtype, blocks)
+    np.savez_compressed(os.path.join(HERE, "kquants_ref.npz"), **fx)
+    print("kquants_ref.npz:", {k: v.shape for k, v in fx.items()})
 
 
 def kernels_fixture():
@@ -100,5 +123,7 @@ def kernels_fixture():
 
 
 if __name__ == "__main__":
-    q4_0_fixture()
-    kernels_fixture()
+    # optional arguments pick fixtures by name (q4_0, kquants, kernels); default all
+    makers = {"q4_0": q4_0_fixture, "kquants": kquants_fixture, "kernels": kernels_fixture}
+    for name in sys.argv[1:] or list(makers):
+        makers[name]()

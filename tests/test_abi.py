@@ -37,7 +37,7 @@ def test_headers_include_no_gpu_runtime_header():
 
 def test_every_declared_symbol_is_exported_with_declared_arity():
     decl = declared()
-    assert len(decl) == 16
+    assert len(decl) == 21
     lib = jinf_amd.lib()
     for name, n in decl.items():
         assert hasattr(lib, name), name
@@ -75,6 +75,13 @@ FAKE = P(0x1000)  # never dereferenced: every call below is rejected on the host
     lambda L: L.jinf_matvec_q4_0(FAKE, FAKE, FAKE, 16, 100, None),
     lambda L: L.jinf_matvec_q4_0(FAKE, FAKE, FAKE, -1, 128, None),
     lambda L: L.jinf_matvec_q4_0(None, FAKE, FAKE, 16, 128, None),
+    lambda L: L.jinf_matvec(FAKE, 3, FAKE, FAKE, 16, 128, None),     # Q4_1: not served
+    lambda L: L.jinf_matvec(FAKE, 12, FAKE, FAKE, 16, 128, None),    # Q4_K needs cols % 256
+    lambda L: L.jinf_matvec(FAKE, 14, FAKE, FAKE, 16, 4097, None),
+    lambda L: L.jinf_dequant_rows(FAKE, 256, FAKE, 3, 10, 256, FAKE, 4, 0, None),
+    lambda L: L.jinf_dequant_rows(FAKE, 128, FAKE, 12, 10, 128, FAKE, 4, 0, None),
+    lambda L: L.jinf_dequant_rows(FAKE, 100, FAKE, 8, 10, 128, FAKE, 4, 0, None),
+    lambda L: L.jinf_dequant_rows(FAKE, 256, FAKE, 14, 10, 256, None, 11, 0, None),
 ])
 def test_invalid_arguments_rejected_on_host(call):
     assert call(jinf_amd.lib()) == _lib.JINF_HIP_ERR_INVALID
@@ -87,6 +94,8 @@ def test_invalid_arguments_rejected_on_host(call):
     lambda L: L.jinf_softmax_rows_f32(FAKE, 64, FAKE, 64, 0, 64, None, 1, 1.0, None),
     lambda L: L.jinf_embed_q4_0(FAKE, 128, FAKE, 10, 128, FAKE, 0, 1, None),
     lambda L: L.jinf_matvec_q4_0(FAKE, FAKE, FAKE, 0, 128, None),
+    lambda L: L.jinf_matvec(FAKE, 14, FAKE, FAKE, 16, 0, None),
+    lambda L: L.jinf_dequant_rows(FAKE, 256, FAKE, 12, 10, 256, FAKE, 0, 0, None),
 ])
 def test_empty_work_is_ok_and_enqueues_nothing(call):
     assert call(jinf_amd.lib()) == _lib.JINF_HIP_OK
@@ -101,4 +110,7 @@ def test_drop_ins_are_noops_for_empty_sizes():
     L.jinf_cuda_dequantize_q4_0(FAKE, FAKE, 0, None)
     L.jinf_cuda_rope(FAKE, FAKE, 128, 0, 0, 5, 1e4, None)
     L.jinf_cuda_dequant_matvec(FAKE, FAKE, FAKE, 0, 128, 2, None)
-    L.jinf_cuda_dequant_matvec(FAKE, FAKE, FAKE, 16, 128, 12, None)  # unsupported qtype: no-op
+    L.jinf_cuda_dequant_matvec(FAKE, FAKE, FAKE, 16, 128, 3, None)  # unsupported qtype: no-op
+    L.jinf_cuda_dequantize_q4_K(FAKE, FAKE, 0, None)
+    L.jinf_cuda_dequantize_q8_0(FAKE, FAKE, -1, None)
+    L.jinf_cuda_dequantize_q6_K(FAKE, FAKE, 0, None)

@@ -1,9 +1,14 @@
-"""GPU parity: Q4_0 dequant-GEMV (jinf_cuda_dequant_matvec / jinf_matvec_q4_0)
-against the oracle's fp64 dot product of the exactly dequantized matrix.
+"""GPU parity: dequant-GEMV (jinf_cuda_dequant_matvec / jinf_matvec) and row
+dequant (jinf_cuda_dequantize_* / jinf_dequant_rows) for Q4_0, Q8_0, Q4_K and
+Q6_K, against the oracle (fp64 dot product of the exactly dequantized matrix).
 
-Bar: |y - y_oracle| <= 1e-5 * sum_j |w_j x_j| per row: the dot product's own
-fp32 rounding scale (a relative bound on y itself is meaningless where the
-terms cancel)."""
+Bars:
+- GEMV: |y - y_oracle| <= 1e-5 * sum_j |w_j x_j| per row, the dot product's own
+  fp32 rounding scale (a relative bound on y itself is meaningless where the
+  terms cancel); a one-hot x reproduces a dequantized column bit for bit
+  (with -0.0 read as +0.0, as the reference's +0.0f-initialised sum gives);
+- dequant: bit-exact (fp32), and one RNE rounding of the exact weight (fp16).
+"""
 import ctypes
 
 import numpy as np
@@ -18,6 +23,9 @@ from gpu_util import host, say
 
 pytestmark = pytest.mark.gpu
 
+QTYPES = [oracle.Q4_0, oracle.Q8_0, oracle.Q4_K, oracle.Q6_K]
+NAMES = {oracle.Q4_0: "Q4_0", oracle.Q8_0: "Q8_0", oracle.Q4_K: "Q4_K", oracle.Q6_K: "Q6_K"}
+
 
 def check(y, ref, a, what):
     err = np.abs(y.astype(np.float64) - ref.astype(np.float64))
@@ -26,31 +34,61 @@ def check(y, ref, a, what):
     assert worst <= 1e-5, what
 
 
-@pytest.mark.parametrize("rows,cols", [(4096, 4096), (1024, 4096), (14336, 4096),
-                                       (4096, 14336), (20000, 4096), (7, 128), (1, 64),
-                                       (3, 2048), (515, 8192), (1024, 28672), (33, 32768)])
-def test_llama_shapes(dev, rows, cols):
-    say(f"matvec rows={rows} cols={cols}")
+def _oracle(qtype, W, x):
+    oracle.set_threads(8)
+    try:
+        return oracle.matvec(qtype, W, x)
+    finally:
+        oracle.set_threads(1)
+
+
+# Llama-3-8B projections (q/o, k/v, gate/up, down), a partial tile, the 70B
+# down projection width (7 tiles), a width past the tiled kernel (generic),
+# and odd row counts.
+SHAPES = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (7, 2048),
+          (515, 8192), (1024, 28672), (33, 32768)]
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_llama_shapes(dev, qtype, rows, cols):
+    say(f"{NAMES[qtype]} matvec rows={rows} cols={cols}")
+    r = tu.rng(rows + cols + qtype)
+    W = tu.quant_table(r, qtype, rows, cols)
+    x = tu.normal(r, (cols,), 0.0, 1.0, np.float32)
+    ref, a = _oracle(qtype, W, x)
+    y = host(jinf_amd.matvec(to_dev(W), to_dev(x), qtype))
+    check(y, ref, a, f"{NAMES[qtype]} {rows}x{cols}")
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (20000, 4096), (7, 128), (1, 64)])
+def test_q4_0_entry_point(dev, rows, cols):
+    say(f"jinf_matvec_q4_0 rows={rows} cols={cols}")
     r = tu.rng(rows + cols)
     W = tu.q4_0_table(r, rows, cols)
     x = tu.normal(r, (cols,), 0.0, 1.0, np.float32)
-    oracle.set_threads(8)
-    ref, a = oracle.matvec_q4_0(W, x)
-    oracle.set_threads(1)
+    ref, a = _oracle(oracle.Q4_0, W, x)
     y = host(jinf_amd.matvec_q4_0(to_dev(W), to_dev(x)))
     check(y, ref, a, f"{rows}x{cols}")
 
 
-@pytest.mark.parametrize("rows,cols,w_off,x_off", [(33, 96, 0, 0), (50, 32 * 5, 0, 0),
-                                                   (40, 4096, 2, 0), (40, 4096, 0, 1),
-                                                   (17, 4160, 0, 0)])
-def test_generic_path_and_drop_in(dev, rows, cols, w_off, x_off):
-    say(f"drop-in matvec rows={rows} cols={cols} W+{w_off}B x+{x_off} floats")
-    r = tu.rng(cols + w_off)
-    W = tu.q4_0_table(r, rows, cols)
+# (qtype, rows, cols, W byte offset, x float offset): unaligned pointers and
+# widths off the fast path's granule take the generic kernel.
+GENERIC = [(oracle.Q4_0, 33, 96, 0, 0), (oracle.Q4_0, 40, 4096, 2, 0), (oracle.Q4_0, 40, 4096, 0, 1),
+           (oracle.Q4_0, 17, 4160, 0, 0), (oracle.Q4_0, 9, 256, 1, 0),
+           (oracle.Q8_0, 50, 160, 0, 0), (oracle.Q8_0, 40, 4096, 2, 0), (oracle.Q8_0, 40, 4096, 0, 3),
+           (oracle.Q4_K, 21, 768, 4, 0), (oracle.Q4_K, 40, 4096, 0, 1), (oracle.Q4_K, 3, 256, 0, 0),
+           (oracle.Q6_K, 19, 1280, 0, 0), (oracle.Q6_K, 40, 4096, 2, 0), (oracle.Q6_K, 8, 2048, 0, 2)]
+
+
+@pytest.mark.parametrize("qtype,rows,cols,w_off,x_off", GENERIC)
+def test_generic_path_and_drop_in(dev, qtype, rows, cols, w_off, x_off):
+    say(f"drop-in {NAMES[qtype]} matvec rows={rows} cols={cols} W+{w_off}B x+{x_off} floats")
+    r = tu.rng(cols + w_off + qtype)
+    W = tu.quant_table(r, qtype, rows, cols)
     x = tu.normal(r, (cols,), 0.0, 1.0, np.float32)
-    ref, a = oracle.matvec_q4_0(W, x)
-    wraw = np.zeros(W.size + 8, np.uint8)
+    ref, a = _oracle(qtype, W, x)
+    wraw = np.zeros(W.size + 16, np.uint8)
     wraw[w_off:w_off + W.size] = W.reshape(-1)
     xraw = np.zeros(cols + 4, np.float32)
     xraw[x_off:x_off + cols] = x
@@ -58,30 +96,82 @@ def test_generic_path_and_drop_in(dev, rows, cols, w_off, x_off):
     y = torch.full((rows + 1,), -7.0, dtype=torch.float32, device=dev)
     jinf_amd.lib().jinf_cuda_dequant_matvec(
         ctypes.c_void_p(wd.data_ptr() + w_off), ctypes.c_void_p(xd.data_ptr() + 4 * x_off),
-        ctypes.c_void_p(y.data_ptr()), rows, cols, 2,
+        ctypes.c_void_p(y.data_ptr()), rows, cols, qtype,
         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     yh = host(y)
     check(yh[:rows], ref, a, "drop-in")
     assert yh[rows] == -7.0
 
 
-def test_one_hot_columns_exact(dev):
-    say("one-hot x reproduces dequantized columns bit for bit")
-    r = tu.rng(5)
-    rows, cols = 256, 4096
-    W = tu.q4_0_table(r, rows, cols)
-    Wf = oracle.dequant_q4_0(W).reshape(rows, cols)
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("cols", [4096, 14336])
+def test_one_hot_columns_exact(dev, qtype, cols):
+    say(f"{NAMES[qtype]} one-hot x reproduces dequantized columns bit for bit (cols={cols})")
+    r = tu.rng(5 + qtype)
+    rows = 256
+    W = tu.quant_table(r, qtype, rows, cols)
+    Wf = oracle.dequant(qtype, W).reshape(rows, cols)
     wd = to_dev(W)
-    for j in (0, 1, 30, 31, 32, 2047, 4095):
+    for j in (0, 1, 2, 3, 15, 16, 30, 31, 32, 255, 256, 2047, 4095, cols - 1):
         x = np.zeros(cols, np.float32)
         x[j] = 1.0
-        y = host(jinf_amd.matvec_q4_0(wd, to_dev(x)))
-        assert tu.bits_equal(y, Wf[:, j]), j
+        y = host(jinf_amd.matvec(wd, to_dev(x), qtype))
+        # + 0.0: a -0.0 weight gives +0.0, as in the reference, whose sum
+        # starts at +0.0f (cuda/matmul_kernels.cu:21, 58, 115, 147)
+        assert tu.bits_equal(y, Wf[:, j] + np.float32(0.0)), (NAMES[qtype], j)
 
 
 def test_unsupported_qtype_leaves_output(dev):
     y = torch.full((16,), 3.0, dtype=torch.float32, device=dev)
-    w = torch.zeros(16 * 144 // 1, dtype=torch.uint8, device=dev)
+    w = torch.zeros(16 * 20, dtype=torch.uint8, device=dev)
     x = torch.ones(256, dtype=torch.float32, device=dev)
-    jinf_amd.cuda_dequant_matvec(w, x, y, 16, 256, qtype=12)
+    jinf_amd.cuda_dequant_matvec(w, x, y, 16, 256, qtype=3)  # Q4_1: not served
     assert np.all(host(y) == 3.0)
+
+
+# ---- row dequant ----
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("n_blocks,off", [(16, 0), (56, 0), (3, 2), (1, 1)])
+def test_dequantize_drop_ins_bit_exact(dev, qtype, n_blocks, off):
+    say(f"jinf_cuda_dequantize {NAMES[qtype]} n_blocks={n_blocks} byte offset {off}")
+    e, nbytes = oracle.qtype_geometry(qtype)
+    r = tu.rng(n_blocks * 7 + qtype)
+    blocks = tu.quant_table(r, qtype, 1, e * n_blocks, 0.05).reshape(-1)
+    raw = np.zeros(blocks.size + 16, np.uint8)
+    raw[off:off + blocks.size] = blocks
+    out = torch.full((e * n_blocks + 1,), -5.0, dtype=torch.float32, device=dev)
+    jinf_amd.cuda_dequantize(qtype, to_dev(raw), out, n_blocks, byte_offset=off)
+    o = host(out)
+    assert tu.bits_equal(o[:-1], oracle.dequant(qtype, blocks))
+    assert o[-1] == -5.0
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16], ids=["f32", "f16"])
+def test_dequant_rows_gather(dev, qtype, out_dtype):
+    say(f"jinf_dequant_rows {NAMES[qtype]} -> {out_dtype}")
+    e, nbytes = oracle.qtype_geometry(qtype)
+    n_vocab, n_embd = 300, 4096
+    r = tu.rng(11 + qtype)
+    table = tu.quant_table(r, qtype, n_vocab, n_embd, 0.05)
+    ids = np.array([0, 299, 17, 17, -1, 300, 5, 123456, 42], np.int32)
+    out = host(jinf_amd.dequant_rows(to_dev(table), qtype, n_embd, to_dev(ids), out_dtype))
+    full = oracle.dequant(qtype, table).reshape(n_vocab, n_embd)
+    for i, t in enumerate(ids):
+        want = full[t] if 0 <= t < n_vocab else np.zeros(n_embd, np.float32)
+        if out_dtype == torch.float16:
+            want = oracle.f32_to_f16(want)
+        assert tu.bits_equal(out[i], want), (NAMES[qtype], i, int(t))
+
+
+def test_dequant_rows_strided_unaligned_output(dev):
+    """ld_out not a multiple of 4 floats: the scalar-store variant."""
+    say("jinf_dequant_rows Q6_K strided fp32 output, ld = 4096 + 3")
+    r = tu.rng(3)
+    table = tu.quant_table(r, oracle.Q6_K, 8, 4096, 0.05)
+    out = torch.full((8, 4099), 9.0, dtype=torch.float32, device=dev)
+    jinf_amd.dequant_rows(to_dev(table), oracle.Q6_K, 4096, None, torch.float32, out=out[:, :4096])
+    o = host(out)
+    assert tu.bits_equal(o[:, :4096], oracle.dequant(oracle.Q6_K, table).reshape(8, 4096))
+    assert np.all(o[:, 4096:] == 9.0)

@@ -28,6 +28,28 @@ def q4_0_table(r, n_rows, n_embd, scale_sigma=0.02):
     return blk.reshape(n_rows, nb * Q4_BLOCK)
 
 
+def quant_table(r, qtype, n_rows, n_cols, scale_sigma=0.01):
+    """Random weight rows of a GGUF block type (qtype codes 2, 8, 12, 14):
+    binary16 scales fp16(|N(0, scale_sigma)|), every other byte uniform (Q6_K
+    int8 sub-block scales included, so negative scales occur)."""
+    if qtype == 2:
+        return q4_0_table(r, n_rows, n_cols, scale_sigma)
+    elems, nbytes = {8: (32, 34), 12: (256, 144), 14: (256, 210)}[qtype]
+    nb = n_cols // elems
+    blk = r.integers(0, 256, size=(n_rows, nb, nbytes), dtype=np.uint8)
+    d = np.abs(r.normal(0.0, scale_sigma, size=(n_rows, nb))).astype(np.float16)
+    dv = d.view(np.uint8).reshape(n_rows, nb, 2)
+    if qtype == 8:
+        blk[:, :, 0:2] = dv
+    elif qtype == 12:
+        blk[:, :, 0:2] = dv
+        dmin = np.abs(r.normal(0.0, scale_sigma, size=(n_rows, nb))).astype(np.float16)
+        blk[:, :, 2:4] = dmin.view(np.uint8).reshape(n_rows, nb, 2)
+    else:
+        blk[:, :, 208:210] = dv
+    return blk.reshape(n_rows, nb * nbytes)
+
+
 def q4_0_blocks(d_bits, qs):
     """Build blocks from fp16 scale bit patterns [n] and nibble bytes [n, 16]."""
     d_bits = np.asarray(d_bits, dtype=np.uint16)
