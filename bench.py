@@ -172,6 +172,33 @@ def build_softmax(torch, jinf, g, n_seq, n_heads, max_len, keep):
                   lambda o, s, lc: o.softmax_rows(s, lc, n_heads, 1.0))
 
 
+def build_attention(torch, jinf, g, name, n_seq, max_ctx, nh, nkv, hd, lens, kv_dtype, keep):
+    """GQA decode attention over an n_seq-sequence KV cache.  Algorithmic bytes:
+    every live K and V row of every kv head read once, q read, out written."""
+    es = 2 if kv_dtype == torch.float16 else 4
+    live = int(lens.sum().item())
+    nbytes = 2 * live * nkv * hd * es + 2 * n_seq * nh * hd * 4 + n_seq * 4
+    foot = 2 * n_seq * max_ctx * nkv * hd * es
+    n_past = int(lens[0].item())  # the drop-in takes the length on the host
+    sets = []
+    for _ in range(max(2, n_sets(foot))):
+        k = torch.randn((n_seq, max_ctx, nkv * hd), generator=g, device="cuda").to(kv_dtype)
+        v = torch.randn((n_seq, max_ctx, nkv * hd), generator=g, device="cuda").to(kv_dtype)
+        q = torch.randn((n_seq, nh * hd), generator=g, device="cuda") * 2.0
+        o = torch.empty((n_seq, nh * hd), dtype=torch.float32, device="cuda")
+        lc = lens.clone()
+        keep.append((q, k, v, lc, o))
+        if n_seq == 1 and kv_dtype == torch.float32:  # the reference's drop-in
+            sets.append(lambda q=q, k=k, v=v, o=o: jinf.cuda_attention(
+                o, q, k, v, hd, nh, nkv, n_past, max_ctx))
+        else:
+            sets.append(lambda q=q, k=k, v=v, lc=lc, o=o: jinf.attention_decode(
+                q, k, v, lc, nh, nkv, out=o))
+    return Kernel(name, nbytes, n_seq, "sequences", sets, "attn_decode_kernel",
+                  keep[-len(sets)][:4],
+                  lambda o, q, k, v, lc: o.attention(q, k, v, lc, nh, nkv, hd))
+
+
 # GGUF block geometry (values, bytes) and where each format keeps its binary16
 # scales (byte offsets within the block).
 QGEOM = {2: (32, 18, (0,)), 8: (32, 34, (0,)), 12: (256, 144, (0, 2)), 14: (256, 210, (208,))}
@@ -261,6 +288,24 @@ def workload(name, torch, jinf, seed):
                "q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096, down 4096x14336, " + desc,
                "storage": desc + ", f32 vectors", "baseline_configs": [],
                "note": "SURVEY 8(f) f1, next component"}
+    elif name == "llama3-70b-attention":
+        pos = torch.randint(0, 8192, (64,), generator=g, device="cuda", dtype=torch.int32)
+        ks = [build_attention(torch, jinf, g, "gqa_attention", 64, 8192, 64, 8, 128, pos + 1,
+                              torch.float16, keep)]
+        cfg = {"workload": name, "dtype": "f32 math, f16 KV cache, f32 q and out",
+               "shapes": "Llama-3-70B decode attention, 64 sequences: 64/8 heads x 128, "
+               "KV cache [64, 8192, 8 x 128] fp16, len = pos + 1, pos ~ U[0, 8192)",
+               "storage": "f16 KV cache", "baseline_configs": [5],
+               "note": "SURVEY 8(f) f2, next component (config 5's sequences and lengths)"}
+    elif name == "llama3-8b-attention-b1":
+        lens = torch.full((1,), 4096, dtype=torch.int32, device="cuda")
+        ks = [build_attention(torch, jinf, g, "gqa_attention_b1", 1, 4096, 32, 8, 128, lens,
+                              torch.float32, keep)]
+        cfg = {"workload": name, "dtype": "f32",
+               "shapes": "Llama-3-8B decode attention through the reference's drop-in "
+               "jinf_cuda_attention: one sequence, 32/8 heads x 128, fp32 cache, n_past 4096",
+               "storage": "f32 KV cache", "baseline_configs": [],
+               "note": "SURVEY 8(f) f2, batch 1"}
     elif name in ("rope", "norm", "swiglu", "gather", "softmax"):
         b = {"rope": lambda: build_rope(torch, jinf, g, 512, 32, 8, 128,
                                         torch.arange(512, dtype=torch.int32, device="cuda"), keep),
@@ -412,6 +457,8 @@ _KERNEL_KEYS = [("ew_vec_kernel<unsigned short, 1", "swiglu"),
                 ("matvec_kernel<12, false>", "gemv_down"),
                 ("matvec_kernel<14, false>", "gemv_down"),
                 ("matvec_any_kernel", "gemv_generic"),
+                ("attn_decode_kernel", "gqa_attention"),
+                ("attn_decode_any_kernel", "gqa_attention_generic"),
                 ("copyBuffer", "copy_calibration")]
 
 

@@ -98,6 +98,20 @@ void jinf_cuda_dequantize_q6_K(const void* data, float* output, int n_blocks,
 void jinf_cuda_dequant_matvec(const void* weight, const float* input, float* output,
                               int rows, int cols, int qtype, hipStream_t stream);
 
+/* GQA decode attention for one query token: for every query head h (kv head
+ * h / (n_heads / n_heads_kv)), out_h = softmax_t((q_h . k_t) / sqrt(head_dim))
+ * applied to v_t over t < n_past, all fp32.  k_cache and v_cache are one
+ * layer's [max_ctx][n_heads_kv][head_dim] fp32 caches (the engine writes the
+ * current token's rows at position n_past - 1 first, src/engine.cpp:446-453).
+ * n_past <= 0 enqueues nothing (output untouched); n_past > max_ctx prints one
+ * stderr line and enqueues nothing (the reference would read past the cache).
+ * head_dim <= 1024.  Nothing is allocated: the interface has no workspace.
+ * Replaces jinf_cuda_attention, cuda/attention_kernel.cu:100-115 (kernel
+ * :25-96). */
+void jinf_cuda_attention(float* output, const float* q, const float* k_cache,
+                         const float* v_cache, int head_dim, int n_heads,
+                         int n_heads_kv, int n_past, int max_ctx, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

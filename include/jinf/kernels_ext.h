@@ -144,6 +144,23 @@ int jinf_dequant_rows(void* out, int ld_out, const void* table, int qtype, int n
                       int n_embd, const int32_t* ids, int n_ids, int out_type,
                       hipStream_t stream);
 
+/* Batched GQA decode attention (cuda/attention_kernel.cu:25-96 over many
+ * sequences, with an fp16 or fp32 KV cache): for sequence s and query head h
+ * (kv head h / (n_heads / n_heads_kv)),
+ *   out[s, h*hd:(h+1)*hd] = sum_t softmax_t(scale * q[s,h] . k[s,t,kv]) v[s,t,kv]
+ * over t < lens[s] (clamped to [0, max_ctx]); a sequence with no position
+ * gets zeros.  q and out are fp32 with row strides ld_q, ld_out (elements).
+ * Cache element (s, t, kv head j, dim d) is at s*ld_seq + t*ld_pos + j*hd + d
+ * in k_cache / v_cache, of kv_type JINF_HIP_F32 or JINF_HIP_F16.
+ * scale = 0 means 1/sqrt(head_dim); otherwise finite and > 0.  lens is a
+ * device array of n_seq int32.  Fast path: head_dim 64 or 128, caches, q
+ * and strides 16-byte aligned.  Nothing is allocated. */
+int jinf_attention_decode(float* out, int ld_out, const float* q, int ld_q,
+                          const void* k_cache, const void* v_cache, int kv_type,
+                          int64_t ld_pos, int64_t ld_seq, const int32_t* lens,
+                          int n_seq, int max_ctx, int head_dim, int n_heads,
+                          int n_heads_kv, float scale, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

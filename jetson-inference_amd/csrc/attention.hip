@@ -1,0 +1,397 @@
+// GQA decode attention for gfx950: one new query token per sequence against
+// its KV cache.
+//
+// Semantics (reference cuda/attention_kernel.cu:25-96, called from
+// src/engine.cpp:446-459 after the K/V rows of the current token are written
+// at position n_past): for query head h, kv head j = h / (n_heads / n_heads_kv),
+//   score_t = (q_h . k_t) * scale,  t < len        (scale = 1/sqrt(head_dim))
+//   out_h   = sum_t softmax(score)_t * v_t
+// in fp32.  The cache of one sequence is [position][kv head][head_dim] with
+// ld_pos elements between positions (n_heads_kv * head_dim in the engine);
+// fp32 as in the reference, or fp16 (one rounding of the fp32 K/V rows).
+//
+// Design.  Decode attention streams the K and V rows once (2 * head_dim *
+// bytes per position and kv head) and is HBM-bound.  A workgroup owns one
+// (sequence, kv head) and the G query heads that read it, so each K/V byte is
+// fetched once for the whole GQA group; its waves split the positions into
+// 64-position tiles and keep flash-decoding state (running max m, sum l and
+// the output accumulator) in registers:
+//   - scores: LPP lanes per position, each with head_dim / LPP dims of every
+//     query head in registers (LPP chosen so that G * head_dim / LPP <= 64
+//     registers), load their slice of the K row (the row is read coalesced)
+//     and reduce the partial dots across the LPP lanes; the score goes to LDS;
+//   - softmax: lane t takes position t of the tile: one tile max and one sum
+//     per head (DPP wave reductions), one exp per position and head, and the
+//     probabilities go back to LDS;
+//   - P V: lane l owns dims l, l + 64, ... of every head; each V row is read
+//     coalesced once and multiplied into all G heads with probabilities read
+//     from LDS as broadcasts;
+//   - the waves' states merge through LDS at the end (flash-decoding combine,
+//     in wave order).
+// When there are too few (sequence, kv head) pairs to fill the GPU (batch-1
+// decode), each workgroup takes a single query head instead (the G heads of
+// a group then share the K/V bytes through L2) and gets up to 16 waves.
+// The reference's interface has no workspace, so the positions of one head
+// are not split across workgroups.
+//
+// head_dim 64 and 128 with 16-byte aligned rows take this kernel; anything
+// else takes a one-wave-per-head kernel (dims on lanes, one wave reduction
+// per position) with the same arithmetic.
+#include "jinf_device.h"
+#include "jinf_host.h"
+#include "jinf/kernels.h"
+#include "jinf/kernels_ext.h"
+
+namespace jinf {
+
+constexpr int kAtTile = 64;  // positions per tile (one per lane in the softmax step)
+
+template <typename T> struct KV;
+template <> struct KV<float> {
+    static __device__ __forceinline__ float get(const float* p, int i) { return p[i]; }
+};
+template <> struct KV<uint16_t> {
+    static __device__ __forceinline__ float get(const uint16_t* p, int i) { return h2f(p[i]); }
+};
+
+// n consecutive elements (n * sizeof(T) a multiple of 16, p 16-byte aligned)
+// widened to fp32.
+template <typename T, int N>
+__device__ __forceinline__ void load_row(const T* p, float (&f)[N]) {
+    if constexpr (sizeof(T) == 4) {
+        static_assert(N % 4 == 0, "fp32 slices are whole 16-byte chunks");
+#pragma unroll
+        for (int c = 0; c < N / 4; ++c) {
+            const float4 v = reinterpret_cast<const float4*>(p)[c];
+            f[4 * c] = v.x; f[4 * c + 1] = v.y; f[4 * c + 2] = v.z; f[4 * c + 3] = v.w;
+        }
+    } else {
+        static_assert(N % 8 == 0, "fp16 slices are whole 16-byte chunks");
+#pragma unroll
+        for (int c = 0; c < N / 8; ++c) {
+            const uint4 v = reinterpret_cast<const uint4*>(p)[c];
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f[8 * c + 2 * i] = h2f((uint16_t)(w[i] & 0xFFFFu));
+                f[8 * c + 2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
+            }
+        }
+    }
+}
+
+// Sum over aligned groups of L consecutive lanes (L a power of two <= 16):
+// every lane of the group gets the group's sum.
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (L >= 2) v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    if constexpr (L >= 4) v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    if constexpr (L >= 8) v += __shfl_xor(v, 4, kWave);
+    if constexpr (L >= 16) v += __shfl_xor(v, 8, kWave);
+    return v;
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// grid: (n_heads_kv * group / G, n_seq); block: waves * 64 (G > 1: 4 waves;
+// G == 1: up to 16).
+// LDS: waves * G * 64 floats (scores / probabilities), then the merge area
+// waves * G * (HD + 2) floats.
+template <typename TKV, int HD, int G>
+__global__ __launch_bounds__(G == 1 ? 1024 : 256) void attn_decode_kernel(
+    float* __restrict__ out, int64_t ld_out, const float* __restrict__ q, int64_t ld_q,
+    const TKV* __restrict__ kc, const TKV* __restrict__ vc, int64_t ld_pos, int64_t ld_seq,
+    const int32_t* __restrict__ lens, int n_past, int group, float scale) {
+    // lens[s] is clamped to [0, n_past] (n_past = the cache's positions)
+    // lanes per position: G * DPQ <= 64 q registers and a K slice of <= 32
+    constexpr int LPP = (HD * G / 64) > (HD / 32) ? (HD * G / 64) : (HD / 32);
+    constexpr int DPQ = HD / LPP;                                // q/k dims per lane
+    constexpr int PPP = kWave / LPP;                             // positions per pass
+    constexpr int NPASS = kAtTile / PPP;
+    constexpr int DPL = HD / kWave;                              // P V dims per lane
+    static_assert(LPP <= 16 && DPQ * G <= 64 && DPQ >= 8 && DPQ <= 32, "tile shape");
+    extern __shared__ float at_lds[];
+    const int waves = blockDim.x / kWave;
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int s = blockIdx.y;
+    const int h0 = blockIdx.x * G;      // first query head of this workgroup
+    const int j = h0 / group;           // its kv head
+    const int len = lens ? min(max(lens[s], 0), n_past) : n_past;
+    float* sc = at_lds + wave * G * kAtTile;  // this wave's scores [G][64]
+
+    const TKV* kb = kc + (int64_t)s * ld_seq + (int64_t)j * HD;
+    const TKV* vb = vc + (int64_t)s * ld_seq + (int64_t)j * HD;
+    const int sub = lane % LPP;  // which DPQ-slice of the row this lane holds
+
+    float qv[G][DPQ];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float* qh = q + (int64_t)s * ld_q + (int64_t)(h0 + g) * HD + sub * DPQ;
+#pragma unroll
+        for (int c = 0; c < DPQ / 4; ++c) {
+            const float4 v = reinterpret_cast<const float4*>(qh)[c];
+            qv[g][4 * c] = v.x; qv[g][4 * c + 1] = v.y; qv[g][4 * c + 2] = v.z; qv[g][4 * c + 3] = v.w;
+        }
+    }
+
+    float m[G], l[G], acc[G][DPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) acc[g][i] = 0.0f;
+    }
+
+    for (int t0 = wave * kAtTile; t0 < len; t0 += waves * kAtTile) {
+        // scores of the tile
+#pragma unroll 2
+        for (int pass = 0; pass < NPASS; ++pass) {
+            const int pt = pass * PPP + lane / LPP;  // position within the tile
+            const int pos = t0 + pt < len ? t0 + pt : len - 1;
+            float kf[DPQ];
+            load_row<TKV, DPQ>(kb + (int64_t)pos * ld_pos + sub * DPQ, kf);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float d = 0.0f;
+#pragma unroll
+                for (int i = 0; i < DPQ; ++i) d = fmaf(qv[g][i], kf[i], d);
+                d = group_sum<LPP>(d);
+                if (sub == 0) sc[g * kAtTile + pt] = t0 + pt < len ? d * scale : -INFINITY;
+            }
+        }
+        wave_lds_sync();
+        // online softmax over the tile: lane = position
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float st = sc[g * kAtTile + lane];
+            const float mn = fmaxf(m[g], wave_max_f32(st));  // finite: position t0 is live
+            const float corr = exp_neg(m[g] - mn);             // 0 on the first tile
+            const float p = exp_neg(st - mn);
+            l[g] = fmaf(l[g], corr, wave_sum_f32(p));
+            m[g] = mn;
+            sc[g * kAtTile + lane] = p;
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) acc[g][i] *= corr;
+        }
+        wave_lds_sync();
+        // P V
+        const int nt = len - t0 < kAtTile ? len - t0 : kAtTile;
+        const TKV* vt = vb + (int64_t)t0 * ld_pos + lane;
+        for (int t = 0; t < nt; ++t) {
+            float vv[DPL];
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) vv[i] = KV<TKV>::get(vt + (int64_t)t * ld_pos, i * kWave);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float p = sc[g * kAtTile + t];
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) acc[g][i] = fmaf(p, vv[i], acc[g][i]);
+            }
+        }
+        wave_lds_sync();
+    }
+
+    // merge the waves' states in wave order
+    float* mg = at_lds + waves * G * kAtTile;  // [waves][G][HD + 2]
+    constexpr int MS = HD + 2;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float* e = mg + (wave * G + g) * MS;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) e[lane + i * kWave] = acc[g][i];
+        if (lane == 0) {
+            e[HD] = m[g];
+            e[HD + 1] = l[g];
+        }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
+        const int g = idx / HD, d = idx % HD;
+        float M = -INFINITY;
+        for (int w = 0; w < waves; ++w) M = fmaxf(M, mg[(w * G + g) * MS + HD]);
+        float num = 0.0f, den = 0.0f;
+        for (int w = 0; w < waves; ++w) {
+            const float* e = mg + (w * G + g) * MS;
+            const float f = exp_neg(e[HD] - M);  // idle waves: m = -inf -> 0
+            num = fmaf(f, e[d], num);
+            den = fmaf(f, e[HD + 1], den);
+        }
+        out[(int64_t)s * ld_out + (int64_t)(h0 + g) * HD + d] = len > 0 ? num / den : 0.0f;
+    }
+}
+
+// Any head_dim (<= 1024) and alignment: one wave per (sequence, query head);
+// lane l owns dims l, l + 64, ...; one wave reduction per position for the
+// score; online softmax per position.
+template <typename TKV>
+__global__ __launch_bounds__(64) void attn_decode_any_kernel(
+    float* __restrict__ out, int64_t ld_out, const float* __restrict__ q, int64_t ld_q,
+    const TKV* __restrict__ kc, const TKV* __restrict__ vc, int64_t ld_pos, int64_t ld_seq,
+    const int32_t* __restrict__ lens, int n_past, int group, int hd, float scale) {
+    constexpr int kMaxDPL = 16;
+    const int lane = threadIdx.x;
+    const int h = blockIdx.x, s = blockIdx.y;
+    const int j = h / group;
+    const int len = lens ? min(max(lens[s], 0), n_past) : n_past;
+    const TKV* kb = kc + (int64_t)s * ld_seq + (int64_t)j * hd;
+    const TKV* vb = vc + (int64_t)s * ld_seq + (int64_t)j * hd;
+    const float* qh = q + (int64_t)s * ld_q + (int64_t)h * hd;
+    float qv[kMaxDPL], acc[kMaxDPL];
+#pragma unroll
+    for (int i = 0; i < kMaxDPL; ++i) {
+        const int d = lane + i * kWave;
+        qv[i] = d < hd ? qh[d] : 0.0f;
+        acc[i] = 0.0f;
+    }
+    float m = -INFINITY, l = 0.0f;
+    for (int t = 0; t < len; ++t) {
+        const TKV* kt = kb + (int64_t)t * ld_pos;
+        const TKV* vt = vb + (int64_t)t * ld_pos;
+        float part = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxDPL; ++i) {
+            const int d = lane + i * kWave;
+            if (d < hd) part = fmaf(qv[i], KV<TKV>::get(kt, d), part);
+        }
+        const float st = wave_sum_f32(part) * scale;
+        const float mn = fmaxf(m, st);
+        const float corr = exp_neg(m - mn);
+        const float p = exp_neg(st - mn);
+        l = fmaf(l, corr, p);
+        m = mn;
+#pragma unroll
+        for (int i = 0; i < kMaxDPL; ++i) {
+            const int d = lane + i * kWave;
+            if (d < hd) acc[i] = fmaf(p, KV<TKV>::get(vt, d), acc[i] * corr);
+        }
+    }
+    float* oh = out + (int64_t)s * ld_out + (int64_t)h * hd;
+#pragma unroll
+    for (int i = 0; i < kMaxDPL; ++i) {
+        const int d = lane + i * kWave;
+        if (d < hd) oh[d] = len > 0 ? acc[i] / l : 0.0f;
+    }
+}
+
+template <typename TKV, int HD, int G>
+static int at_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, const void* k,
+                     const void* v, int64_t ld_pos, int64_t ld_seq, const int32_t* lens,
+                     int n_past, int n_seq, int n_heads, int group, int waves, float scale,
+                     hipStream_t stream) {
+    const size_t shmem = ((size_t)waves * G * kAtTile + (size_t)waves * G * (HD + 2)) * 4;
+    return launch(attn_decode_kernel<TKV, HD, G>, dim3(n_heads / G, n_seq), dim3(waves * kWave),
+                  shmem, stream, out, ld_out, q, ld_q, static_cast<const TKV*>(k),
+                  static_cast<const TKV*>(v), ld_pos, ld_seq, lens, n_past, group, scale);
+}
+
+template <typename TKV, int HD>
+static int at_pick_g(int G, float* out, int64_t ld_out, const float* q, int64_t ld_q,
+                     const void* k, const void* v, int64_t ld_pos, int64_t ld_seq,
+                     const int32_t* lens, int n_past, int n_seq, int n_heads, int group,
+                     int waves, float scale, hipStream_t stream) {
+    switch (G) {
+        case 8: return at_launch<TKV, HD, 8>(out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq, n_heads, group, waves, scale, stream);
+        case 4: return at_launch<TKV, HD, 4>(out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq, n_heads, group, waves, scale, stream);
+        case 2: return at_launch<TKV, HD, 2>(out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq, n_heads, group, waves, scale, stream);
+        default: return at_launch<TKV, HD, 1>(out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq, n_heads, group, waves, scale, stream);
+    }
+}
+
+// Every sequence has n_past positions (the drop-in: lens == nullptr), or
+// lens[s] of at most n_past (the cache's capacity) positions.
+static int attention_decode(float* out, int64_t ld_out, const float* q, int64_t ld_q,
+                            const void* k, const void* v, int kv_type, int64_t ld_pos,
+                            int64_t ld_seq, const int32_t* lens, int n_past, int n_seq,
+                            int head_dim, int n_heads, int n_heads_kv, float scale,
+                            hipStream_t stream) {
+    if (n_seq < 0 || head_dim <= 0 || n_heads <= 0 || n_heads_kv <= 0) return JINF_HIP_ERR_INVALID;
+    if (n_seq == 0) return JINF_HIP_OK;
+    if (!out || !q || !k || !v || n_heads % n_heads_kv != 0) return JINF_HIP_ERR_INVALID;
+    if (kv_type != JINF_HIP_F32 && kv_type != JINF_HIP_F16) return JINF_HIP_ERR_INVALID;
+    if (head_dim > 1024 || ld_pos < (int64_t)n_heads_kv * head_dim) return JINF_HIP_ERR_INVALID;
+    if (ld_out < (int64_t)n_heads * head_dim || ld_q < (int64_t)n_heads * head_dim)
+        return JINF_HIP_ERR_INVALID;
+    if (n_seq > 65535 || n_heads > 0x7FFFFFFF / 2) return JINF_HIP_ERR_INVALID;
+    if (!(scale > 0.0f) || !(scale < INFINITY)) return JINF_HIP_ERR_INVALID;
+    if (!aligned(out, 4) || !aligned(q, 4)) return JINF_HIP_ERR_INVALID;
+    const int group = n_heads / n_heads_kv;
+    const int64_t es = kv_type == JINF_HIP_F16 ? 2 : 4;
+    const bool fast = (head_dim == 64 || head_dim == 128) && aligned(k, 16) && aligned(v, 16) &&
+                      aligned(q, 16) && (ld_pos * es) % 16 == 0 && (ld_seq * es) % 16 == 0 &&
+                      ld_q % 4 == 0;
+    if (!fast) {
+        const dim3 grid(n_heads, n_seq);
+        if (kv_type == JINF_HIP_F16)
+            return launch(attn_decode_any_kernel<uint16_t>, grid, dim3(kWave), 0, stream, out,
+                          ld_out, q, ld_q, static_cast<const uint16_t*>(k),
+                          static_cast<const uint16_t*>(v), ld_pos, ld_seq, lens, n_past, group,
+                          head_dim, scale);
+        return launch(attn_decode_any_kernel<float>, grid, dim3(kWave), 0, stream, out, ld_out,
+                      q, ld_q, static_cast<const float*>(k), static_cast<const float*>(v), ld_pos,
+                      ld_seq, lens, n_past, group, head_dim, scale);
+    }
+    // Enough (sequence, kv head) pairs: one workgroup per pair, all its query
+    // heads (up to 8) together.  Otherwise one query head per workgroup, with
+    // more waves when the (known) context is long.
+    int G = 1, waves = 4;  // G > 1 always runs 4 waves (its launch bound)
+    if ((int64_t)n_seq * n_heads_kv >= 128) {
+        G = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+    } else {
+        const int tiles = lens ? 64 : (n_past + kAtTile - 1) / kAtTile;
+        waves = tiles < 4 ? 4 : tiles > 16 ? 16 : tiles;
+    }
+    if (head_dim == 64) {
+        if (kv_type == JINF_HIP_F16)
+            return at_pick_g<uint16_t, 64>(G, out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq, n_heads, group, waves, scale, stream);
+        return at_pick_g<float, 64>(G, out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq, n_heads, group, waves, scale, stream);
+    }
+    if (kv_type == JINF_HIP_F16)
+        return at_pick_g<uint16_t, 128>(G, out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq, n_heads, group, waves, scale, stream);
+    return at_pick_g<float, 128>(G, out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq, n_heads, group, waves, scale, stream);
+}
+
+// 1/sqrt(head_dim) rounded once from fp64 (the reference uses rsqrtf).
+static float inv_sqrt_hd(int head_dim) { return (float)(1.0 / sqrt((double)head_dim)); }
+
+}  // namespace jinf
+
+extern "C" int jinf_attention_decode(float* out, int ld_out, const float* q, int ld_q,
+                                     const void* k_cache, const void* v_cache, int kv_type,
+                                     int64_t ld_pos, int64_t ld_seq, const int32_t* lens,
+                                     int n_seq, int max_ctx, int head_dim, int n_heads,
+                                     int n_heads_kv, float scale, hipStream_t stream) {
+    if ((!lens && n_seq > 0) || max_ctx < 0) return JINF_HIP_ERR_INVALID;
+    if (n_seq > 1 && ld_seq < (int64_t)max_ctx * ld_pos) return JINF_HIP_ERR_INVALID;
+    if (scale == 0.0f && head_dim > 0) scale = jinf::inv_sqrt_hd(head_dim);
+    return jinf::attention_decode(out, ld_out, q, ld_q, k_cache, v_cache, kv_type, ld_pos, ld_seq,
+                                  lens, max_ctx, n_seq, head_dim, n_heads, n_heads_kv, scale,
+                                  stream);
+}
+
+// Drop-in for cuda/attention_kernel.cu:100-115: one sequence, fp32 cache
+// [max_ctx][n_heads_kv][head_dim], n_past positions (n_past <= 0: nothing).
+extern "C" void jinf_cuda_attention(float* output, const float* q, const float* k_cache,
+                                    const float* v_cache, int head_dim, int n_heads,
+                                    int n_heads_kv, int n_past, int max_ctx, hipStream_t stream) {
+    if (n_past <= 0) return;
+    if (head_dim <= 0 || n_heads <= 0 || n_heads_kv <= 0 || (max_ctx > 0 && n_past > max_ctx)) {
+        JINF_LOG("jinf_cuda_attention: invalid argument (head_dim=%d n_heads=%d n_heads_kv=%d "
+                 "n_past=%d max_ctx=%d)", head_dim, n_heads, n_heads_kv, n_past, max_ctx);
+        return;
+    }
+    const int64_t kvw = (int64_t)n_heads_kv * head_dim;
+    const int st = jinf::attention_decode(output, (int64_t)n_heads * head_dim, q,
+                                          (int64_t)n_heads * head_dim, k_cache, v_cache,
+                                          JINF_HIP_F32, kvw, kvw * (max_ctx > 0 ? max_ctx : n_past),
+                                          nullptr, n_past, 1, head_dim, n_heads, n_heads_kv,
+                                          jinf::inv_sqrt_hd(head_dim), stream);
+    if (st == JINF_HIP_ERR_INVALID)
+        JINF_LOG("jinf_cuda_attention: invalid argument (head_dim=%d n_heads=%d n_heads_kv=%d)",
+                 head_dim, n_heads, n_heads_kv);
+}

@@ -159,6 +159,39 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     return ((r0 + r1) + r2) + r3;
 }
 
+// exp(a) for a softmax argument a = s - m <= 0, accurate to ~2 ulp:
+// Cody-Waite splitting of a*log2(e) into hi + lo (hi the rounded product, lo its
+// exact rounding error plus a times the tail of log2(e)), then
+// 2^hi (v_exp_f32) * (1 + lo*ln2).  |lo| <= 2^-24 |hi| + tiny, so the
+// dropped second-order term is below 1e-13.  Six VALU ops against ~12 for the
+// library expf.  a < -104 (including -inf) returns +0: the true value is below
+// the smallest fp32 subnormal there.  Arguments below about -87.3 give fp32
+// subnormals, which the hardware exp2 may return as 0 (absolute error < 1.2e-38).
+__device__ __forceinline__ float exp_neg(float a) {
+    constexpr float kL2E = 1.44269502162933349609375f;        // fl32(log2 e)
+    constexpr float kL2ELo = 1.925963033500011079e-08f;       // log2 e - kL2E
+    constexpr float kLn2 = 0.693147180559945309f;
+    const float hi = a * kL2E;
+    float lo = fmaf(a, kL2E, -hi);
+    lo = fmaf(a, kL2ELo, lo);
+    const float e = __builtin_amdgcn_exp2f(hi);
+    const float r = fmaf(e, lo * kLn2, e);
+    return a < -104.0f ? 0.0f : r;
+}
+
+// fp32 wave max, same DPP pattern as wave_sum_f32 (every lane gets the result).
+__device__ __forceinline__ float wave_max_f32(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x124>(v));
+    v = fmaxf(v, dpp_f32<0x128>(v));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 // Workgroup reductions.  blockDim.x must be a multiple of 64 and at most 1024.
 // `lds` holds one slot per wave; each thread folds the per-wave partials in
 // wave order, so every thread returns the same value without a second

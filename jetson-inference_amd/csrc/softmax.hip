@@ -43,26 +43,6 @@ __device__ __forceinline__ int live_len(const int32_t* lens, int rows_per_len, i
     return L > n_cols ? n_cols : L;
 }
 
-// exp(a) for the softmax argument a = s - m <= 0, accurate to ~2 ulp:
-// Cody-Waite splitting of a*log2(e) into hi + lo (hi the rounded product, lo its
-// exact rounding error plus a times the tail of log2(e)), then
-// 2^hi (v_exp_f32) * (1 + lo*ln2).  |lo| <= 2^-24 |hi| + tiny, so the
-// dropped second-order term is below 1e-13.  Six VALU ops against ~12 for the
-// library expf.  a < -104 (including -inf) returns +0: the true value is below
-// the smallest fp32 subnormal there.  Arguments below about -87.3 give fp32
-// subnormals, which the hardware exp2 may return as 0 (absolute error < 1.2e-38).
-__device__ __forceinline__ float exp_neg(float a) {
-    constexpr float kL2E = 1.44269502162933349609375f;        // fl32(log2 e)
-    constexpr float kL2ELo = 1.925963033500011079e-08f;       // log2 e - kL2E
-    constexpr float kLn2 = 0.693147180559945309f;
-    const float hi = a * kL2E;
-    float lo = fmaf(a, kL2E, -hi);
-    lo = fmaf(a, kL2ELo, lo);
-    const float e = __builtin_amdgcn_exp2f(hi);
-    const float r = fmaf(e, lo * kLn2, e);
-    return a < -104.0f ? 0.0f : r;
-}
-
 template <int CPT = kSmCPT>
 __global__ __launch_bounds__(1024) void softmax_vec_kernel(
     float* out, int ld_out, const float* in, int ld_in, int n_cols, const int32_t* lens,

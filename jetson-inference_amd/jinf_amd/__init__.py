@@ -2,7 +2,7 @@
 reduction path -- RMSNorm (+ fused residual add), interleaved GQA RoPE,
 SwiGLU, masked row softmax and the GGUF Q4_0 token-embedding gather -- and,
 beside them, the dequant-GEMV and row dequant for GGUF Q4_0 / Q8_0 / Q4_K /
-Q6_K weights.
+Q6_K weights and GQA decode attention.
 
 The kernels live in libjinf_hip.so behind the C-ABI of include/jinf/*.h;
 this package is a thin ctypes/torch front end used by tests and bench.py.
@@ -10,6 +10,8 @@ this package is a thin ctypes/torch front end used by tests and bench.py.
 from ._lib import F16, F32, LIB_PATH, Q4_0, Q4_K, Q6_K, Q8_0, lib, version  # noqa: F401
 from .ops import (  # noqa: F401
     JinfError,
+    attention_decode,
+    cuda_attention,
     cuda_dequant_matvec,
     cuda_dequantize,
     cuda_dequantize_q4_0,

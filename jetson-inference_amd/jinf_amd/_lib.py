@@ -41,6 +41,7 @@ SIGNATURES = {
     "jinf_cuda_dequantize_q4_K": (None, [_P, _P, _I, _P]),
     "jinf_cuda_dequantize_q8_0": (None, [_P, _P, _I, _P]),
     "jinf_cuda_dequantize_q6_K": (None, [_P, _P, _I, _P]),
+    "jinf_cuda_attention": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     # extensions (include/jinf/kernels_ext.h)
     "jinf_hip_version": (ctypes.c_char_p, []),
     "jinf_rmsnorm_rows": (_I, [_P, _I, _P, _I, _P, _I, _I, _F, _I, _I, _P]),
@@ -53,6 +54,8 @@ SIGNATURES = {
     "jinf_matvec_q4_0": (_I, [_P, _P, _P, _I, _I, _P]),
     "jinf_matvec": (_I, [_P, _I, _P, _P, _I, _I, _P]),
     "jinf_dequant_rows": (_I, [_P, _I, _P, _I, _I, _I, _P, _I, _I, _P]),
+    "jinf_attention_decode": (_I, [_P, _I, _P, _I, _P, _P, _I, ctypes.c_int64, ctypes.c_int64,
+                                   _P, _I, _I, _I, _I, _I, _F, _P]),
 }
 
 _lib = None

@@ -189,6 +189,25 @@ def dequant_rows(table, qtype, n_embd, ids=None, out_dtype=torch.float32, out=No
     return out
 
 
+def attention_decode(q, k_cache, v_cache, lens, n_heads, n_heads_kv, scale=0.0, out=None):
+    """Batched GQA decode attention.  q fp32 [n_seq, n_heads*hd]; caches
+    [n_seq, max_ctx, n_heads_kv*hd] fp32 or fp16 (same dtype); lens int32
+    [n_seq].  Returns out fp32 [n_seq, n_heads*hd]."""
+    n_seq, max_ctx, kvw = k_cache.shape
+    hd = kvw // n_heads_kv
+    if v_cache.shape != k_cache.shape or v_cache.dtype != k_cache.dtype:
+        raise JinfError("k and v caches must match")
+    if lens.dtype != torch.int32:
+        raise JinfError("lens must be int32")
+    out = torch.empty((n_seq, n_heads * hd), dtype=torch.float32, device=q.device) if out is None else out
+    _check(lib().jinf_attention_decode(_ptr(out), out.stride(0), _ptr(q), q.stride(0),
+                                       _ptr(k_cache), _ptr(v_cache), _act(k_cache),
+                                       k_cache.stride(1), k_cache.stride(0), _ptr(lens), n_seq,
+                                       max_ctx, hd, n_heads, n_heads_kv, float(scale), _stream()),
+           "jinf_attention_decode")
+    return out
+
+
 # ---- drop-in entry points (reference signatures; fp32, one row) ----
 
 def cuda_rmsnorm(out, x, weight, eps=1e-5):
@@ -237,4 +256,10 @@ def cuda_dequantize(qtype, data, out, n_blocks, byte_offset=0):
             Q4_K: "jinf_cuda_dequantize_q4_K", Q6_K: "jinf_cuda_dequantize_q6_K"}[qtype]
     ptr = ctypes.c_void_p(data.data_ptr() + byte_offset)
     getattr(lib(), name)(ptr, _ptr(out), int(n_blocks), _stream())
+    return out
+
+
+def cuda_attention(out, q, k_cache, v_cache, head_dim, n_heads, n_heads_kv, n_past, max_ctx):
+    lib().jinf_cuda_attention(_ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), int(head_dim),
+                              int(n_heads), int(n_heads_kv), int(n_past), int(max_ctx), _stream())
     return out

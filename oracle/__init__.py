@@ -43,6 +43,8 @@ _SIG = {
     "jo_qtype_geometry": (_I, [_I, ctypes.POINTER(_I)]),
     "jo_dequant": (None, [_I, _P, _P, _I]),
     "jo_matvec": (None, [_I, _P, _P, _P, _P, _I, _I]),
+    "jo_attention": (None, [_P, _L, _P, _L, _P, _P, _I, _L, _L, _P, _I, _I, _I, _I,
+                            ctypes.c_double, _P]),
 }
 
 # qtype codes (include/jinf/quant.h:8-24)
@@ -297,3 +299,27 @@ def matvec(qtype, W_u8, x):
     a = np.empty(rows, np.float64)
     lib().jo_matvec(int(qtype), _p(W), _p(x), _p(y), _p(a), rows, cols)
     return y, a
+
+
+# ---- GQA decode attention ----
+
+def attention(q, k_cache, v_cache, lens, n_heads, n_heads_kv, head_dim, scale=None):
+    """q fp32 [n_seq, n_heads*head_dim]; caches [n_seq, max_ctx, n_heads_kv*head_dim]
+    (fp32 or fp16, same dtype); lens int32 [n_seq] (positions read per sequence).
+    Returns (out fp32 [n_seq, n_heads*head_dim], sum_t p_t |v_t| fp64, same shape)."""
+    q = _c(np.asarray(q, dtype=np.float32))
+    k = _c(k_cache)
+    v = _c(v_cache)
+    assert k.dtype == v.dtype and k.shape == v.shape
+    n_seq, max_ctx, kvw = k.shape
+    assert kvw == n_heads_kv * head_dim and q.shape == (n_seq, n_heads * head_dim)
+    lens = _c(np.asarray(lens, dtype=np.int32))
+    assert head_dim <= 1024 and n_heads % n_heads_kv == 0
+    if scale is None:
+        scale = 1.0 / np.sqrt(float(head_dim))
+    out = np.empty((n_seq, n_heads * head_dim), np.float32)
+    a = np.empty((n_seq, n_heads * head_dim), np.float64)
+    lib().jo_attention(_p(out), n_heads * head_dim, _p(q), n_heads * head_dim, _p(k), _p(v),
+                       _act(k), kvw, max_ctx * kvw, _p(lens), n_seq, head_dim, n_heads,
+                       n_heads_kv, float(scale), _p(a))
+    return out, a

@@ -20,6 +20,7 @@
  *   Q4_0 dequant-GEMV      cuda/matmul_kernels.cu:8-43, 198-225
  *   Q4_K / Q8_0 / Q6_K     src/quant.cpp:64-105, cuda/dequant_kernels.cu:25-110,
  *   dequant and GEMV       cuda/matmul_kernels.cu:47-185
+ *   GQA decode attention   cuda/attention_kernel.cu:25-96, src/engine.cpp:446-459
  * Build with -ffp-contract=off (no FMA contraction) and without fast-math.
  *
  * fp16 storage: every stored value is fl16(fl32(expression)) with
@@ -472,6 +473,65 @@ void jo_matvec(int qtype, const uint8_t* W, const float* x, float* y, double* ab
             }
             y[r] = (float)acc;
             if (abs_y) abs_y[r] = aabs;
+        }
+    }
+}
+
+/* ---- GQA decode attention (cuda/attention_kernel.cu:25-96) ---- */
+
+/* For every sequence s and query head h (kv head h / (n_heads / n_heads_kv)):
+ *   score_t = (q_h . k_t) * scale             t = 0 .. lens[s] - 1
+ *   p_t     = exp(score_t - max) / sum_u exp(score_u - max)
+ *   out_h   = sum_t p_t * v_t
+ * evaluated entirely in fp64 from the stored fp32/fp16 values and rounded to
+ * fp32 once (the reference rounds the dot, the exp, the sum and every
+ * accumulation to fp32; the GPU tolerance covers that).  The cache of sequence
+ * s, position t, kv head j starts at element s * ld_seq + t * ld_pos +
+ * j * head_dim.  abs_out (optional) receives sum_t p_t |v_t[d]|, the scale of
+ * the output's rounding error.  Positions at or past lens[s] are never read. */
+void jo_attention(float* out, int64_t ld_out, const float* q, int64_t ld_q, const void* k,
+                  const void* v, int kv_type, int64_t ld_pos, int64_t ld_seq,
+                  const int32_t* lens, int n_seq, int head_dim, int n_heads, int n_heads_kv,
+                  double scale, double* abs_out) {
+    const int group = n_heads / n_heads_kv;
+#pragma omp parallel num_threads(jo_threads)
+    {
+        double acc[1024], aabs[1024];
+#pragma omp for schedule(dynamic, 1) collapse(2)
+        for (int s = 0; s < n_seq; ++s) {
+            for (int h = 0; h < n_heads; ++h) {
+                const int len = lens[s];
+                const int j = h / group;
+                const float* qh = q + (int64_t)s * ld_q + (int64_t)h * head_dim;
+                double m = -INFINITY;
+                for (int t = 0; t < len; ++t) {
+                    const int64_t o = (int64_t)s * ld_seq + (int64_t)t * ld_pos + (int64_t)j * head_dim;
+                    double dot = 0.0;
+                    for (int d = 0; d < head_dim; ++d) dot += (double)qh[d] * (double)ld_act(k, kv_type, o + d);
+                    const double sc = dot * scale;
+                    if (sc > m) m = sc;
+                }
+                for (int d = 0; d < head_dim; ++d) acc[d] = aabs[d] = 0.0;
+                double l = 0.0;
+                for (int t = 0; t < len; ++t) {
+                    const int64_t o = (int64_t)s * ld_seq + (int64_t)t * ld_pos + (int64_t)j * head_dim;
+                    double dot = 0.0;
+                    for (int d = 0; d < head_dim; ++d) dot += (double)qh[d] * (double)ld_act(k, kv_type, o + d);
+                    const double e = exp(dot * scale - m);
+                    l += e;
+                    for (int d = 0; d < head_dim; ++d) {
+                        const double vv = (double)ld_act(v, kv_type, o + d);
+                        acc[d] += e * vv;
+                        aabs[d] += e * fabs(vv);
+                    }
+                }
+                float* oh = out + (int64_t)s * ld_out + (int64_t)h * head_dim;
+                double* ah = abs_out ? abs_out + ((int64_t)s * n_heads + h) * head_dim : 0;
+                for (int d = 0; d < head_dim; ++d) {
+                    oh[d] = len > 0 ? (float)(acc[d] / l) : 0.0f;
+                    if (ah) ah[d] = len > 0 ? aabs[d] / l : 0.0;
+                }
+            }
         }
     }
 }

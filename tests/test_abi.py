@@ -37,7 +37,7 @@ def test_headers_include_no_gpu_runtime_header():
 
 def test_every_declared_symbol_is_exported_with_declared_arity():
     decl = declared()
-    assert len(decl) == 21
+    assert len(decl) == 23
     lib = jinf_amd.lib()
     for name, n in decl.items():
         assert hasattr(lib, name), name
@@ -82,6 +82,14 @@ FAKE = P(0x1000)  # never dereferenced: every call below is rejected on the host
     lambda L: L.jinf_dequant_rows(FAKE, 128, FAKE, 12, 10, 128, FAKE, 4, 0, None),
     lambda L: L.jinf_dequant_rows(FAKE, 100, FAKE, 8, 10, 128, FAKE, 4, 0, None),
     lambda L: L.jinf_dequant_rows(FAKE, 256, FAKE, 14, 10, 256, None, 11, 0, None),
+    # attention: lens missing, n_heads not a multiple of n_heads_kv, bad scale,
+    # ld_pos below one position, kv type, head_dim too large
+    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 0, 128, 4096, None, 2, 32, 128, 2, 1, 0.0, None),
+    lambda L: L.jinf_attention_decode(FAKE, 384, FAKE, 384, FAKE, FAKE, 0, 256, 8192, FAKE, 2, 32, 128, 3, 2, 0.0, None),
+    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 0, 128, 4096, FAKE, 2, 32, 128, 2, 1, -1.0, None),
+    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 0, 64, 4096, FAKE, 2, 32, 128, 2, 1, 0.0, None),
+    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 7, 128, 4096, FAKE, 2, 32, 128, 2, 1, 0.0, None),
+    lambda L: L.jinf_attention_decode(FAKE, 4096, FAKE, 4096, FAKE, FAKE, 0, 2048, 65536, FAKE, 2, 32, 2048, 2, 1, 0.0, None),
 ])
 def test_invalid_arguments_rejected_on_host(call):
     assert call(jinf_amd.lib()) == _lib.JINF_HIP_ERR_INVALID
@@ -96,6 +104,7 @@ def test_invalid_arguments_rejected_on_host(call):
     lambda L: L.jinf_matvec_q4_0(FAKE, FAKE, FAKE, 0, 128, None),
     lambda L: L.jinf_matvec(FAKE, 14, FAKE, FAKE, 16, 0, None),
     lambda L: L.jinf_dequant_rows(FAKE, 256, FAKE, 12, 10, 256, FAKE, 0, 0, None),
+    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 0, 128, 4096, FAKE, 0, 32, 128, 2, 1, 0.0, None),
 ])
 def test_empty_work_is_ok_and_enqueues_nothing(call):
     assert call(jinf_amd.lib()) == _lib.JINF_HIP_OK
@@ -114,3 +123,4 @@ def test_drop_ins_are_noops_for_empty_sizes():
     L.jinf_cuda_dequantize_q4_K(FAKE, FAKE, 0, None)
     L.jinf_cuda_dequantize_q8_0(FAKE, FAKE, -1, None)
     L.jinf_cuda_dequantize_q6_K(FAKE, FAKE, 0, None)
+    L.jinf_cuda_attention(FAKE, FAKE, FAKE, FAKE, 128, 32, 8, 0, 4096, None)
