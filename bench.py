@@ -187,14 +187,16 @@ def build_attention(torch, jinf, g, name, n_seq, max_ctx, nh, nkv, hd, lens, kv_
         q = torch.randn((n_seq, nh * hd), generator=g, device="cuda") * 2.0
         o = torch.empty((n_seq, nh * hd), dtype=torch.float32, device="cuda")
         lc = lens.clone()
-        keep.append((q, k, v, lc, o))
+        ws = jinf.attention_workspace(n_seq, nh, hd, max_ctx)
+        keep.append((q, k, v, lc, o, ws))
         if n_seq == 1 and kv_dtype == torch.float32:  # the reference's drop-in
             sets.append(lambda q=q, k=k, v=v, o=o: jinf.cuda_attention(
                 o, q, k, v, hd, nh, nkv, n_past, max_ctx))
         else:
-            sets.append(lambda q=q, k=k, v=v, lc=lc, o=o: jinf.attention_decode(
-                q, k, v, lc, nh, nkv, out=o))
-    return Kernel(name, nbytes, n_seq, "sequences", sets, "attn_decode_kernel",
+            sets.append(lambda q=q, k=k, v=v, lc=lc, o=o, ws=ws: jinf.attention_decode(
+                q, k, v, lc, nh, nkv, out=o, workspace=ws))
+    return Kernel(name, nbytes, n_seq, "sequences", sets,
+                  "attn_mfma_kernel" if kv_dtype == torch.float16 else "attn_decode_kernel",
                   keep[-len(sets)][:4],
                   lambda o, q, k, v, lc: o.attention(q, k, v, lc, nh, nkv, hd))
 
@@ -458,6 +460,8 @@ _KERNEL_KEYS = [("ew_vec_kernel<unsigned short, 1", "swiglu"),
                 ("matvec_kernel<14, false>", "gemv_down"),
                 ("matvec_any_kernel", "gemv_generic"),
                 ("attn_decode_kernel", "gqa_attention"),
+                ("attn_mfma_kernel", "gqa_attention"),
+                ("attn_combine_kernel", "gqa_attention_combine"),
                 ("attn_decode_any_kernel", "gqa_attention_generic"),
                 ("copyBuffer", "copy_calibration")]
 

@@ -154,12 +154,23 @@ int jinf_dequant_rows(void* out, int ld_out, const void* table, int qtype, int n
  * in k_cache / v_cache, of kv_type JINF_HIP_F32 or JINF_HIP_F16.
  * scale = 0 means 1/sqrt(head_dim); otherwise finite and > 0.  lens is a
  * device array of n_seq int32.  Fast path: head_dim 64 or 128, caches, q
- * and strides 16-byte aligned.  Nothing is allocated. */
+ * and strides 16-byte aligned; an fp16 cache then runs on the matrix cores
+ * (|q * scale| < 65504).  Nothing is allocated.  workspace (device memory,
+ * optional: NULL or too small runs every sequence in one work item) lets an
+ * fp16-cache call split contexts longer than 1024 positions over several
+ * workgroups; it needs jinf_attention_workspace_bytes(n_seq, n_heads,
+ * head_dim, max_ctx) bytes, holds no state between calls, and must not be
+ * shared by calls running concurrently. */
 int jinf_attention_decode(float* out, int ld_out, const float* q, int ld_q,
                           const void* k_cache, const void* v_cache, int kv_type,
                           int64_t ld_pos, int64_t ld_seq, const int32_t* lens,
                           int n_seq, int max_ctx, int head_dim, int n_heads,
-                          int n_heads_kv, float scale, hipStream_t stream);
+                          int n_heads_kv, float scale, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes jinf_attention_decode can use to split long contexts
+ * (0 for an empty shape). */
+size_t jinf_attention_workspace_bytes(int n_seq, int n_heads, int head_dim, int max_ctx);
 
 #ifdef __cplusplus
 }

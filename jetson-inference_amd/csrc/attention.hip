@@ -15,7 +15,9 @@
 // (sequence, kv head) and the G query heads that read it, so each K/V byte is
 // fetched once for the whole GQA group; its waves split the positions into
 // 64-position tiles and keep flash-decoding state (running max m, sum l and
-// the output accumulator) in registers:
+// the output accumulator) in registers.  An fp16 cache runs on the matrix
+// cores (attn_mfma_kernel below); an fp32 cache (the reference's drop-in) on
+// the vector ALUs:
 //   - scores: LPP lanes per position, each with head_dim / LPP dims of every
 //     query head in registers (LPP chosen so that G * head_dim / LPP <= 64
 //     registers), load their slice of the K row (the row is read coalesced)
@@ -279,6 +281,356 @@ __global__ __launch_bounds__(64) void attn_decode_any_kernel(
     }
 }
 
+// ---- fp16 cache: matrix-core kernel ----
+//
+// For an fp16 cache the GQA group's work per 64-position tile is two small
+// matrix products, done on the matrix cores with v_mfma_f32_16x16x16_f16
+// (A 16x16 rows x k, B 16x16 k x columns, fp32 accumulate; lane l supplies A
+// row l % 16 / B column l % 16 at k = 4 (l / 16) .. + 3, and holds D rows
+// 4 (l / 16) .. + 3 of column l % 16):
+//   S^T[t][c] = sum_d K[t][d] Q'[d][c]   A = K rows (fp16, exact),
+//                                          B = columns c = 8 head slots x {hi, lo}
+//   O[c][d]  += sum_t P'[c][t] V[t][d]   A = P' (hi / lo rows), B = V
+// q' = q * scale and P' = p * 2^15 are split into fp16 hi + lo parts
+// (hi = fp16(x), lo = fp16(x - hi)), so the products keep about 22
+// significant bits; the 2^15 keeps the probabilities in fp16's normal range
+// and is divided out exactly at the end.  The score accumulator's layout
+// (lane: column c, rows = 4 positions) is exactly the A layout P needs, so
+// the softmax runs in registers; V goes through LDS (rows padded by 8 bytes,
+// so the four lane groups hit different banks) and each B fragment is four
+// 16-bit reads.  The dot-product index is permuted identically in K and Q'
+// (lane group g, k-step s covers dims (HD/4) g + 4 s .. + 3), so each lane
+// loads its K slice as contiguous 16-byte pieces.
+typedef _Float16 am_h4 __attribute__((ext_vector_type(4)));
+typedef float am_f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kAmChunk = 1024;     // positions per work item when a workspace splits them
+constexpr float kAmPScale = 32768.0f;  // 2^15
+
+__device__ __forceinline__ am_h4 am_h4_from(uint32_t lo, uint32_t hi) {
+    const uint2 u = make_uint2(lo, hi);
+    return __builtin_bit_cast(am_h4, u);
+}
+
+__device__ __forceinline__ float ror8(float v) { return dpp_f32<0x128>(v); }  // row_ror:8
+
+// One 16-byte direct-to-LDS load per lane: lane l's 16 bytes from gptr land
+// at LDS byte lds_base + 16 l (lds_base wave-uniform).  Issued from inline
+// assembly so that the compiler's wait-count tracking, which cannot tell
+// this wave's K and V regions apart, adds no wait for it; the kernel waits
+// for these loads itself (an uncounted load can only make the compiler's
+// own waits longer, never shorter).
+// M0 (the LDS destination register) is saved and restored around the load,
+// so the statement leaves every register the compiler knows about intact.
+__device__ __forceinline__ void lds_load16(const void* gptr, const void* lds_base) {
+    const uint32_t off = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_base;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(gptr), "s"(__builtin_amdgcn_readfirstlane(off))
+        : "memory");
+}
+
+// s_waitcnt immediate that waits until at most N vector-memory operations
+// are outstanding (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt and
+// lgkmcnt left at their maxima).
+template <int N>
+constexpr int waitcnt_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    return (N & 0xF) | ((N >> 4) << 14) | 0x0F70;
+}
+
+// grid (n_heads / G, n_chunks, n_seq), 256 threads.  ws == nullptr: one chunk
+// spanning the sequence, output written directly; otherwise each (sequence,
+// head, chunk) writes an unnormalised partial {O[HD], m, l} to ws and
+// attn_combine_kernel merges them.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_mfma_kernel(
+    float* __restrict__ out, int64_t ld_out, const float* __restrict__ q, int64_t ld_q,
+    const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t ld_pos,
+    int64_t ld_seq, const int32_t* __restrict__ lens, int n_past, int group, int G,
+    int n_heads, float scale, float* __restrict__ ws, int chunk) {
+    constexpr int KS = HD / 16;        // k-steps of the score product
+    constexpr int DPG = HD / 4;        // dims per lane group in the score product
+    constexpr int KLD = DPG / 8;       // 16-byte K loads per position block
+    constexpr int NB = HD / 16;        // 16-dim blocks of the output
+    constexpr int VCH = HD / 8;        // 16-byte chunks per V row
+    constexpr int VRS = kWave / VCH;   // V rows per load instruction
+    constexpr int VLD = kAtTile / VRS; // V loads per lane per tile
+    constexpr int PITCH = HD * 2;      // LDS bytes per staged V row
+    constexpr int MS = HD + 2;         // merge record: O[HD], m, l
+    extern __shared__ uint8_t am_lds[];
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+    const int col = lane & 15, lg = lane >> 4;
+    const int slot = col & 7;          // head slot of this column
+    const bool lo_col = col >= 8;
+    const int s = blockIdx.z;
+    const int h0 = blockIdx.x * G;
+    const int j = h0 / group;
+    const int len = lens ? min(max(lens[s], 0), n_past) : n_past;
+    const int c0 = blockIdx.y * chunk;
+    const int c1 = min(c0 + chunk, len);
+    uint8_t* vst = am_lds + wave * 2 * kAtTile * PITCH;  // V tile, then K tile
+    const uint16_t* kb = kc + (int64_t)s * ld_seq + (int64_t)j * HD;
+    const uint16_t* vb = vc + (int64_t)s * ld_seq + (int64_t)j * HD;
+
+    // Q' fragments of this lane's column (zero for unused head slots): the
+    // lane's DPG contiguous q values, loaded unconditionally
+    am_h4 qf[KS];
+    {
+        const float qs = slot < G ? scale : 0.0f;
+        const float4* qp = reinterpret_cast<const float4*>(
+            q + (int64_t)s * ld_q + (int64_t)(h0 + (slot < G ? slot : 0)) * HD + DPG * lg);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const float4 v = qp[ks];
+            const float x[4] = {v.x * qs, v.y * qs, v.z * qs, v.w * qs};
+            _Float16 hv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const _Float16 hi = (_Float16)x[i];
+                hv[i] = lo_col ? (_Float16)(x[i] - (float)hi) : hi;
+            }
+            qf[ks] = am_h4{hv[0], hv[1], hv[2], hv[3]};
+        }
+    }
+
+    float m = -INFINITY, lsum = 0.0f;
+    am_f4 O[NB];
+#pragma unroll
+    for (int n = 0; n < NB; ++n) O[n] = am_f4{0.f, 0.f, 0.f, 0.f};
+
+    // Software pipeline over the wave's tiles, all loads straight to LDS
+    // (global_load_lds_dwordx4: instruction i of a tile fills the wave's
+    // 16-byte slots 64 i + lane, so the source address picks the layout):
+    // the next tile's K rows are requested right after the current score
+    // product has read the K buffer, its V rows right after the current P V
+    // has read the V buffer; the waits below let the other buffer's loads
+    // stay in flight.  Rows past the end re-read the last live row (finite,
+    // masked out).  K slot (row r, p) holds chunk p ^ swizzle(r) so that the
+    // 16 rows of a fragment read hit distinct banks; V slot (r, p) holds
+    // chunk p ^ 2 ((r >> 2) & 3) for the same reason.
+    uint8_t* kst = vst + kAtTile * PITCH;  // this wave's K tile, after its V tile
+    auto kswz = [](int r) { return HD == 128 ? (r & 15) : ((r >> 1) & 7); };
+    auto load_k = [&](int t0) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only: K buffer reads are done
+#pragma unroll
+        for (int i = 0; i < VLD; ++i) {
+            const int slot_i = kWave * i + lane;
+            const int row = slot_i / VCH;
+            const int c = (slot_i % VCH) ^ kswz(row);
+            const uint16_t* src = kb + (int64_t)min(t0 + row, c1 - 1) * ld_pos + 8 * c;
+            lds_load16(src, kst + 1024 * i);
+        }
+    };
+    auto load_v = [&](int t0) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only: V buffer reads are done
+#pragma unroll
+        for (int i = 0; i < VLD; ++i) {
+            const int slot_i = kWave * i + lane;
+            const int row = slot_i / VCH;
+            const int c = (slot_i % VCH) ^ (2 * ((row >> 2) & 3));
+            const uint16_t* src = vb + (int64_t)min(t0 + row, c1 - 1) * ld_pos + 8 * c;
+            lds_load16(src, vst + 1024 * i);
+        }
+    };
+    const int tstep = 4 * kAtTile;
+    if (c0 + wave * kAtTile < c1) {
+        load_k(c0 + wave * kAtTile);
+        load_v(c0 + wave * kAtTile);
+    }
+    for (int t0 = c0 + wave * kAtTile; t0 < c1; t0 += tstep) {
+        const bool more = t0 + tstep < c1;  // wave-uniform
+        // K(t) has landed once at most the VLD V loads issued after it remain
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm<VLD>());
+        wave_lds_sync();
+        // scores: A fragment = 4 halves of row 16 b + col at dims DPG lg + 4 ks
+        am_f4 S[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            S[b] = am_f4{0.f, 0.f, 0.f, 0.f};
+            const int r = 16 * b + col;
+#pragma unroll
+            for (int u = 0; u < KLD; ++u) {
+                const int c = (DPG * lg) / 8 + u;  // 16-byte chunk of the row
+                const uint4 w = *reinterpret_cast<const uint4*>(kst + r * PITCH + 16 * (c ^ kswz(r)));
+                S[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(am_h4_from(w.x, w.y), qf[2 * u], S[b], 0, 0, 0);
+                S[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(am_h4_from(w.z, w.w), qf[2 * u + 1], S[b], 0, 0, 0);
+            }
+        }
+        wave_lds_sync();
+        if (more) load_k(t0 + tstep);
+        // hi + lo columns, mask, tile max (lanes of one column: xor 16, 32)
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float v = S[b][r] + ror8(S[b][r]);
+                const float vm = t0 + 16 * b + 4 * lg + r < c1 ? v : -INFINITY;
+                S[b][r] = vm;
+                tmax = fmaxf(tmax, vm);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+        const float mn = fmaxf(m, tmax);
+        const float corr = exp_neg(m - mn);
+        m = mn;
+        float psum = 0.0f;
+        am_h4 P[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            _Float16 hv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float pr = exp_neg(S[b][r] - mn);
+                psum += pr;
+                const float ps = pr * kAmPScale;
+                const _Float16 hi = (_Float16)ps;
+                hv[r] = lo_col ? (_Float16)(ps - (float)hi) : hi;
+            }
+            P[b] = am_h4{hv[0], hv[1], hv[2], hv[3]};
+        }
+        lsum = fmaf(lsum, corr, psum);
+        // rescale O: its rows 4 lg + r are slots (4 lg + r) & 7, whose factor
+        // sits in lane slot (lane group 0)
+        float cr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float c_lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr), r));
+            const float c_hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr), 4 + r));
+            cr[r] = (lg & 1) ? c_hi : c_lo;
+        }
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) O[n][r] *= cr[r];
+        // O += P' V once the tile's V has landed in LDS (the next tile's K
+        // loads, issued later, may stay in flight)
+        if (more)
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm<VLD>());
+        else
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
+        wave_lds_sync();
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint8_t* vrow = vst + (16 * b + 4 * lg) * PITCH + 2 * (col & 7);
+#pragma unroll
+            for (int n = 0; n < NB; ++n) {
+                const int p = (2 * n + (col >> 3)) ^ (2 * lg);  // swizzled chunk
+                const uint16_t* p0 = reinterpret_cast<const uint16_t*>(vrow + 16 * p);
+                const uint32_t x0 = p0[0] | ((uint32_t)p0[PITCH / 2] << 16);
+                const uint32_t x1 = p0[PITCH] | ((uint32_t)p0[3 * PITCH / 2] << 16);
+                O[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(P[b], am_h4_from(x0, x1), O[n], 0, 0, 0);
+            }
+        }
+        wave_lds_sync();
+        if (more) load_v(t0 + tstep);
+    }
+
+    // hi + lo rows (lane groups 2, 3 hold the lo rows of groups 0, 1), the
+    // column's probability sum over its four lane groups
+#pragma unroll
+    for (int n = 0; n < NB; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) O[n][r] += __shfl_xor(O[n][r], 32, kWave);
+    lsum += __shfl_xor(lsum, 16, kWave);
+    lsum += __shfl_xor(lsum, 32, kWave);
+
+    // merge the four waves (wave order) through LDS
+    __syncthreads();
+    float* mg = reinterpret_cast<float*>(am_lds);  // [4][8][MS]
+    if (lg < 2) {
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                mg[(wave * 8 + 4 * lg + r) * MS + 16 * n + col] = O[n][r] * (1.0f / kAmPScale);
+    }
+    if (lg == 0 && col < 8) {
+        mg[(wave * 8 + col) * MS + HD] = m;
+        mg[(wave * 8 + col) * MS + HD + 1] = lsum;
+    }
+    __syncthreads();
+    const int nch = gridDim.y;
+    for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
+        const int g = idx / HD, d = idx % HD;
+        float M = -INFINITY;
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, mg[(w * 8 + g) * MS + HD]);
+        float num = 0.0f, den = 0.0f;
+        if (M > -INFINITY) {
+            for (int w = 0; w < 4; ++w) {
+                const float* e = mg + (w * 8 + g) * MS;
+                const float f = exp_neg(e[HD] - M);
+                num = fmaf(f, e[d], num);
+                den = fmaf(f, e[HD + 1], den);
+            }
+        }
+        if (!ws) {
+            out[(int64_t)s * ld_out + (int64_t)(h0 + g) * HD + d] = den > 0.0f ? num / den : 0.0f;
+        } else {
+            float* rec = ws + (((int64_t)s * n_heads + h0 + g) * nch + blockIdx.y) * MS;
+            rec[d] = num;
+            if (d == 0) {
+                rec[HD] = M;
+                rec[HD + 1] = den;
+            }
+        }
+    }
+}
+
+// Merge of the chunk partials: grid (n_heads, n_seq), head_dim threads.
+__global__ __launch_bounds__(256) void attn_combine_kernel(
+    float* __restrict__ out, int64_t ld_out, const float* __restrict__ ws,
+    const int32_t* __restrict__ lens, int n_past, int n_heads, int hd, int nch, int chunk) {
+    const int h = blockIdx.x, s = blockIdx.y, d = threadIdx.x;
+    if (d >= hd) return;
+    const int len = lens ? min(max(lens[s], 0), n_past) : n_past;
+    const int used = (len + chunk - 1) / chunk;
+    const float* rec = ws + ((int64_t)s * n_heads + h) * nch * (hd + 2);
+    float M = -INFINITY;
+    for (int c = 0; c < used; ++c) M = fmaxf(M, rec[c * (hd + 2) + hd]);
+    float num = 0.0f, den = 0.0f;
+    if (M > -INFINITY) {
+        for (int c = 0; c < used; ++c) {
+            const float* e = rec + c * (hd + 2);
+            const float f = exp_neg(e[hd] - M);
+            num = fmaf(f, e[d], num);
+            den = fmaf(f, e[hd + 1], den);
+        }
+    }
+    out[(int64_t)s * ld_out + (int64_t)h * hd + d] = den > 0.0f ? num / den : 0.0f;
+}
+
+static size_t am_workspace_bytes(int n_seq, int n_heads, int head_dim, int max_ctx) {
+    const int64_t nch = ((int64_t)max_ctx + kAmChunk - 1) / kAmChunk;
+    return (size_t)n_seq * n_heads * nch * (head_dim + 2) * sizeof(float);
+}
+
+template <int HD>
+static int am_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, const void* k,
+                     const void* v, int64_t ld_pos, int64_t ld_seq, const int32_t* lens,
+                     int n_past, int n_seq, int n_heads, int group, int G, float scale,
+                     void* workspace, size_t ws_bytes, hipStream_t stream) {
+    const size_t shmem = (size_t)4 * 2 * kAtTile * HD * 2;  // K and V tile per wave
+    const bool split = workspace && n_past > kAmChunk &&
+                       ws_bytes >= am_workspace_bytes(n_seq, n_heads, HD, n_past);
+    const int nch = split ? (n_past + kAmChunk - 1) / kAmChunk : 1;
+    const int chunk = split ? kAmChunk : (n_past > 0 ? n_past : 1);
+    float* ws = split ? static_cast<float*>(workspace) : nullptr;
+    int st = launch(attn_mfma_kernel<HD>, dim3(n_heads / G, nch, n_seq), dim3(256), shmem, stream,
+                    out, ld_out, q, ld_q, static_cast<const uint16_t*>(k),
+                    static_cast<const uint16_t*>(v), ld_pos, ld_seq, lens, n_past, group, G,
+                    n_heads, scale, ws, chunk);
+    if (st != JINF_HIP_OK || !split) return st;
+    return launch(attn_combine_kernel, dim3(n_heads, n_seq), dim3(HD), 0, stream, out, ld_out,
+                  (const float*)ws, lens, n_past, n_heads, HD, nch, chunk);
+}
+
 template <typename TKV, int HD, int G>
 static int at_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, const void* k,
                      const void* v, int64_t ld_pos, int64_t ld_seq, const int32_t* lens,
@@ -309,7 +661,7 @@ static int attention_decode(float* out, int64_t ld_out, const float* q, int64_t 
                             const void* k, const void* v, int kv_type, int64_t ld_pos,
                             int64_t ld_seq, const int32_t* lens, int n_past, int n_seq,
                             int head_dim, int n_heads, int n_heads_kv, float scale,
-                            hipStream_t stream) {
+                            void* workspace, size_t ws_bytes, hipStream_t stream) {
     if (n_seq < 0 || head_dim <= 0 || n_heads <= 0 || n_heads_kv <= 0) return JINF_HIP_ERR_INVALID;
     if (n_seq == 0) return JINF_HIP_OK;
     if (!out || !q || !k || !v || n_heads % n_heads_kv != 0) return JINF_HIP_ERR_INVALID;
@@ -336,9 +688,19 @@ static int attention_decode(float* out, int64_t ld_out, const float* q, int64_t 
                       q, ld_q, static_cast<const float*>(k), static_cast<const float*>(v), ld_pos,
                       ld_seq, lens, n_past, group, head_dim, scale);
     }
-    // Enough (sequence, kv head) pairs: one workgroup per pair, all its query
-    // heads (up to 8) together.  Otherwise one query head per workgroup, with
-    // more waves when the (known) context is long.
+    // fp16 cache: the matrix-core kernel, all query heads of a group (up to
+    // 8) per workgroup.
+    if (kv_type == JINF_HIP_F16) {
+        const int G = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+        if (head_dim == 64)
+            return am_launch<64>(out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq,
+                                 n_heads, group, G, scale, workspace, ws_bytes, stream);
+        return am_launch<128>(out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq,
+                              n_heads, group, G, scale, workspace, ws_bytes, stream);
+    }
+    // fp32 cache: enough (sequence, kv head) pairs: one workgroup per pair,
+    // all its query heads (up to 8) together.  Otherwise one query head per
+    // workgroup, with more waves when the (known) context is long.
     int G = 1, waves = 4;  // G > 1 always runs 4 waves (its launch bound)
     if ((int64_t)n_seq * n_heads_kv >= 128) {
         G = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
@@ -346,13 +708,8 @@ static int attention_decode(float* out, int64_t ld_out, const float* q, int64_t 
         const int tiles = lens ? 64 : (n_past + kAtTile - 1) / kAtTile;
         waves = tiles < 4 ? 4 : tiles > 16 ? 16 : tiles;
     }
-    if (head_dim == 64) {
-        if (kv_type == JINF_HIP_F16)
-            return at_pick_g<uint16_t, 64>(G, out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq, n_heads, group, waves, scale, stream);
+    if (head_dim == 64)
         return at_pick_g<float, 64>(G, out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq, n_heads, group, waves, scale, stream);
-    }
-    if (kv_type == JINF_HIP_F16)
-        return at_pick_g<uint16_t, 128>(G, out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq, n_heads, group, waves, scale, stream);
     return at_pick_g<float, 128>(G, out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq, n_heads, group, waves, scale, stream);
 }
 
@@ -361,17 +718,25 @@ static float inv_sqrt_hd(int head_dim) { return (float)(1.0 / sqrt((double)head_
 
 }  // namespace jinf
 
+extern "C" size_t jinf_attention_workspace_bytes(int n_seq, int n_heads, int head_dim,
+                                                int max_ctx) {
+    if (n_seq <= 0 || n_heads <= 0 || head_dim <= 0 || max_ctx <= 0) return 0;
+    return jinf::am_workspace_bytes(n_seq, n_heads, head_dim, max_ctx);
+}
+
 extern "C" int jinf_attention_decode(float* out, int ld_out, const float* q, int ld_q,
                                      const void* k_cache, const void* v_cache, int kv_type,
                                      int64_t ld_pos, int64_t ld_seq, const int32_t* lens,
                                      int n_seq, int max_ctx, int head_dim, int n_heads,
-                                     int n_heads_kv, float scale, hipStream_t stream) {
+                                     int n_heads_kv, float scale, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream) {
     if ((!lens && n_seq > 0) || max_ctx < 0) return JINF_HIP_ERR_INVALID;
     if (n_seq > 1 && ld_seq < (int64_t)max_ctx * ld_pos) return JINF_HIP_ERR_INVALID;
+    if (workspace && !jinf::aligned(workspace, 4)) return JINF_HIP_ERR_INVALID;
     if (scale == 0.0f && head_dim > 0) scale = jinf::inv_sqrt_hd(head_dim);
     return jinf::attention_decode(out, ld_out, q, ld_q, k_cache, v_cache, kv_type, ld_pos, ld_seq,
                                   lens, max_ctx, n_seq, head_dim, n_heads, n_heads_kv, scale,
-                                  stream);
+                                  workspace, workspace_bytes, stream);
 }
 
 // Drop-in for cuda/attention_kernel.cu:100-115: one sequence, fp32 cache
@@ -390,7 +755,7 @@ extern "C" void jinf_cuda_attention(float* output, const float* q, const float* 
                                           (int64_t)n_heads * head_dim, k_cache, v_cache,
                                           JINF_HIP_F32, kvw, kvw * (max_ctx > 0 ? max_ctx : n_past),
                                           nullptr, n_past, 1, head_dim, n_heads, n_heads_kv,
-                                          jinf::inv_sqrt_hd(head_dim), stream);
+                                          jinf::inv_sqrt_hd(head_dim), nullptr, 0, stream);
     if (st == JINF_HIP_ERR_INVALID)
         JINF_LOG("jinf_cuda_attention: invalid argument (head_dim=%d n_heads=%d n_heads_kv=%d)",
                  head_dim, n_heads, n_heads_kv);

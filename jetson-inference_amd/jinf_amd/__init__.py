@@ -11,6 +11,7 @@ from ._lib import F16, F32, LIB_PATH, Q4_0, Q4_K, Q6_K, Q8_0, lib, version  # no
 from .ops import (  # noqa: F401
     JinfError,
     attention_decode,
+    attention_workspace,
     cuda_attention,
     cuda_dequant_matvec,
     cuda_dequantize,

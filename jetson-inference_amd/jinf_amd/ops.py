@@ -189,10 +189,18 @@ def dequant_rows(table, qtype, n_embd, ids=None, out_dtype=torch.float32, out=No
     return out
 
 
-def attention_decode(q, k_cache, v_cache, lens, n_heads, n_heads_kv, scale=0.0, out=None):
+def attention_workspace(n_seq, n_heads, head_dim, max_ctx, device="cuda"):
+    """A workspace tensor for attention_decode's split of long contexts."""
+    nbytes = lib().jinf_attention_workspace_bytes(n_seq, n_heads, head_dim, max_ctx)
+    return torch.empty(max(nbytes, 4), dtype=torch.uint8, device=device)
+
+
+def attention_decode(q, k_cache, v_cache, lens, n_heads, n_heads_kv, scale=0.0, out=None,
+                     workspace=None):
     """Batched GQA decode attention.  q fp32 [n_seq, n_heads*hd]; caches
     [n_seq, max_ctx, n_heads_kv*hd] fp32 or fp16 (same dtype); lens int32
-    [n_seq].  Returns out fp32 [n_seq, n_heads*hd]."""
+    [n_seq]; workspace: optional uint8 tensor (attention_workspace).  Returns
+    out fp32 [n_seq, n_heads*hd]."""
     n_seq, max_ctx, kvw = k_cache.shape
     hd = kvw // n_heads_kv
     if v_cache.shape != k_cache.shape or v_cache.dtype != k_cache.dtype:
@@ -203,7 +211,9 @@ def attention_decode(q, k_cache, v_cache, lens, n_heads, n_heads_kv, scale=0.0, 
     _check(lib().jinf_attention_decode(_ptr(out), out.stride(0), _ptr(q), q.stride(0),
                                        _ptr(k_cache), _ptr(v_cache), _act(k_cache),
                                        k_cache.stride(1), k_cache.stride(0), _ptr(lens), n_seq,
-                                       max_ctx, hd, n_heads, n_heads_kv, float(scale), _stream()),
+                                       max_ctx, hd, n_heads, n_heads_kv, float(scale),
+                                       _ptr(workspace),
+                                       0 if workspace is None else workspace.numel(), _stream()),
            "jinf_attention_decode")
     return out
 

@@ -37,7 +37,7 @@ def test_headers_include_no_gpu_runtime_header():
 
 def test_every_declared_symbol_is_exported_with_declared_arity():
     decl = declared()
-    assert len(decl) == 23
+    assert len(decl) == 24
     lib = jinf_amd.lib()
     for name, n in decl.items():
         assert hasattr(lib, name), name
@@ -66,7 +66,7 @@ FAKE = P(0x1000)  # never dereferenced: every call below is rejected on the host
     lambda L: L.jinf_swiglu_rows(FAKE, 64, FAKE, 64, FAKE, 32, 2, 64, 1, None),
     lambda L: L.jinf_swiglu_rows(FAKE, 64, FAKE, 64, FAKE, 64, 2, 64, 3, None),
     lambda L: L.jinf_residual_add_rows(FAKE, 64, None, 64, 2, 64, 1, None),
-    lambda L: L.jinf_softmax_rows_f32(FAKE, 64, FAKE, 64, 2, 64, None, 1, 0.0, None),
+    lambda L: L.jinf_softmax_rows_f32(FAKE, 64, FAKE, 64, 2, 64, None, 1, 0.0, None, 0, None),
     lambda L: L.jinf_softmax_rows_f32(FAKE, 64, FAKE, 64, 2, 64, FAKE, 0, 1.0, None),
     lambda L: L.jinf_softmax_rows_f32(FAKE, 64, FAKE, 64, 2, 64, None, 1, float("nan"), None),
     lambda L: L.jinf_embed_q4_0(FAKE, 100, FAKE, 10, 100, FAKE, 4, 1, None),
@@ -84,12 +84,12 @@ FAKE = P(0x1000)  # never dereferenced: every call below is rejected on the host
     lambda L: L.jinf_dequant_rows(FAKE, 256, FAKE, 14, 10, 256, None, 11, 0, None),
     # attention: lens missing, n_heads not a multiple of n_heads_kv, bad scale,
     # ld_pos below one position, kv type, head_dim too large
-    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 0, 128, 4096, None, 2, 32, 128, 2, 1, 0.0, None),
-    lambda L: L.jinf_attention_decode(FAKE, 384, FAKE, 384, FAKE, FAKE, 0, 256, 8192, FAKE, 2, 32, 128, 3, 2, 0.0, None),
-    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 0, 128, 4096, FAKE, 2, 32, 128, 2, 1, -1.0, None),
-    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 0, 64, 4096, FAKE, 2, 32, 128, 2, 1, 0.0, None),
-    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 7, 128, 4096, FAKE, 2, 32, 128, 2, 1, 0.0, None),
-    lambda L: L.jinf_attention_decode(FAKE, 4096, FAKE, 4096, FAKE, FAKE, 0, 2048, 65536, FAKE, 2, 32, 2048, 2, 1, 0.0, None),
+    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 0, 128, 4096, None, 2, 32, 128, 2, 1, 0.0, None, 0, None),
+    lambda L: L.jinf_attention_decode(FAKE, 384, FAKE, 384, FAKE, FAKE, 0, 256, 8192, FAKE, 2, 32, 128, 3, 2, 0.0, None, 0, None),
+    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 0, 128, 4096, FAKE, 2, 32, 128, 2, 1, -1.0, None, 0, None),
+    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 0, 64, 4096, FAKE, 2, 32, 128, 2, 1, 0.0, None, 0, None),
+    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 7, 128, 4096, FAKE, 2, 32, 128, 2, 1, 0.0, None, 0, None),
+    lambda L: L.jinf_attention_decode(FAKE, 4096, FAKE, 4096, FAKE, FAKE, 0, 2048, 65536, FAKE, 2, 32, 2048, 2, 1, 0.0, None, 0, None),
 ])
 def test_invalid_arguments_rejected_on_host(call):
     assert call(jinf_amd.lib()) == _lib.JINF_HIP_ERR_INVALID
@@ -104,7 +104,7 @@ def test_invalid_arguments_rejected_on_host(call):
     lambda L: L.jinf_matvec_q4_0(FAKE, FAKE, FAKE, 0, 128, None),
     lambda L: L.jinf_matvec(FAKE, 14, FAKE, FAKE, 16, 0, None),
     lambda L: L.jinf_dequant_rows(FAKE, 256, FAKE, 12, 10, 256, FAKE, 0, 0, None),
-    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 0, 128, 4096, FAKE, 0, 32, 128, 2, 1, 0.0, None),
+    lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 0, 128, 4096, FAKE, 0, 32, 128, 2, 1, 0.0, None, 0, None),
 ])
 def test_empty_work_is_ok_and_enqueues_nothing(call):
     assert call(jinf_amd.lib()) == _lib.JINF_HIP_OK

@@ -67,10 +67,11 @@ def test_drop_in_no_op_for_empty_context(dev):
     assert np.all(host(out) == -3.0)
 
 
-# (n_seq, max_ctx, n_heads, n_heads_kv, head_dim, kv dtype): covers one query
-# head per workgroup (few pairs), GQA groups of 2/4/8 per workgroup (>= 128
-# (sequence, kv head) pairs), head_dim 64 and 128, the generic kernel
-# (head_dim 96), fp32 and fp16 caches.
+# (n_seq, max_ctx, n_heads, n_heads_kv, head_dim, kv dtype): fp16 caches run
+# the matrix-core kernel (GQA groups of 8, 4, 2 and 1 query heads per
+# workgroup slot set, head_dim 64 and 128); fp32 caches the VALU kernel (one
+# query head per workgroup for few (sequence, kv head) pairs, groups of 4
+# otherwise); head_dim 96 and 80 the generic kernel.
 CASES = [(8, 8192, 64, 8, 128, np.float16),   # 70B heads, long ragged contexts
          (16, 2048, 64, 8, 128, np.float16),  # G = 8
          (16, 1024, 32, 8, 128, np.float32),  # G = 4
@@ -120,3 +121,31 @@ def test_explicit_scale_and_single_position(dev):
     ref, a = oracle.attention(q, k, v, lens, nh, nkv, hd, scale=0.5)
     oracle.set_threads(1)
     check(out, ref, a, "scale 0.5")
+
+
+# Split of long contexts over workgroups through a workspace (fp16 caches):
+# several chunks per sequence, a sequence shorter than one chunk, one that
+# ends exactly on a chunk boundary, and batch 1.
+SPLIT = [(8, 8192, 64, 8, 128), (3, 3000, 32, 8, 128), (1, 8192, 32, 8, 128),
+         (5, 2500, 16, 2, 64)]
+
+
+@pytest.mark.parametrize("n_seq,max_ctx,nh,nkv,hd", SPLIT)
+def test_split_contexts_with_workspace(dev, n_seq, max_ctx, nh, nkv, hd):
+    say(f"jinf_attention_decode + workspace n_seq={n_seq} ctx={max_ctx} heads={nh}/{nkv} hd={hd}")
+    r = tu.rng(n_seq * 13 + max_ctx)
+    lens = r.integers(1, max_ctx + 1, size=n_seq).astype(np.int32)
+    lens[0] = max_ctx
+    if n_seq > 2:
+        lens[1] = 1000
+        lens[2] = 2048
+    q, k, v, kp, vp = make(r, n_seq, max_ctx, nh, nkv, hd, lens, np.float16, qsigma=2.0)
+    ref, a = _oracle(q, k, v, lens, nh, nkv, hd, max_ctx)
+    ws = jinf_amd.attention_workspace(n_seq, nh, hd, max_ctx)
+    assert ws.numel() == n_seq * nh * ((max_ctx + 1023) // 1024) * (hd + 2) * 4
+    qd, kd, vd, ld = to_dev(q), to_dev(kp), to_dev(vp), to_dev(lens)
+    out = host(jinf_amd.attention_decode(qd, kd, vd, ld, nh, nkv, workspace=ws))
+    check(out, ref, a, f"split {n_seq}x{nh}/{nkv}x{hd}")
+    # the same call without a workspace (one work item per sequence)
+    out1 = host(jinf_amd.attention_decode(qd, kd, vd, ld, nh, nkv))
+    check(out1, ref, a, "unsplit")
