@@ -308,6 +308,16 @@ def workload(name, torch, jinf, seed):
                "jinf_cuda_attention: one sequence, 32/8 heads x 128, fp32 cache, n_past 4096",
                "storage": "f32 KV cache", "baseline_configs": [],
                "note": "SURVEY 8(f) f2, batch 1"}
+    elif name == "llama3-8b-attention-b1-f16":
+        lens = torch.full((1,), 8192, dtype=torch.int32, device="cuda")
+        ks = [build_attention(torch, jinf, g, "gqa_attention_b1_f16", 1, 8192, 32, 8, 128, lens,
+                              torch.float16, keep)]
+        cfg = {"workload": name, "dtype": "f32 math, f16 KV cache, f32 q and out",
+               "shapes": "Llama-3-8B decode attention at batch 1 through jinf_attention_decode "
+               "with a workspace (context split over 1024-position chunks): 32/8 heads x 128, "
+               "fp16 cache, 8192 positions",
+               "storage": "f16 KV cache", "baseline_configs": [],
+               "note": "SURVEY 8(f) f2, batch 1 with split contexts"}
     elif name in ("rope", "norm", "swiglu", "gather", "softmax"):
         b = {"rope": lambda: build_rope(torch, jinf, g, 512, 32, 8, 128,
                                         torch.arange(512, dtype=torch.int32, device="cuda"), keep),
@@ -489,11 +499,17 @@ def main():
                     help="also run a plain 256 MiB device copy (PMC scaling reference)")
     ap.add_argument("--rocprof-summary", nargs="+", metavar="DB",
                     help="summarize rocprofv3 result databases and exit (no GPU use)")
+    ap.add_argument("--bytes", nargs="*", metavar="KERNEL=BYTES",
+                    help="with --rocprof-summary: algorithmic bytes per launch of more kernels")
     args = ap.parse_args()
 
     if args.rocprof_summary:
         nb = {"rope": 10487808, "residual_rmsnorm": 67117056, "swiglu": 176160768,
               "q4_0_gather": 43008000, "gemv_down": 33103872}
+        if args.bytes:  # extra "kernel=bytes" pairs (workloads with random shapes)
+            for kv in args.bytes:
+                k, v = kv.split("=")
+                nb[k] = int(v)
         print(rocprof_summary(args.rocprof_summary, nb))
         return
 

@@ -157,8 +157,8 @@ int jinf_dequant_rows(void* out, int ld_out, const void* table, int qtype, int n
  * and strides 16-byte aligned; an fp16 cache then runs on the matrix cores
  * (|q * scale| < 65504).  Nothing is allocated.  workspace (device memory,
  * optional: NULL or too small runs every sequence in one work item) lets an
- * fp16-cache call split contexts longer than 1024 positions over several
- * workgroups; it needs jinf_attention_workspace_bytes(n_seq, n_heads,
+ * fp16-cache call split long contexts (chunks of at least 256 positions)
+ * over several workgroups; it needs jinf_attention_workspace_bytes(n_seq, n_heads,
  * head_dim, max_ctx) bytes, holds no state between calls, and must not be
  * shared by calls running concurrently. */
 int jinf_attention_decode(float* out, int ld_out, const float* q, int ld_q,

@@ -182,19 +182,26 @@ __global__ __launch_bounds__(G == 1 ? 1024 : 256) void attn_decode_kernel(
             for (int i = 0; i < DPL; ++i) acc[g][i] *= corr;
         }
         wave_lds_sync();
-        // P V
+        // P V, 8 positions at a time with their V loads issued together
+        // (rows past the end re-read the last live row; their p is 0)
         const int nt = len - t0 < kAtTile ? len - t0 : kAtTile;
         const TKV* vt = vb + (int64_t)t0 * ld_pos + lane;
-        for (int t = 0; t < nt; ++t) {
-            float vv[DPL];
+        for (int t = 0; t < nt; t += 8) {
+            float vv[8][DPL];
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) vv[i] = KV<TKV>::get(vt + (int64_t)t * ld_pos, i * kWave);
+            for (int u = 0; u < 8; ++u) {
+                const int tt = t + u < nt ? t + u : nt - 1;
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float p = sc[g * kAtTile + t];
-#pragma unroll
-                for (int i = 0; i < DPL; ++i) acc[g][i] = fmaf(p, vv[i], acc[g][i]);
+                for (int i = 0; i < DPL; ++i) vv[u][i] = KV<TKV>::get(vt + (int64_t)tt * ld_pos, i * kWave);
             }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float p = sc[g * kAtTile + t + u];
+#pragma unroll
+                    for (int i = 0; i < DPL; ++i) acc[g][i] = fmaf(p, vv[u][i], acc[g][i]);
+                }
         }
         wave_lds_sync();
     }
@@ -304,7 +311,11 @@ __global__ __launch_bounds__(64) void attn_decode_any_kernel(
 typedef _Float16 am_h4 __attribute__((ext_vector_type(4)));
 typedef float am_f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kAmChunk = 1024;     // positions per work item when a workspace splits them
+// A workspace splits contexts into chunks of kAmChunkMin positions or more,
+// sized so that about kAmTargetItems work items fill the GPU (few, long
+// sequences get short chunks; many sequences long ones).
+constexpr int kAmChunkMin = 256;
+constexpr int kAmTargetItems = 1024;
 constexpr float kAmPScale = 32768.0f;  // 2^15
 
 __device__ __forceinline__ am_h4 am_h4_from(uint32_t lo, uint32_t hi) {
@@ -607,7 +618,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(
 }
 
 static size_t am_workspace_bytes(int n_seq, int n_heads, int head_dim, int max_ctx) {
-    const int64_t nch = ((int64_t)max_ctx + kAmChunk - 1) / kAmChunk;
+    const int64_t nch = ((int64_t)max_ctx + kAmChunkMin - 1) / kAmChunkMin;
     return (size_t)n_seq * n_heads * nch * (head_dim + 2) * sizeof(float);
 }
 
@@ -617,10 +628,16 @@ static int am_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, c
                      int n_past, int n_seq, int n_heads, int group, int G, float scale,
                      void* workspace, size_t ws_bytes, hipStream_t stream) {
     const size_t shmem = (size_t)4 * 2 * kAtTile * HD * 2;  // K and V tile per wave
-    const bool split = workspace && n_past > kAmChunk &&
+    // chunk: a multiple of 64 positions, at least kAmChunkMin, giving about
+    // kAmTargetItems (sequence, head group, chunk) items
+    const int64_t work = (int64_t)n_past * n_seq * (n_heads / G);
+    int64_t ch = (work + kAmTargetItems - 1) / kAmTargetItems;
+    ch = (ch + 63) / 64 * 64;
+    if (ch < kAmChunkMin) ch = kAmChunkMin;
+    const bool split = workspace && n_past > ch &&
                        ws_bytes >= am_workspace_bytes(n_seq, n_heads, HD, n_past);
-    const int nch = split ? (n_past + kAmChunk - 1) / kAmChunk : 1;
-    const int chunk = split ? kAmChunk : (n_past > 0 ? n_past : 1);
+    const int chunk = split ? (int)ch : (n_past > 0 ? n_past : 1);
+    const int nch = split ? (n_past + chunk - 1) / chunk : 1;
     float* ws = split ? static_cast<float*>(workspace) : nullptr;
     int st = launch(attn_mfma_kernel<HD>, dim3(n_heads / G, nch, n_seq), dim3(256), shmem, stream,
                     out, ld_out, q, ld_q, static_cast<const uint16_t*>(k),

@@ -142,7 +142,7 @@ def test_split_contexts_with_workspace(dev, n_seq, max_ctx, nh, nkv, hd):
     q, k, v, kp, vp = make(r, n_seq, max_ctx, nh, nkv, hd, lens, np.float16, qsigma=2.0)
     ref, a = _oracle(q, k, v, lens, nh, nkv, hd, max_ctx)
     ws = jinf_amd.attention_workspace(n_seq, nh, hd, max_ctx)
-    assert ws.numel() == n_seq * nh * ((max_ctx + 1023) // 1024) * (hd + 2) * 4
+    assert ws.numel() == n_seq * nh * ((max_ctx + 255) // 256) * (hd + 2) * 4
     qd, kd, vd, ld = to_dev(q), to_dev(kp), to_dev(vp), to_dev(lens)
     out = host(jinf_amd.attention_decode(qd, kd, vd, ld, nh, nkv, workspace=ws))
     check(out, ref, a, f"split {n_seq}x{nh}/{nkv}x{hd}")
