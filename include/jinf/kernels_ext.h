@@ -33,7 +33,10 @@ extern "C" {
 
 enum jinf_hip_status {
     JINF_HIP_OK = 0,
+    JINF_HIP_ERR_IO = 1,
+    JINF_HIP_ERR_PARSE = 2,
     JINF_HIP_ERR_DEVICE = 3,
+    JINF_HIP_ERR_OOM = 4,
     JINF_HIP_ERR_INVALID = 5
 };
 

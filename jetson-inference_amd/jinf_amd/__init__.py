@@ -32,3 +32,4 @@ from .ops import (  # noqa: F401
     softmax_rows,
     swiglu,
 )
+from . import gguf  # noqa: F401,E402

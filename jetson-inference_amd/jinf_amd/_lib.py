@@ -57,6 +57,29 @@ SIGNATURES = {
     "jinf_attention_decode": (_I, [_P, _I, _P, _I, _P, _P, _I, ctypes.c_int64, ctypes.c_int64,
                                    _P, _I, _I, _I, _I, _I, _F, _P, ctypes.c_size_t, _P]),
     "jinf_attention_workspace_bytes": (ctypes.c_size_t, [_I, _I, _I, _I]),
+    # GGUF files (include/jinf/gguf_hip.h)
+    "jinf_hip_gguf_load": (_I, [ctypes.POINTER(_P), ctypes.c_char_p]),
+    "jinf_hip_gguf_free": (None, [_P]),
+    "jinf_hip_gguf_version": (ctypes.c_uint32, [_P]),
+    "jinf_hip_gguf_alignment": (ctypes.c_uint32, [_P]),
+    "jinf_hip_gguf_data_offset": (ctypes.c_uint64, [_P]),
+    "jinf_hip_gguf_n_kv": (ctypes.c_uint64, [_P]),
+    "jinf_hip_gguf_n_tensors": (ctypes.c_uint64, [_P]),
+    "jinf_hip_gguf_hparams_of": (_P, [_P]),
+    "jinf_hip_gguf_find_kv": (ctypes.c_int64, [_P, ctypes.c_char_p]),
+    "jinf_hip_gguf_kv_key": (ctypes.c_char_p, [_P, ctypes.c_uint64]),
+    "jinf_hip_gguf_kv_type": (_I, [_P, ctypes.c_uint64]),
+    "jinf_hip_gguf_kv_scalar": (_I, [_P, ctypes.c_uint64, _P]),
+    "jinf_hip_gguf_kv_str": (ctypes.c_char_p, [_P, ctypes.c_uint64]),
+    "jinf_hip_gguf_kv_array": (_I, [_P, ctypes.c_uint64, ctypes.POINTER(_I),
+                                    ctypes.POINTER(ctypes.c_uint64)]),
+    "jinf_hip_gguf_get_str": (ctypes.c_char_p, [_P, ctypes.c_char_p, ctypes.c_char_p]),
+    "jinf_hip_gguf_get_u32": (ctypes.c_uint32, [_P, ctypes.c_char_p, ctypes.c_uint32]),
+    "jinf_hip_gguf_get_f32": (_F, [_P, ctypes.c_char_p, _F]),
+    "jinf_hip_gguf_find_tensor": (ctypes.c_int64, [_P, ctypes.c_char_p]),
+    "jinf_hip_gguf_tensor_at": (_P, [_P, ctypes.c_uint64]),
+    "jinf_hip_gguf_upload": (_I, [_P, ctypes.c_uint64, _P, ctypes.c_uint64, _P]),
+    "jinf_hip_q4_0_repack_ggml": (_I, [_P, ctypes.c_int64, _P]),
 }
 
 _lib = None
