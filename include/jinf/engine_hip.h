@@ -1,0 +1,128 @@
+/*
+ * jinf MI355X: the decode engine -- the reference's per-token forward loop
+ * (src/engine.cpp:418-511 per layer, :684-760 per token) running entirely on
+ * this library's kernels, with every weight resident in device memory.
+ *
+ * One token step is: embedding gather; per layer RMSNorm (fused with the
+ * previous residual add), q/k/v dequant-GEMVs, RoPE at position n_past, the
+ * K/V rows written into the layer's cache at n_past, GQA attention over
+ * n_past + 1 positions, output GEMV, residual add fused into the FFN RMSNorm,
+ * gate/up GEMVs, SiLU * up, down GEMV; final residual add + RMSNorm, output
+ * GEMV to the logits, and an on-device greedy argmax.  Positions and lengths
+ * live in device memory, so the whole step is captured once as a HIP graph
+ * and replayed for every token.
+ *
+ * Status codes are jinf_status values (0 OK, 1 I/O, 2 parse, 3 device,
+ * 4 out of memory, 5 invalid argument).  An engine is used by one host
+ * thread at a time.  This header includes no HIP or CUDA header.
+ */
+#ifndef JINF_ENGINE_HIP_H
+#define JINF_ENGINE_HIP_H
+
+#include <stdint.h>
+#include "gguf_hip.h"
+#include "kernels_ext.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct jinf_hip_engine jinf_hip_engine;
+
+/* Device pointers and jinf_qtype codes of one layer's weights, the fields of
+ * jinf_layer_ptrs (include/jinf/engine.h:56-81).  Norm weights are F32 (0)
+ * or F16 (1); matrices are Q4_0 (2), Q8_0 (8), Q4_K (12) or Q6_K (14),
+ * [rows = outputs, cols = inputs] in blocks along the inputs. */
+typedef struct jinf_hip_layer_weights {
+    const void* attn_norm;
+    const void* ffn_norm;
+    const void* attn_q;
+    const void* attn_k;
+    const void* attn_v;
+    const void* attn_output;
+    const void* ffn_gate;
+    const void* ffn_up;
+    const void* ffn_down;
+    int32_t attn_norm_type;
+    int32_t ffn_norm_type;
+    int32_t attn_q_type;
+    int32_t attn_k_type;
+    int32_t attn_v_type;
+    int32_t attn_output_type;
+    int32_t ffn_gate_type;
+    int32_t ffn_up_type;
+    int32_t ffn_down_type;
+} jinf_hip_layer_weights;
+
+/* A model whose weights already sit in device memory (owned by the caller,
+ * who keeps them alive while the engine exists).  token_embd: F32, F16, Q4_0,
+ * Q8_0, Q4_K or Q6_K rows of n_embd; output: a matrix type (NULL: tied to
+ * token_embd).  kv_type: JINF_HIP_F32 (the reference's cache) or JINF_HIP_F16
+ * (attention on the matrix cores). */
+typedef struct jinf_hip_engine_desc {
+    int   n_layers, n_embd, n_heads, n_heads_kv, n_ff, n_vocab, max_context;
+    float rms_norm_eps, rope_freq_base;
+    int   kv_type;
+    const void* token_embd;
+    int32_t     token_embd_type;
+    const void* output_norm;
+    int32_t     output_norm_type;
+    const void* output;
+    int32_t     output_type;
+    const jinf_hip_layer_weights* layers;   /* n_layers entries */
+} jinf_hip_engine_desc;
+
+/* Creates the engine: KV caches [n_layers][max_context][n_heads_kv * head_dim]
+ * (zeroed), activation buffers and its own stream (replaces jinf_engine_create,
+ * src/engine.cpp:40-220, for a resident model). */
+int jinf_hip_engine_create(jinf_hip_engine** out, const jinf_hip_engine_desc* desc);
+
+/* Same from a GGUF file: every tensor the forward loop reads (token_embd,
+ * blk.N.{attn_norm,attn_q,attn_k,attn_v,attn_output,ffn_norm,ffn_gate,ffn_up,
+ * ffn_down}, output_norm, output -- tied to token_embd when absent) is
+ * uploaded into one device allocation the engine owns; hyper-parameters come
+ * from the file.  q4_0_ggml_order != 0 converts Q4_0 tensors written in
+ * upstream ggml's element order to jinf's (jinf_hip_q4_0_repack_ggml). */
+int jinf_hip_engine_create_gguf(jinf_hip_engine** out, const jinf_hip_gguf* file,
+                                int max_context, int kv_type, int q4_0_ggml_order);
+
+void jinf_hip_engine_destroy(jinf_hip_engine* e);
+
+/* Zeroes the KV caches and n_past (jinf_engine_reset, src/engine.cpp:294-302). */
+int jinf_hip_engine_reset(jinf_hip_engine* e);
+
+int jinf_hip_engine_n_past(const jinf_hip_engine* e);
+
+/* Decodes n_tokens tokens one at a time (jinf_engine_forward,
+ * src/engine.cpp:684-760); *logits receives the device pointer of the last
+ * token's n_vocab fp32 logits (valid until the next call).  Returns after the
+ * work has finished.  Status 5 when the context would exceed max_context or
+ * a token id is outside [0, n_vocab). */
+int jinf_hip_engine_forward(jinf_hip_engine* e, const int32_t* tokens, int n_tokens,
+                            const float** logits);
+
+/* Greedy generation (jinf_engine_generate, src/engine.cpp:762-805): the
+ * prompt (if any) is decoded, then up to max_tokens argmax tokens (first
+ * maximum on ties) are emitted and fed back; token 2 (end of sequence) is
+ * emitted and stops generation. */
+int jinf_hip_engine_generate(jinf_hip_engine* e, const int32_t* prompt, int n_prompt,
+                             int32_t* output, int max_tokens, int* n_generated);
+
+/* Copies the first n (<= n_vocab) logits of the last decoded token to dst
+ * (host or device memory) and waits for the copy; the reference's caller
+ * reads them through the device pointer forward returns. */
+int jinf_hip_engine_copy_logits(const jinf_hip_engine* e, float* dst, int n);
+
+/* 1 (default): replay the captured token step as a HIP graph; 0: launch the
+ * kernels one by one (same results). */
+int jinf_hip_engine_use_graph(jinf_hip_engine* e, int on);
+
+/* Bytes of weights one token step reads (every matrix once, one embedding
+ * row, the norms): the numerator of the decode bandwidth. */
+uint64_t jinf_hip_engine_step_weight_bytes(const jinf_hip_engine* e);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JINF_ENGINE_HIP_H */

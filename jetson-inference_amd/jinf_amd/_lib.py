@@ -1,5 +1,4 @@
-"""ctypes binding of libjinf_hip.so, the C-ABI declared in include/jinf/kernels.h
-and include/jinf/kernels_ext.h.
+"""ctypes binding of libjinf_hip.so, the C-ABI declared in include/jinf/*.h.
 
 The library links the HIP runtime by soname (libamdhip64.so.7).  PyTorch ships
 its own copy with the same soname, so torch is imported first: the dynamic
@@ -80,6 +79,17 @@ SIGNATURES = {
     "jinf_hip_gguf_tensor_at": (_P, [_P, ctypes.c_uint64]),
     "jinf_hip_gguf_upload": (_I, [_P, ctypes.c_uint64, _P, ctypes.c_uint64, _P]),
     "jinf_hip_q4_0_repack_ggml": (_I, [_P, ctypes.c_int64, _P]),
+    # decode engine (include/jinf/engine_hip.h)
+    "jinf_hip_engine_create": (_I, [ctypes.POINTER(_P), _P]),
+    "jinf_hip_engine_create_gguf": (_I, [ctypes.POINTER(_P), _P, _I, _I, _I]),
+    "jinf_hip_engine_destroy": (None, [_P]),
+    "jinf_hip_engine_reset": (_I, [_P]),
+    "jinf_hip_engine_n_past": (_I, [_P]),
+    "jinf_hip_engine_forward": (_I, [_P, _P, _I, ctypes.POINTER(_P)]),
+    "jinf_hip_engine_generate": (_I, [_P, _P, _I, _P, _I, ctypes.POINTER(_I)]),
+    "jinf_hip_engine_copy_logits": (_I, [_P, _P, _I]),
+    "jinf_hip_engine_use_graph": (_I, [_P, _I]),
+    "jinf_hip_engine_step_weight_bytes": (ctypes.c_uint64, [_P]),
 }
 
 _lib = None

@@ -1,0 +1,236 @@
+"""GPU parity: the decode engine (include/jinf/engine_hip.h) against the
+oracle's decode loop (oracle/engine.py, pinned against a float64 textbook
+decoder in test_oracle_engine.py) on tiny random models with every weight
+format, GQA grouping and KV-cache type.
+
+Bar: after every token, |logits - logits_oracle| <= TOL * max |logits_oracle|
+with TOL 1e-4 for an fp32 KV cache.  Each stage of the engine agrees with the
+oracle's to within a few fp32 ulps of its operands' scale (the kernels' own
+parity tests); the bar leaves room for those differences to pass through two
+layers and the attention history (measured: up to 1.4e-5).  With an fp16
+cache both sides round K and V to fp16, but a K or V value that differs in
+its last fp32 bits can round to the neighbouring fp16 value, a 2^-11
+relative step that reaches the logits directly: TOL is 4e-4 there (measured:
+up to 4.1e-5).
+A wrong position, cache slot, weight row or residual moves the logits by O(1).
+The captured graph and the kernel-by-kernel path give identical bits, and
+greedy generation reproduces a host-side argmax loop exactly.
+"""
+import numpy as np
+import pytest
+
+import jinf_amd
+import model_util as mu
+from gpu_util import say
+from jinf_amd.engine import Engine, EngineError
+from oracle import engine as oeng
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+TOL_F16_KV = 4e-4
+
+MODELS = {
+    # head_dim 64, 4 query heads on 2 kv heads, every block type
+    "mixed": dict(),
+    # F16 norms, Q4_0 embedding, output tied to the embedding
+    "q4_0-f16norm-tied": dict(types={k: mu.Q4_0 for k in mu.MIXED}, norm_type=mu.F16,
+                              embd_type=mu.Q4_0, tied=True),
+    # head_dim 128, 4 query heads on 1 kv head, F16 embedding table
+    "hd128-gqa4": dict(n_embd=512, n_heads=4, n_heads_kv=1, n_ff=512, embd_type=mu.F16),
+    # head_dim 96 (generic attention kernel), no output norm, F32 embedding
+    "hd96": dict(n_embd=384, n_heads=4, n_heads_kv=2, n_ff=768,
+                 types={k: (mu.Q4_0, mu.Q8_0) for k in mu.MIXED}, embd_type=mu.F32,
+                 out_type=mu.Q8_0, output_norm=False),
+}
+TOKENS = [5, 17, 999, 0, 42, 17, 3, 500]
+
+
+def make_engine(hp, W, max_ctx, kv_type, graph=True):
+    e = Engine(hp, mu.to_device(W), max_ctx, kv_type)
+    e.use_graph(graph)
+    return e
+
+
+def compare(got, ref, what, tol=TOL):
+    scale = float(np.max(np.abs(ref)))
+    err = float(np.max(np.abs(got.astype(np.float64) - ref.astype(np.float64))))
+    say(f"{what}: max error / max |logit| = {err / scale:.2e}")
+    assert np.all(np.isfinite(got)), what
+    assert err <= tol * scale, what
+
+
+@pytest.mark.parametrize("kv_type", [mu.F32, mu.F16], ids=["kv-f32", "kv-f16"])
+@pytest.mark.parametrize("name", list(MODELS))
+def test_decode_matches_oracle(dev, name, kv_type):
+    say(f"engine decode {name} kv={'f16' if kv_type else 'f32'}")
+    hp, W = mu.tiny_model(seed=11, **MODELS[name])
+    ref = oeng.Decoder(hp, W, max_context=16, kv_type=kv_type)
+    with make_engine(hp, W, 16, kv_type) as e:
+        for t, tok in enumerate(TOKENS):
+            e.forward([tok])
+            assert e.n_past == t + 1
+            compare(e.logits(), ref.step(tok), f"{name} token {t}",
+                    TOL_F16_KV if kv_type == mu.F16 else TOL)
+
+
+def test_graph_eager_and_batched_calls_identical(dev):
+    say("graph replay vs kernel-by-kernel vs one multi-token call")
+    hp, W = mu.tiny_model(seed=12)
+    with make_engine(hp, W, 16, mu.F16, graph=True) as g, \
+            make_engine(hp, W, 16, mu.F16, graph=False) as k:
+        for tok in TOKENS:
+            g.forward([tok])
+            k.forward([tok])
+            assert np.array_equal(g.logits().view(np.uint32), k.logits().view(np.uint32))
+        last = g.logits()
+        g.reset()
+        assert g.n_past == 0
+        g.forward(TOKENS)
+        assert g.n_past == len(TOKENS)
+        assert np.array_equal(g.logits().view(np.uint32), last.view(np.uint32))
+
+
+def test_long_context_split_attention(dev):
+    """fp16 cache over 600 positions: the attention splits the context over
+    several workgroups per head; logits checked around the split boundaries."""
+    say("engine decode 600 tokens, head_dim 128, fp16 cache")
+    hp, W = mu.tiny_model(seed=13, n_embd=512, n_heads=4, n_heads_kv=2, n_ff=512, n_layers=1,
+                          n_vocab=512)
+    toks = [int(t) for t in np.random.default_rng(13).integers(0, 512, size=600)]
+    ref = oeng.Decoder(hp, W, max_context=640, kv_type=mu.F16)
+    refs = [ref.step(t) for t in toks]
+    with make_engine(hp, W, 640, mu.F16) as e:
+        done = 0
+        for t in (0, 255, 256, 257, 511, 512, 599):
+            e.forward(toks[done:t + 1])
+            done = t + 1
+            compare(e.logits(), refs[t], f"position {t}", TOL_F16_KV)
+
+
+def test_generate_matches_host_greedy_loop(dev):
+    say("greedy generation vs forward + host argmax")
+    hp, W = mu.tiny_model(seed=14, n_vocab=300)
+    prompt = [7, 8, 9]
+    with make_engine(hp, W, 32, mu.F32) as a, make_engine(hp, W, 32, mu.F32) as b:
+        out = a.generate(prompt, 12)
+        b.forward(prompt)
+        want = []
+        for _ in range(12):
+            best = oeng.first_argmax(b.logits())
+            want.append(best)
+            if best == oeng.EOS:
+                break
+            b.forward([best])
+        assert out == want
+        assert a.n_past == b.n_past == len(prompt) + len(out) - (out[-1] == oeng.EOS)
+        # continuing without a prompt picks up the last step's argmax
+        more = a.generate([], 3)
+        nxt = oeng.first_argmax(b.logits())
+        assert more[0] == nxt
+        # the oracle agrees wherever its top-2 gap exceeds the parity bar
+        ref = oeng.Decoder(hp, W, max_context=32)
+        lg = ref.forward(prompt)
+        for tok in out:
+            srt = np.sort(lg)[::-1]
+            if srt[0] - srt[1] > 2 * TOL * np.max(np.abs(lg)):
+                assert tok == oeng.first_argmax(lg)
+            lg = ref.step(tok)
+
+
+def pass_through_model(n_vocab=64, n_embd=256):
+    """Every layer matrix zero (the residual stream keeps the embedding), an
+    output norm keeping only element 0, and an output matrix whose row 2 reads
+    element 0: token 2 (end of sequence) wins for every input."""
+    hp = dict(n_layers=2, n_embd=n_embd, n_heads=4, n_heads_kv=2, n_ff=256, n_vocab=n_vocab,
+              rope_freq_base=10000.0, rms_norm_eps=1e-5)
+    kvd = 2 * (n_embd // 4)
+    zeros = lambda r, c: (np.zeros((r, c // 32 * 18), np.uint8), mu.Q4_0)  # noqa: E731
+    W = {"token_embd.weight": (np.abs(np.random.default_rng(1).normal(size=(n_vocab, n_embd)))
+                               .astype(np.float32) + 0.1, mu.F32)}
+    shapes = {"attn_q": (n_embd, n_embd), "attn_k": (kvd, n_embd), "attn_v": (kvd, n_embd),
+              "attn_output": (n_embd, n_embd), "ffn_gate": (256, n_embd),
+              "ffn_up": (256, n_embd), "ffn_down": (n_embd, 256)}
+    for L in range(2):
+        for n in mu.LAYER_TENSORS:
+            W[f"blk.{L}.{n}.weight"] = ((np.ones(n_embd, np.float32), mu.F32) if n.endswith("norm")
+                                        else zeros(*shapes[n]))
+    g = np.zeros(n_embd, np.float32)
+    g[0] = 1.0
+    W["output_norm.weight"] = (g, mu.F32)
+    out = np.zeros((n_vocab, n_embd // 32, 34), np.uint8)
+    out[2, 0, 0:2] = np.array([1.0], np.float16).view(np.uint8)
+    out[2, 0, 2] = 1
+    W["output.weight"] = (out.reshape(n_vocab, -1), mu.Q8_0)
+    return hp, W
+
+
+def test_generate_stops_at_eos(dev):
+    say("generation stops after emitting token 2")
+    hp, W = pass_through_model()
+    with make_engine(hp, W, 16, mu.F32) as e:
+        assert e.generate([5, 6], 10) == [oeng.EOS]
+        assert e.n_past == 2
+        lg = e.logits()
+        assert lg[2] > 0 and np.all(np.delete(lg, 2) == 0)
+
+
+def test_generate_stops_at_context_end(dev):
+    say("generation stops when the cache is full")
+    hp, W = mu.tiny_model(seed=15, n_vocab=64, n_layers=1)
+    ref = oeng.Decoder(hp, W, max_context=6)
+    want = ref.generate([1, 2, 3, 4], 10)
+    with make_engine(hp, W, 6, mu.F32) as e:
+        out = e.generate([1, 2, 3, 4], 10)
+        assert len(out) == len(want) and e.n_past == ref.n_past == 6
+        with pytest.raises(EngineError) as ex:
+            e.forward([1])
+        assert ex.value.status == 5
+
+
+def test_forward_rejects_bad_tokens_and_overflow(dev):
+    hp, W = mu.tiny_model(seed=16, n_vocab=64, n_layers=1)
+    with make_engine(hp, W, 4, mu.F32) as e:
+        for bad in ([64], [-1], [1, 2, 3, 4, 5]):
+            with pytest.raises(EngineError) as ex:
+                e.forward(bad)
+            assert ex.value.status == 5
+            assert e.n_past == 0
+        with pytest.raises(EngineError):
+            e.generate([], 3)        # nothing decoded yet
+        e.forward([1, 2, 3, 4])
+        assert e.n_past == 4
+
+
+def test_step_weight_bytes(dev):
+    hp, W = mu.tiny_model(seed=17)
+    want = sum(a.nbytes for k, (a, _) in W.items() if k != "token_embd.weight")
+    emb = W["token_embd.weight"][0]
+    want += emb.nbytes // emb.shape[0]
+    with make_engine(hp, W, 8, mu.F32) as e:
+        assert e.step_weight_bytes == want
+
+
+@pytest.mark.parametrize("ggml_order", [False, True], ids=["jinf-order", "ggml-order"])
+def test_gguf_engine_matches_resident_weights(dev, tmp_path, ggml_order):
+    say(f"engine from a GGUF file, Q4_0 in {'ggml' if ggml_order else 'jinf'} order")
+    hp, W = mu.tiny_model(seed=18, embd_type=mu.Q4_0)
+    path = tmp_path / "tiny.gguf"
+    mu.write_gguf(str(path), hp, W, q4_0_ggml_order=ggml_order)
+    with make_engine(hp, W, 16, mu.F16) as a, \
+            Engine.from_gguf(str(path), 16, mu.F16, q4_0_ggml_order=ggml_order) as b:
+        assert b.step_weight_bytes == a.step_weight_bytes
+        for tok in TOKENS:
+            a.forward([tok])
+            b.forward([tok])
+            assert np.array_equal(a.logits().view(np.uint32), b.logits().view(np.uint32))
+
+
+def test_gguf_missing_tensor(dev, tmp_path):
+    hp, W = mu.tiny_model(seed=19, n_layers=1)
+    del W["blk.0.ffn_up.weight"]
+    path = tmp_path / "broken.gguf"
+    mu.write_gguf(str(path), hp, W)
+    with pytest.raises(EngineError) as ex:
+        Engine.from_gguf(str(path), 16)
+    assert ex.value.status == 2
