@@ -333,6 +333,164 @@ def workload(name, torch, jinf, seed):
 
 
 # --------------------------------------------------------------------------
+# decode engine: Llama-3-8B-shaped random weights resident in HBM, one token
+# per step through jinf_hip_engine (include/jinf/engine_hip.h)
+# --------------------------------------------------------------------------
+
+ENGINE_MODELS = {
+    # llama.cpp's Q4_0 file layout: Q4_0 everywhere, Q6_K output
+    "llama3-8b-decode": dict(mat=dict.fromkeys(("attn_q", "attn_k", "attn_v", "attn_output",
+                                                "ffn_gate", "ffn_up", "ffn_down"), 2),
+                             embd=2, out=14, desc="Q4_0 weights, Q6_K output"),
+    # Q4_K_M: Q4_K, with Q6_K for attn_v and ffn_down, Q6_K output
+    "llama3-8b-decode-q4_k_m": dict(mat=dict(attn_q=12, attn_k=12, attn_v=14, attn_output=12,
+                                             ffn_gate=12, ffn_up=12, ffn_down=14),
+                                    embd=12, out=14,
+                                    desc="Q4_K weights, Q6_K for attn_v, ffn_down and output"),
+}
+LLAMA3_8B = dict(n_layers=32, n_embd=4096, n_heads=32, n_heads_kv=8, n_ff=14336,
+                 n_vocab=128256, rope_freq_base=500000.0, rms_norm_eps=1e-5)
+PROMPT = [1, 450, 4696, 310, 2834, 338]   # the reference bench's prompt ids
+
+
+def engine_weights(torch, g, spec, hp):
+    """{GGUF name: (device tensor, qtype)} of a random Llama-3-8B-shaped model."""
+    H, F, V = hp["n_embd"], hp["n_ff"], hp["n_vocab"]
+    KV = hp["n_heads_kv"] * (H // hp["n_heads"])
+    shapes = dict(attn_q=(H, H), attn_k=(KV, H), attn_v=(KV, H), attn_output=(H, H),
+                  ffn_gate=(F, H), ffn_up=(F, H), ffn_down=(H, F))
+    W = {"token_embd.weight": (quant_table(torch, spec["embd"], V, H, g), spec["embd"]),
+         "output.weight": (quant_table(torch, spec["out"], V, H, g), spec["out"]),
+         "output_norm.weight": (torch.randn(H, generator=g, device="cuda") * 0.05 + 1.0, 0)}
+    for L in range(hp["n_layers"]):
+        for n in ("attn_norm", "ffn_norm"):
+            W[f"blk.{L}.{n}.weight"] = (torch.randn(H, generator=g, device="cuda") * 0.05 + 1.0, 0)
+        for n, (rows, cols) in shapes.items():
+            W[f"blk.{L}.{n}.weight"] = (quant_table(torch, spec["mat"][n], rows, cols, g),
+                                        spec["mat"][n])
+    return W
+
+
+def engine_cpu_baseline(W, hp, spec, threads, budget_s):
+    """The oracle's decode loop (oracle/engine.py) on a host copy of the
+    weights: the prompt, then greedy tokens until the budget is spent."""
+    sys.path.insert(0, ROOT)
+    import oracle
+    from oracle import engine as oeng
+
+    oracle.set_threads(threads)
+    Wh = {k: (t.cpu().numpy(), qt) for k, (t, qt) in W.items()}
+    dec = oeng.Decoder(hp, Wh, max_context=64, kv_type=1)
+    times = []
+    tok = PROMPT[0]
+    t_end = time.perf_counter() + budget_s
+    for i in range(60):
+        t0 = time.perf_counter()
+        lg = dec.step(tok)
+        times.append(time.perf_counter() - t0)
+        tok = PROMPT[i + 1] if i + 1 < len(PROMPT) else oeng.first_argmax(lg)
+        if time.perf_counter() > t_end and len(times) >= 2:
+            break
+    med = sorted(times)[len(times) // 2]
+    return med, len(times)
+
+
+def engine_bench(args, torch, jinf_amd):
+    spec = ENGINE_MODELS[args.workload]
+    hp = dict(LLAMA3_8B)
+    max_ctx = 8192
+    g = torch.Generator(device="cuda")
+    g.manual_seed(args.seed)
+    W = engine_weights(torch, g, spec, hp)
+    torch.cuda.synchronize()
+    from jinf_amd.engine import Engine
+
+    e = Engine(hp, W, max_ctx, jinf_amd.F16)
+    e.use_graph(not args.no_graph)
+    wbytes = e.step_weight_bytes
+    kvd = hp["n_heads_kv"] * hp["n_embd"] // hp["n_heads"]
+    log(f"engine ready: {wbytes / 1e9:.3f} GB of weights read per token")
+
+    # prefill as in the reference bench (6 prompt tokens, one forward call)
+    t0 = time.perf_counter()
+    e.forward(PROMPT)
+    prefill_s = time.perf_counter() - t0
+    for _ in range(max(1, args.warmup)):
+        e.forward([PROMPT[-1]])
+    # timed decode steps: K tokens in one forward call (each step is the
+    # captured graph; one synchronization at the end)
+    toks = [int(t) for t in torch.randint(0, hp["n_vocab"], (args.steps,), generator=g,
+                                          device="cuda").cpu()]
+    start_pos = e.n_past
+    t0 = time.perf_counter()
+    e.forward(toks)
+    dec_s = time.perf_counter() - t0
+    ms_tok = dec_s / args.steps * 1e3
+    mean_ctx = start_pos + (args.steps + 1) / 2
+    kv_bytes = 2 * hp["n_layers"] * kvd * 2 * mean_ctx      # fp16 K and V rows read
+    step_bytes = wbytes + kv_bytes
+    # greedy generation through jinf_hip_engine_generate (per-token host
+    # read of the argmax, as the reference's generate loop)
+    n_gen = min(args.steps, max_ctx - e.n_past - 1)
+    t0 = time.perf_counter()
+    out = e.generate([], n_gen)
+    gen_s = time.perf_counter() - t0
+    log(f"token steps decoded in this run: {e.n_past}")
+    e.close()
+
+    gbs = step_bytes / (ms_tok * 1e-3) / 1e9
+    cpu = None
+    if args.cpu_seconds > 0:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        try:
+            med, runs = engine_cpu_baseline(W, hp, spec, threads, args.cpu_seconds)
+            cpu = {"value": round(wbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+                   "kind": "port", "tokens_per_s": round(1.0 / med, 4), "runs": runs,
+                   "sample": f"oracle decode loop (oracle/engine.py, C kernels -O3, {threads} "
+                             f"OpenMP threads) on a host copy of the same weights: the prompt "
+                             f"and greedy tokens, median of {runs} tokens, "
+                             f"{args.cpu_seconds:.0f} s budget",
+                   "cpu_model": cpu_model()}
+        except Exception as exc:  # the baseline is reported, never required
+            log(f"cpu baseline failed: {exc!r}")
+    out_line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_tok, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 math, " + spec["desc"] + ", f16 KV cache",
+        "data": "synthetic: random Llama-3-8B-shaped weights (seeded torch RNG on device, block "
+                "bytes uniform, fp16 scales |N(0,0.02)|), random token ids",
+        "config": {"workload": args.workload,
+                   "shapes": "Llama-3-8B: 32 layers, hidden 4096, 32/8 heads x 128, FFN 14336, "
+                             "vocab 128256, batch 1 decode",
+                   "storage": spec["desc"] + ", f16 KV cache (max_context 8192)",
+                   "step": "one token through every layer (jinf_hip_engine_forward), captured "
+                           "HIP graph replayed per token",
+                   "tokens_per_s": round(1e3 / ms_tok, 2),
+                   "generate_tokens_per_s": round(len(out) / gen_s, 2) if out else None,
+                   "generated": len(out),
+                   "prefill_6_tokens_ms": round(prefill_s * 1e3, 3),
+                   "weight_bytes_per_token": wbytes,
+                   "kv_bytes_per_token_mean": int(kv_bytes),
+                   "context": [start_pos, start_pos + args.steps],
+                   "baseline_configs": [], "note": "SURVEY 8(f) f4, the engine forward loop"},
+        "frac_of_peak": round(gbs / PEAK_GBS, 4),
+        "launch": "eager stream" if args.no_graph else "HIP graph per token",
+        "wall_s_timed": round(dec_s, 4),
+        "roofline": {"bound": "hbm", "kernel": "decode step (every kernel of one token)",
+                     "achieved": round(gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_GBS, 4), "bytes_per_launch": int(step_bytes),
+                     "avg_launch_us": round(ms_tok * 1e3, 3),
+                     "traffic": traffic_from_profiles("decode_step", args.workload)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out_line), flush=True)
+
+
+# --------------------------------------------------------------------------
 # CPU baseline: the oracle (a C restatement of the reference arithmetic) on
 # the host cores, same workload shapes, on a copy of buffer set 0
 # --------------------------------------------------------------------------
@@ -393,7 +551,44 @@ def calibrate_copy(torch, reps=5):
     torch.cuda.synchronize()
 
 
-def rocprof_summary(dbs, bytes_per_kernel):
+def clean_kernel(name):
+    """Kernel name without its parameter list (templates kept)."""
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            return name[:i]
+    return name
+
+
+def per_step_table(dbs, steps):
+    """Every kernel of the run grouped by name: dispatches per step and GPU
+    microseconds per step (sum of dispatch durations / steps)."""
+    import sqlite3
+
+    tot = {}
+    for db in dbs:
+        c = sqlite3.connect(db)
+        for name, n, total in c.execute("select name, count(*), sum(duration) from kernels "
+                                        "group by name"):
+            k = clean_kernel(name)
+            a = tot.setdefault(k, [0, 0.0])
+            a[0] += n
+            a[1] += total
+    all_us = sum(v[1] for v in tot.values()) / 1e3 / steps
+    out = [f"per step ({steps} steps profiled; all dispatches of the run divided by the step "
+           f"count): {all_us:.1f} us of kernel time per step",
+           f"  {'kernel':72s} {'calls/step':>10s} {'us/step':>9s} {'share':>6s}"]
+    for k, (n, total) in sorted(tot.items(), key=lambda kv: -kv[1][1]):
+        us = total / 1e3 / steps
+        out.append(f"  {k[:72]:72s} {n / steps:10.2f} {us:9.1f} {us / all_us:6.1%}")
+    return out
+
+
+def rocprof_summary(dbs, bytes_per_kernel, steps=0):
     """Text summary of rocprofv3 databases: per-kernel dispatch durations and,
     for --pmc runs, per-dispatch FETCH_SIZE / WRITE_SIZE (KiB), the copy
     calibration factors, and the resulting HBM bytes per launch."""
@@ -424,6 +619,8 @@ def rocprof_summary(dbs, bytes_per_kernel):
             key = short_kernel(name)
             if key:
                 ctrs[(key, cn)] = (v, n)
+    if steps:
+        lines += per_step_table(dbs, steps)
     lines.append("kernel durations (rocprofv3 --kernel-trace), microseconds:")
     lines.append(f"  {'kernel':44s} {'calls':>6s} {'avg':>9s} {'min':>9s} {'max':>9s}")
     for k, (n, avg, mn, mx) in sorted(durs.items()):
@@ -501,6 +698,9 @@ def main():
                     help="summarize rocprofv3 result databases and exit (no GPU use)")
     ap.add_argument("--bytes", nargs="*", metavar="KERNEL=BYTES",
                     help="with --rocprof-summary: algorithmic bytes per launch of more kernels")
+    ap.add_argument("--per-step", type=int, default=0, metavar="STEPS",
+                    help="with --rocprof-summary: also every kernel's time per step, the run "
+                         "holding STEPS steps")
     args = ap.parse_args()
 
     if args.rocprof_summary:
@@ -510,7 +710,7 @@ def main():
             for kv in args.bytes:
                 k, v = kv.split("=")
                 nb[k] = int(v)
-        print(rocprof_summary(args.rocprof_summary, nb))
+        print(rocprof_summary(args.rocprof_summary, nb, args.per_step))
         return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -527,6 +727,9 @@ def main():
     jinf_amd.lib()
     torch.cuda.set_device(0)
     log(f"{jinf_amd.version()} on {torch.cuda.get_device_name(0)}; workload {args.workload}")
+    if args.workload in ENGINE_MODELS:
+        engine_bench(args, torch, jinf_amd)
+        return
     ks, cfg, keep = workload(args.workload, torch, jinf_amd, args.seed)
     torch.cuda.synchronize()
     log("buffers ready: " + ", ".join(f"{k.name} x{len(k.launches)} sets" for k in ks))

@@ -136,6 +136,53 @@ int jinf_matvec(const void* weight, int qtype, const float* x, float* y, int row
 int jinf_matvec_q4_0(const void* weight, const float* x, float* y, int rows, int cols,
                      hipStream_t stream);
 
+/* ---- Dequant-GEMVs fused with the launches around them in the reference's
+ * per-layer sequence (src/engine.cpp:418-511, :736-747).  Same weights and
+ * formats as jinf_matvec; each result equals the unfused sequence's up to the
+ * fp32 rounding of the dot products.  Vectors are fp32, 4-byte aligned; the
+ * fast path wants weights, h/x and g 16-byte aligned, cols a multiple of 256
+ * (2048 for Q6_K) and at most 28672, any other shape runs a slower generic
+ * kernel.  No output may overlap an input. ---- */
+
+/* y = W x^ with x^_j = fl32(fl32(h_j * rs) * g_j), rs = 1/sqrt(sum h^2 / cols
+ * + eps) (the RMSNorm of jinf_rmsnorm_rows, computed inside the GEMV):
+ * the attention / FFN / final RMSNorm and the GEMV that reads its output
+ * (src/engine.cpp:429+432, :487+489, :738+744).  norm_w NULL: x^ = h (plain
+ * GEMV).  norm_type: 0 fp32, 1 fp16 weights g. */
+int jinf_rmsnorm_matvec(const void* weight, int qtype, const float* h, const void* norm_w,
+                        int norm_type, float eps, float* y, int rows, int cols,
+                        hipStream_t stream);
+
+/* y[r] = y[r] + (W x)[r]: a projection and the residual add that follows it
+ * (output projection + residual, src/engine.cpp:461-466; down + residual,
+ * :504-508). */
+int jinf_matvec_add(const void* weight, int qtype, const float* x, float* y, int rows,
+                    int cols, hipStream_t stream);
+
+/* out[i] = silu(g_i) * u_i with g = W_gate x^, u = W_up x^ (x^ as in
+ * jinf_rmsnorm_matvec; SiLU as jinf_cuda_silu_mul): the FFN RMSNorm, gate and
+ * up GEMVs and SiLU * up of src/engine.cpp:487-502 in one launch; only the
+ * n_ff products are written.  Both matrices [n_ff, cols] of qtype. */
+int jinf_rmsnorm_swiglu_matvec(const void* w_gate, const void* w_up, int qtype, const float* h,
+                               const void* norm_w, int norm_type, float eps, float* out,
+                               int n_ff, int cols, hipStream_t stream);
+
+/* Attention input side of one token at position *pos (device int32)
+ * (src/engine.cpp:429-453): with x^ as in jinf_rmsnorm_matvec,
+ *   q_out           = RoPE(W_q x^)       [n_heads * head_dim]
+ *   k_cache row pos = RoPE(W_k x^)       [n_heads_kv * head_dim]
+ *   v_cache row pos = W_v x^
+ * RoPE as jinf_rope_rows at position *pos; the cache rows are
+ * k_cache/v_cache + pos * n_heads_kv * head_dim elements of kv_type (F32, or
+ * F16 rounded once); *pos outside [0, max_ctx) skips the cache stores.  A
+ * NULL weight skips its projection; the others share qtype and cols.
+ * head_dim even, <= 512. */
+int jinf_rmsnorm_qkv_rope(const void* w_q, const void* w_k, const void* w_v, int qtype,
+                          const float* h, const void* norm_w, int norm_type, float eps, int cols,
+                          float* q_out, void* k_cache, void* v_cache, int kv_type,
+                          const int32_t* pos, int max_ctx, int head_dim, int n_heads,
+                          int n_heads_kv, float freq_base, hipStream_t stream);
+
 /* Gather + dequant of table rows for any qtype above (the engine's embedding
  * dispatch by table type, src/engine.cpp:311-334): output row i (ld_out
  * elements apart) is table row ids[i] (row i when ids is NULL), n_embd values

@@ -43,7 +43,7 @@ __device__ __forceinline__ float ew_apply(float a, float b) {
     if constexpr (OP == kAdd) {
         return a + b;
     } else if constexpr (OP == kSwigluExact) {
-        return (a / (1.0f + expf(-a))) * b;
+        return swiglu_exact(a, b);
     } else {
         const float e = __builtin_amdgcn_exp2f(a * -1.44269504088896340736f);
         return (a * __builtin_amdgcn_rcpf(1.0f + e)) * b;

@@ -68,28 +68,6 @@ __global__ __launch_bounds__(256) void eng_embed_dense_kernel(float* __restrict_
     out[i] = v;
 }
 
-// The token's K and V rows into the layer's cache at the current position
-// (src/engine.cpp:441-453); an fp16 cache stores one RNE rounding of each.
-template <typename T>
-__global__ __launch_bounds__(256) void eng_kv_store_kernel(T* __restrict__ kc, T* __restrict__ vc,
-                                                           const float* __restrict__ k,
-                                                           const float* __restrict__ v,
-                                                           int kv_dim,
-                                                           const int32_t* __restrict__ st,
-                                                           int max_ctx) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    const int pos = st[kPos];
-    if (i >= kv_dim || pos < 0 || pos >= max_ctx) return;
-    const int64_t o = (int64_t)pos * kv_dim + i;
-    if constexpr (sizeof(T) == 2) {
-        kc[o] = f2h(k[i]);
-        vc[o] = f2h(v[i]);
-    } else {
-        kc[o] = k[i];
-        vc[o] = v[i];
-    }
-}
-
 // (bv, bi) <- (v, i) if v is larger, or equal with a smaller index.  A NaN v
 // is never taken, and bv never becomes NaN.
 __device__ __forceinline__ void take(float& bv, int& bi, float v, int i) {
@@ -197,8 +175,8 @@ struct jinf_hip_engine {
     char* act = nullptr;            // activations, argmax partials, tokens, state
     char* kv = nullptr;             // K caches, then V caches
     size_t kv_layer_bytes = 0;
-    float *hidden = nullptr, *norm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
-    float *attn = nullptr, *delta = nullptr, *gate = nullptr, *up = nullptr, *logits = nullptr;
+    float *hidden = nullptr, *q = nullptr, *attn = nullptr, *gate = nullptr, *up = nullptr;
+    float* logits = nullptr;
     float* part_v = nullptr;
     int32_t *part_i = nullptr, *tokens = nullptr, *state = nullptr;
     void* ws = nullptr;
@@ -240,9 +218,35 @@ int enqueue_embed(jinf_hip_engine* e) {
                              d.n_embd, e->state + kTok, 1, JINF_HIP_F32, e->stream);
 }
 
+// Q, K and V projections of one layer with their RMSNorm, RoPE and cache
+// stores; matrices of one weight format share a launch.
+int enqueue_qkv(jinf_hip_engine* e, const jinf_hip_layer_weights& w, void* kc, void* vc) {
+    const jinf_hip_engine_desc& d = e->d;
+    const void* W[3] = {w.attn_q, w.attn_k, w.attn_v};
+    const int T[3] = {w.attn_q_type, w.attn_k_type, w.attn_v_type};
+    bool done[3] = {false, false, false};
+    for (int i = 0; i < 3; ++i) {
+        if (done[i]) continue;
+        const void* p[3] = {nullptr, nullptr, nullptr};
+        for (int j = i; j < 3; ++j)
+            if (!done[j] && T[j] == T[i]) {
+                p[j] = W[j];
+                done[j] = true;
+            }
+        ENG_TRY(jinf_rmsnorm_qkv_rope(p[0], p[1], p[2], T[i], e->hidden, w.attn_norm,
+                                      w.attn_norm_type, d.rms_norm_eps, d.n_embd, e->q, kc, vc,
+                                      d.kv_type, e->state + kPos, d.max_context, e->head_dim,
+                                      d.n_heads, d.n_heads_kv, d.rope_freq_base, e->stream));
+    }
+    return JINF_HIP_OK;
+}
+
 // One token step: every launch of src/engine.cpp:692-749 for a model whose
-// layers are all resident, with the residual adds fused into the RMSNorm
-// that follows each of them (same stored values as the separate launches).
+// layers are all resident.  Each RMSNorm runs inside the GEMVs that read its
+// output, each residual add inside the GEMV that produces its addend, RoPE
+// and the cache stores inside the Q/K/V GEMV, SiLU * up inside the gate/up
+// GEMV: per layer one Q/K/V launch (more when the three use different
+// formats), attention, and three GEMVs.
 int enqueue_step(jinf_hip_engine* e) {
     const jinf_hip_engine_desc& d = e->d;
     hipStream_t s = e->stream;
@@ -253,67 +257,37 @@ int enqueue_step(jinf_hip_engine* e) {
     ENG_TRY(enqueue_embed(e));
     for (int L = 0; L < d.n_layers; ++L) {
         const jinf_hip_layer_weights& w = e->layers[L];
-        // attention RMSNorm (src/engine.cpp:429); from layer 1 on it first adds
-        // the previous layer's FFN output to the residual stream (:508)
-        if (L == 0)
-            ENG_TRY(jinf_rmsnorm_rows(e->norm, n, e->hidden, n, w.attn_norm, 1, n, eps,
-                                      JINF_HIP_F32, w.attn_norm_type, s));
-        else
-            ENG_TRY(jinf_residual_rmsnorm_rows(e->norm, n, e->hidden, n, e->delta, n,
-                                               w.attn_norm, 1, n, eps, JINF_HIP_F32,
-                                               w.attn_norm_type, s));
-        // Q, K, V projections (:432-439)
-        ENG_TRY(jinf_matvec(w.attn_q, w.attn_q_type, e->norm, e->q, qd, n, s));
-        ENG_TRY(jinf_matvec(w.attn_k, w.attn_k_type, e->norm, e->k, kvd, n, s));
-        ENG_TRY(jinf_matvec(w.attn_v, w.attn_v_type, e->norm, e->v, kvd, n, s));
-        // RoPE at position n_past (:441-443)
-        ENG_TRY(jinf_rope_rows(e->q, qd, e->k, kvd, e->state + kPos, 0, 1, hd, d.n_heads,
-                               d.n_heads_kv, d.rope_freq_base, JINF_HIP_F32, s));
-        // K, V into the cache (:445-453)
         char* kc = e->kv + (size_t)L * e->kv_layer_bytes;
         char* vc = e->kv + (size_t)(d.n_layers + L) * e->kv_layer_bytes;
-        const dim3 kvg((kvd + 255) / 256);
-        if (d.kv_type == JINF_HIP_F16)
-            ENG_TRY(launch(eng_kv_store_kernel<uint16_t>, kvg, dim3(256), 0, s,
-                           reinterpret_cast<uint16_t*>(kc), reinterpret_cast<uint16_t*>(vc),
-                           e->k, e->v, kvd, e->state, d.max_context));
-        else
-            ENG_TRY(launch(eng_kv_store_kernel<float>, kvg, dim3(256), 0, s,
-                           reinterpret_cast<float*>(kc), reinterpret_cast<float*>(vc), e->k, e->v,
-                           kvd, e->state, d.max_context));
+        // attention RMSNorm, Q/K/V projections, RoPE at n_past and the K/V
+        // cache rows (:429-453): one launch per distinct weight format
+        ENG_TRY(enqueue_qkv(e, w, kc, vc));
         // attention over n_past + 1 positions (:455-459)
         ENG_TRY(jinf_attention_decode(e->attn, qd, e->q, qd, kc, vc, d.kv_type, kvd,
                                       (int64_t)d.max_context * kvd, e->state + kLen, 1,
                                       d.max_context, hd, d.n_heads, d.n_heads_kv, 0.0f, e->ws,
                                       e->ws_bytes, s));
-        // output projection (:461-463); its residual add is fused below (:466)
-        ENG_TRY(jinf_matvec(w.attn_output, w.attn_output_type, e->attn, e->delta, n, qd, s));
-        // FFN RMSNorm (:487)
-        ENG_TRY(jinf_residual_rmsnorm_rows(e->norm, n, e->hidden, n, e->delta, n, w.ffn_norm, 1,
-                                           n, eps, JINF_HIP_F32, w.ffn_norm_type, s));
-        // gate, up, SiLU(gate) * up, down (:489-505)
-        ENG_TRY(jinf_matvec(w.ffn_gate, w.ffn_gate_type, e->norm, e->gate, nff, n, s));
-        ENG_TRY(jinf_matvec(w.ffn_up, w.ffn_up_type, e->norm, e->up, nff, n, s));
-        ENG_TRY(jinf_swiglu_rows(e->gate, nff, e->gate, nff, e->up, nff, 1, nff, JINF_HIP_F32,
-                                 s));
-        ENG_TRY(jinf_matvec(w.ffn_down, w.ffn_down_type, e->gate, e->delta, n, nff, s));
+        // output projection + residual add (:461-466)
+        ENG_TRY(jinf_matvec_add(w.attn_output, w.attn_output_type, e->attn, e->hidden, n, qd, s));
+        // FFN RMSNorm, gate and up projections, SiLU * up (:487-502)
+        if (w.ffn_gate_type == w.ffn_up_type) {
+            ENG_TRY(jinf_rmsnorm_swiglu_matvec(w.ffn_gate, w.ffn_up, w.ffn_gate_type, e->hidden,
+                                               w.ffn_norm, w.ffn_norm_type, eps, e->gate, nff, n,
+                                               s));
+        } else {
+            ENG_TRY(jinf_rmsnorm_matvec(w.ffn_gate, w.ffn_gate_type, e->hidden, w.ffn_norm,
+                                        w.ffn_norm_type, eps, e->gate, nff, n, s));
+            ENG_TRY(jinf_rmsnorm_matvec(w.ffn_up, w.ffn_up_type, e->hidden, w.ffn_norm,
+                                        w.ffn_norm_type, eps, e->up, nff, n, s));
+            ENG_TRY(jinf_swiglu_rows(e->gate, nff, e->gate, nff, e->up, nff, 1, nff,
+                                     JINF_HIP_F32, s));
+        }
+        // down projection + residual add (:504-508)
+        ENG_TRY(jinf_matvec_add(w.ffn_down, w.ffn_down_type, e->gate, e->hidden, n, nff, s));
     }
-    // last residual add + final RMSNorm (:508, :736-741), output projection
-    // (:743-747)
-    const float* x = e->hidden;
-    if (d.output_norm) {
-        if (d.n_layers > 0)
-            ENG_TRY(jinf_residual_rmsnorm_rows(e->norm, n, e->hidden, n, e->delta, n,
-                                               d.output_norm, 1, n, eps, JINF_HIP_F32,
-                                               d.output_norm_type, s));
-        else
-            ENG_TRY(jinf_rmsnorm_rows(e->norm, n, e->hidden, n, d.output_norm, 1, n, eps,
-                                      JINF_HIP_F32, d.output_norm_type, s));
-        x = e->norm;
-    } else if (d.n_layers > 0) {
-        ENG_TRY(jinf_residual_add_rows(e->hidden, n, e->delta, n, 1, n, JINF_HIP_F32, s));
-    }
-    ENG_TRY(jinf_matvec(d.output, d.output_type, x, e->logits, d.n_vocab, n, s));
+    // final RMSNorm (:736-741) and output projection (:743-747)
+    ENG_TRY(jinf_rmsnorm_matvec(d.output, d.output_type, e->hidden, d.output_norm,
+                                d.output_norm_type, eps, e->logits, d.n_vocab, n, s));
     // greedy argmax, next token, position advance (:780-800)
     ENG_TRY(launch(eng_argmax_part_kernel, dim3(e->arg_parts), dim3(kArgThreads), 0, s,
                    e->logits, d.n_vocab, e->part_v, e->part_i));
@@ -465,9 +439,8 @@ int create(jinf_hip_engine** out, const jinf_hip_engine_desc* desc, void* owned)
         off = up_to(off + count * 4, kAlign);
         return o;
     };
-    const size_t o_hidden = take_f(d.n_embd), o_norm = take_f(d.n_embd);
-    const size_t o_q = take_f(e->q_dim), o_k = take_f(e->kv_dim), o_v = take_f(e->kv_dim);
-    const size_t o_attn = take_f(e->q_dim), o_delta = take_f(d.n_embd);
+    const size_t o_hidden = take_f(d.n_embd), o_q = take_f(e->q_dim);
+    const size_t o_attn = take_f(e->q_dim);
     const size_t o_gate = take_f(d.n_ff), o_up = take_f(d.n_ff), o_logits = take_f(d.n_vocab);
     const size_t o_pv = take_f(kArgMaxParts), o_pi = take_f(kArgMaxParts);
     const size_t o_tok = take_f(d.max_context), o_state = take_f(kStateWords);
@@ -489,12 +462,8 @@ int create(jinf_hip_engine** out, const jinf_hip_engine_desc* desc, void* owned)
     }
     auto f = [&](size_t o) { return reinterpret_cast<float*>(e->act + o); };
     e->hidden = f(o_hidden);
-    e->norm = f(o_norm);
     e->q = f(o_q);
-    e->k = f(o_k);
-    e->v = f(o_v);
     e->attn = f(o_attn);
-    e->delta = f(o_delta);
     e->gate = f(o_gate);
     e->up = f(o_up);
     e->logits = f(o_logits);

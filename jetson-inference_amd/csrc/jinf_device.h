@@ -209,6 +209,22 @@ __device__ __forceinline__ double block_sum(double v, double* lds) {
     return s;
 }
 
+// RMSNorm scale rs = 1/sqrt(fl32(fl32(ss)/n) + eps) from an fp64 sum of
+// squares; the sqrt and divide in fp64, rounded once to fp32.
+__device__ __forceinline__ float rms_scale(double ss, int n, float eps) {
+#pragma clang fp contract(off)
+    const float m = (float)ss / (float)n;
+    const float t = m + eps;
+    return (float)(1.0 / sqrt((double)t));
+}
+
+// SwiGLU in fp32 as the reference writes it (cuda/silu_kernel.cu:6-18):
+// (g / (1 + expf(-g))) * u, no contraction.
+__device__ __forceinline__ float swiglu_exact(float g, float u) {
+#pragma clang fp contract(off)
+    return (g / (1.0f + expf(-g))) * u;
+}
+
 __device__ __forceinline__ float block_max(float v, float* lds) {
     v = wave_max(v);
     const int lane = threadIdx.x & (kWave - 1);

@@ -31,9 +31,12 @@
 // Anything the tiled kernel does not serve (unaligned pointers, widths that
 // are not a multiple of the format's tile granule, more than 7 tiles) takes a
 // one-wave-per-row kernel that decodes every weight exactly (quant_device.h).
+#include <type_traits>
+
 #include "jinf_device.h"
 #include "jinf_host.h"
 #include "quant_device.h"
+#include "rope_device.h"
 #include "jinf/kernels.h"
 #include "jinf/kernels_ext.h"
 
@@ -252,7 +255,7 @@ template <> struct MvFmt<kQ6_K> {
     }
 };
 
-template <int QT> struct MvTile {
+template <int QT, int R> struct MvTile {
     using F = MvFmt<QT>;
     static constexpr int kTileBlocks = kMvTileElems / F::kElems;
     static constexpr int kTileBytes = kTileBlocks * F::kBytes;
@@ -260,7 +263,7 @@ template <int QT> struct MvTile {
     static constexpr int kCPL = (kChunks + kWave - 1) / kWave;  // 16-byte chunks per lane
     // chunk slots past a row's kChunks that the last pass writes (see stage)
     static constexpr int kPad = kWave * kCPL - kChunks;
-    static constexpr int kStageChunks = F::kRows * kChunks + kPad;  // per wave
+    static constexpr int kStageChunks = R * kChunks + kPad;  // per wave
     static_assert(kTileBytes % 16 == 0, "tile must be whole 16-byte chunks");
     static_assert(kPad < kWave, "pad must be rewritten by the first pass");
 };
@@ -272,26 +275,150 @@ __device__ __forceinline__ int mv_xslot(int tile, int l, int j) {
     return (tile << 10) + (l << 4) + (j ^ (l & 15));
 }
 
+// ---- what a launch computes around the dot products ----
+//
+// Prologue (the x the rows are multiplied with):
+//   kProNone  x as given;
+//   kProNorm  x_j = fl32(fl32(h_j * rs) * g_j), rs from the fp64 sum of h_j^2
+//             (rms_scale): the reference's RMSNorm launch feeding the GEMV
+//             (cuda/rmsnorm_kernel.cu:9-61), computed by every workgroup.
+// Epilogue (what happens to a finished row value v):
+//   kEpiStore  y[row] = v;
+//   kEpiAdd    y[row] = y[row] + v: the residual add after the output and
+//              down projections (src/engine.cpp:466, :508);
+//   kEpiSwiGLU a group is row r of W_gate and row r of W_up:
+//              y[r] = swiglu_exact(v_gate, v_up) (src/engine.cpp:489-502);
+//   kEpiQKV    rows of up to three matrices (q, k, v segments), a group is two
+//              consecutive rows = one RoPE pair: q pairs are rotated and
+//              stored to y, k pairs rotated and stored into the K cache row
+//              at *pos, v pairs stored into the V cache row
+//              (src/engine.cpp:432-453).
+enum MvPro { kProNone = 0, kProNorm = 1 };
+enum MvEpi { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2, kEpiQKV = 3 };
+
+struct MvJob {
+    const uint8_t* W[3];    // segment matrices (same format and width)
+    int seg_end[3];         // kEpiQKV: virtual row where each segment ends
+    int64_t row_bytes;
+    int rows;               // virtual rows; kEpiSwiGLU: output rows
+    int nb;                 // blocks per row
+    int nt;                 // column tiles
+    const float* x;         // x, or h for kProNorm
+    const void* norm_w;     // kProNorm: g (fp32 or fp16)
+    int norm_f16;
+    float eps;
+    float* y;
+    void* kc;               // kEpiQKV: K / V cache rows [max_ctx][kv_dim]
+    void* vc;
+    const int32_t* pos;
+    int kv_f16, kv_dim, head_dim, max_ctx;
+};
+
+struct NoTheta {};
+template <int EPI> using MvTheta = typename std::conditional<EPI == kEpiQKV, RopeTheta, NoTheta>::type;
+
+template <int QT, int EPI> struct MvGroup {
+    static constexpr bool kPairs = EPI == kEpiSwiGLU || EPI == kEpiQKV;
+    static constexpr int R = kPairs ? 2 : MvFmt<QT>::kRows;  // rows per group
+    static __device__ __host__ int groups(const MvJob& j) {
+        return EPI == kEpiSwiGLU ? j.rows : (j.rows + R - 1) / R;
+    }
+};
+
+// Row r of group g (clamped into the matrix: groups past the end re-read the
+// last row, whose result is never stored).
+template <int QT, int EPI>
+__device__ __forceinline__ const uint8_t* mv_row(const MvJob& j, int g, int r) {
+    constexpr int R = MvGroup<QT, EPI>::R;
+    if constexpr (EPI == kEpiSwiGLU) {
+        const int row = g < j.rows ? g : j.rows - 1;
+        return j.W[r] + (int64_t)row * j.row_bytes;
+    } else {
+        int v = g * R + r;
+        if (v >= j.rows) v = j.rows - 1;
+        if constexpr (EPI == kEpiQKV) {
+            const int s = v < j.seg_end[0] ? 0 : v < j.seg_end[1] ? 1 : 2;
+            const int start = s == 0 ? 0 : j.seg_end[s - 1];
+            return j.W[s] + (int64_t)(v - start) * j.row_bytes;
+        } else {
+            return j.W[0] + (int64_t)v * j.row_bytes;
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void cache_store(void* c, int64_t i, float a, float b) {
+    T* p = static_cast<T*>(c) + i;
+    if constexpr (sizeof(T) == 2) {
+        p[0] = f2h(a);
+        p[1] = f2h(b);
+    } else {
+        p[0] = a;
+        p[1] = b;
+    }
+}
+
+// Finished values v[0..R) of group g (one lane).
+template <int QT, int EPI>
+__device__ __forceinline__ void mv_epilogue(const MvJob& j, const MvTheta<EPI>& th, int g,
+                                            float (&v)[MvGroup<QT, EPI>::R]) {
+    constexpr int R = MvGroup<QT, EPI>::R;
+    if constexpr (EPI == kEpiStore) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (g * R + r < j.rows) j.y[g * R + r] = v[r];
+    } else if constexpr (EPI == kEpiAdd) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (g * R + r < j.rows) j.y[g * R + r] = j.y[g * R + r] + v[r];
+    } else if constexpr (EPI == kEpiSwiGLU) {
+        if (g < j.rows) j.y[g] = swiglu_exact(v[0], v[1]);
+    } else {
+        const int v0 = 2 * g;
+        if (v0 >= j.rows) return;
+        const int s = v0 < j.seg_end[0] ? 0 : v0 < j.seg_end[1] ? 1 : 2;
+        const int local = v0 - (s == 0 ? 0 : j.seg_end[s - 1]);
+        const int pos = j.pos[0];
+        float a = v[0], b = v[1];
+        if (s < 2) {
+            const float2 cs = rope_cs(pos, th.t[(local % j.head_dim) / 2]);
+            rot(a, b, cs.x, cs.y);
+        }
+        if (s == 0) {
+            j.y[local] = a;
+            j.y[local + 1] = b;
+        } else if (pos >= 0 && pos < j.max_ctx) {
+            void* c = s == 1 ? j.kc : j.vc;
+            const int64_t i = (int64_t)pos * j.kv_dim + local;
+            if (j.kv_f16)
+                cache_store<uint16_t>(c, i, a, b);
+            else
+                cache_store<float>(c, i, a, b);
+        }
+    }
+}
+
 // Each wave takes whole groups of R rows (groups g, g + stride, ...) and
 // walks their tiles in order, so a row's partial sums stay in registers until
 // its last tile.  The wave's LDS accesses execute in order; the fences keep
-// the compiler from moving the read-back above the stores.  The only
-// workgroup barrier follows the x staging.
-template <int QT, bool ONE_TILE>
-__global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(
-    const uint8_t* __restrict__ W, int64_t row_bytes, const float* __restrict__ x,
-    float* __restrict__ y, int rows, int nb, int nt) {
+// the compiler from moving the read-back above the stores.  Workgroup
+// barriers only follow the x staging.
+template <int QT, bool ONE_TILE, int PRO, int EPI>
+__global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
+                                                                      MvTheta<EPI> th) {
     using F = MvFmt<QT>;
-    using T = MvTile<QT>;
-    constexpr int R = F::kRows;
+    constexpr int R = MvGroup<QT, EPI>::R;
+    using T = MvTile<QT, R>;
     constexpr int CPL = T::kCPL;
     extern __shared__ uint4 lds[];
     float4* xl = reinterpret_cast<float4*>(lds);
     const int waves = blockDim.x / kWave;
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x & (kWave - 1);
+    const int nb = job.nb;
+    int nt = job.nt;
     uint4* stage = lds + (nt << 10) + wave * T::kStageChunks;
-    const int n_groups = (rows + R - 1) / R;
+    const int n_groups = MvGroup<QT, EPI>::groups(job);
     const int stride = gridDim.x * waves;
     if (ONE_TILE) nt = 1;
 
@@ -302,8 +429,7 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(
         const int nchunk = nbt * F::kBytes / 16;  // whole by the width granule
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int row = g * R + r < rows ? g * R + r : rows - 1;
-            const uint8_t* src = W + (int64_t)row * row_bytes + (int64_t)tb * F::kBytes;
+            const uint8_t* src = mv_row<QT, EPI>(job, g, r) + (int64_t)tb * F::kBytes;
 #pragma unroll
             for (int k = 0; k < CPL; ++k) {
                 // Lanes past the tile's end re-read its last chunk (never used).
@@ -327,10 +453,50 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(
     if (g0 < n_groups) fetch(g0, t0, bufA);
 
     // Stage x (zero past the last value) while the first weights are in flight.
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    for (int f = threadIdx.x; f < (nt << 10); f += blockDim.x) {
-        const float4 v = f < nb * (F::kElems / 4) ? x4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
-        xl[mv_xslot(f >> 10, (f >> 4) & 63, f & 15)] = v;
+    const float4* x4 = reinterpret_cast<const float4*>(job.x);
+    const int nx4 = nb * (F::kElems / 4);
+    if constexpr (PRO == kProNorm) {
+        __shared__ double red[8];
+        double ss = 0.0;
+        for (int f = threadIdx.x; f < (nt << 10); f += blockDim.x) {
+            const float4 v = f < nx4 ? x4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+            xl[mv_xslot(f >> 10, (f >> 4) & 63, f & 15)] = v;
+            ss = fma((double)v.x, (double)v.x, ss);
+            ss = fma((double)v.y, (double)v.y, ss);
+            ss = fma((double)v.z, (double)v.z, ss);
+            ss = fma((double)v.w, (double)v.w, ss);
+        }
+        ss = block_sum(ss, red);
+        const float rs = rms_scale(ss, nb * F::kElems, job.eps);
+        // each thread rescales the slots it wrote
+        for (int f = threadIdx.x; f < nx4; f += blockDim.x) {
+            const int slot = mv_xslot(f >> 10, (f >> 4) & 63, f & 15);
+            float4 v = xl[slot];
+            float w[4];
+            if (job.norm_f16) {
+                const uint2 u = reinterpret_cast<const uint2*>(job.norm_w)[f];
+                w[0] = h2f((uint16_t)(u.x & 0xFFFFu));
+                w[1] = h2f((uint16_t)(u.x >> 16));
+                w[2] = h2f((uint16_t)(u.y & 0xFFFFu));
+                w[3] = h2f((uint16_t)(u.y >> 16));
+            } else {
+                const float4 u = reinterpret_cast<const float4*>(job.norm_w)[f];
+                w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w;
+            }
+            {
+#pragma clang fp contract(off)
+                v.x = (v.x * rs) * w[0];
+                v.y = (v.y * rs) * w[1];
+                v.z = (v.z * rs) * w[2];
+                v.w = (v.w * rs) * w[3];
+            }
+            xl[slot] = v;
+        }
+    } else {
+        for (int f = threadIdx.x; f < (nt << 10); f += blockDim.x) {
+            const float4 v = f < nx4 ? x4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+            xl[mv_xslot(f >> 10, (f >> 4) & 63, f & 15)] = v;
+        }
     }
     __syncthreads();
     if (g0 >= n_groups) return;
@@ -383,13 +549,14 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (t == nt - 1) {  // group complete: reduce and store its rows
+        if (t == nt - 1) {  // group complete: reduce and finish its rows
+            float v[R];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const float v = wave_sum_f32(acc[r]);
-                if (lane == 0 && g * R + r < rows) y[g * R + r] = v;
+                v[r] = wave_sum_f32(acc[r]);
                 acc[r] = 0.0f;
             }
+            if (lane == 0) mv_epilogue<QT, EPI>(job, th, g, v);
         }
     };
 
@@ -419,95 +586,241 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(
     }
 }
 
-// Any width / alignment: one wave per row; each lane takes 8-value groups
-// with stride 64 and decodes them exactly (byte loads), then fma with x.
-template <int QT>
-__global__ __launch_bounds__(256) void matvec_any_kernel(const uint8_t* __restrict__ W,
-                                                         int64_t row_bytes,
-                                                         const float* __restrict__ x,
-                                                         float* __restrict__ y, int rows, int nb) {
+// Any width / alignment: one wave per group of R rows; each lane takes
+// 8-value groups with stride 64, decodes them exactly (byte loads) and fmas
+// them with x (with kProNorm, x_j is formed on the fly from h_j and g_j).
+template <int QT, int PRO, int EPI>
+__global__ __launch_bounds__(256) void matvec_any_kernel(MvJob job, MvTheta<EPI> th) {
     constexpr int E = QGeom<QT>::kElems, B = QGeom<QT>::kBytes;
+    constexpr int R = MvGroup<QT, EPI>::R;
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t row = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-    if (row >= rows) return;
-    const uint8_t* wr = W + row * row_bytes;
-    const int n_groups = nb * (E / 8);
-    float acc = 0.0f;
-    for (int gi = lane; gi < n_groups; gi += kWave) {
+    const int g = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (g >= MvGroup<QT, EPI>::groups(job)) return;
+    const int n8 = job.nb * (E / 8);
+    float rs = 1.0f;
+    if constexpr (PRO == kProNorm) {
+        double ss = 0.0;
+        for (int j = lane; j < 8 * n8; j += kWave) ss = fma((double)job.x[j], (double)job.x[j], ss);
+        rs = rms_scale(wave_sum(ss), 8 * n8, job.eps);
+    }
+    const uint8_t* wr[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wr[r] = mv_row<QT, EPI>(job, g, r);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    for (int gi = lane; gi < n8; gi += kWave) {
         const int b = gi / (E / 8);
         const int e0 = (gi % (E / 8)) * 8;
-        float w[8];
-        decode8<QT>(wr + (int64_t)b * B, e0, w);
-        const float* xp = x + (int64_t)8 * gi;
+        float xv[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc = fmaf(w[i], xp[i], acc);
+        for (int i = 0; i < 8; ++i) {
+            const int j = 8 * gi + i;
+            float xj = job.x[j];
+            if constexpr (PRO == kProNorm) {
+#pragma clang fp contract(off)
+                const float w = job.norm_f16 ? h2f(static_cast<const uint16_t*>(job.norm_w)[j])
+                                             : static_cast<const float*>(job.norm_w)[j];
+                xj = (xj * rs) * w;
+            }
+            xv[i] = xj;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float w[8];
+            decode8<QT>(wr[r] + (int64_t)b * B, e0, w);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[r] = fmaf(w[i], xv[i], acc[r]);
+        }
     }
-    acc = wave_sum_f32(acc);
-    if (lane == 0) y[row] = acc;
+    float v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] = wave_sum_f32(acc[r]);
+    if (lane == 0) mv_epilogue<QT, EPI>(job, th, g, v);
 }
 
-// Launch the tiled kernel with at most grid_cap workgroups.  Single-tile
-// matrices use 4 independent waves per workgroup; wider ones 8 waves sharing
-// one copy of x.  Returns JINF_HIP_ERR_INVALID when the shape is not served.
-template <int QT>
-static int mv_launch(const void* w, const float* x, float* y, int rows, int cols, int grid_cap,
-                     hipStream_t stream) {
+// Launch a job: the tiled kernel with at most 512 workgroups when the shape
+// and alignment allow it (single-tile matrices use 4 independent waves per
+// workgroup; wider ones 8 waves sharing one copy of x), else the
+// one-wave-per-group kernel.
+template <int QT, int PRO, int EPI>
+static int mv_run(MvJob job, int cols, const MvTheta<EPI>& th, hipStream_t stream) {
     using F = MvFmt<QT>;
-    using T = MvTile<QT>;
-    if (cols % F::kColGranule != 0) return JINF_HIP_ERR_INVALID;
-    const int nb = cols / F::kElems;
-    const int nt = (cols + kMvTileElems - 1) / kMvTileElems;
-    if (nt > kMvMaxTiles) return JINF_HIP_ERR_INVALID;
-    const int waves = nt == 1 ? 4 : 8;
-    const int groups = (rows + F::kRows - 1) / F::kRows;
-    int grid = (groups + waves - 1) / waves;
-    if (grid > grid_cap) grid = grid_cap;
-    const size_t shmem = ((size_t)nt * 1024 + (size_t)waves * T::kStageChunks) * 16;
-    const uint8_t* W = static_cast<const uint8_t*>(w);
-    const int64_t row_bytes = (int64_t)nb * F::kBytes;
-    if (nt == 1)
-        return launch(matvec_kernel<QT, true>, dim3(grid), dim3(waves * kWave), shmem, stream, W,
-                      row_bytes, x, y, rows, nb, nt);
-    return launch(matvec_kernel<QT, false>, dim3(grid), dim3(waves * kWave), shmem, stream, W,
-                  row_bytes, x, y, rows, nb, nt);
-}
-
-template <int QT>
-static int matvec_t(const void* w, const float* x, float* y, int rows, int cols,
-                    hipStream_t stream) {
-    using F = MvFmt<QT>;
-    const int nb = cols / F::kElems;
-    if (cols % F::kColGranule == 0 && cols <= kMvMaxTiles * kMvTileElems && aligned(w, 16) &&
-        aligned(x, 16)) {
+    using G = MvGroup<QT, EPI>;
+    using T = MvTile<QT, G::R>;
+    job.nb = cols / F::kElems;
+    job.row_bytes = (int64_t)job.nb * F::kBytes;
+    job.nt = (cols + kMvTileElems - 1) / kMvTileElems;
+    const int n_groups = G::groups(job);
+    bool tiled = cols % F::kColGranule == 0 && job.nt <= kMvMaxTiles && aligned(job.x, 16);
+    for (int s = 0; s < 3; ++s) tiled = tiled && aligned(job.W[s], 16);
+    if (PRO == kProNorm) tiled = tiled && aligned(job.norm_w, job.norm_f16 ? 8 : 16);
+    if (tiled) {
+        const int waves = job.nt == 1 ? 4 : 8;
+        int grid = (n_groups + waves - 1) / waves;
         // 512 workgroups (two per CU on 256 CUs) measured best for Q4_0 at
         // 4096-14336 rows; each wave then streams several items.
-        return mv_launch<QT>(w, x, y, rows, cols, 512, stream);
+        if (grid > 512) grid = 512;
+        const size_t shmem = ((size_t)job.nt * 1024 + (size_t)waves * T::kStageChunks) * 16;
+        if (job.nt == 1)
+            return launch(matvec_kernel<QT, true, PRO, EPI>, dim3(grid), dim3(waves * kWave),
+                          shmem, stream, job, th);
+        return launch(matvec_kernel<QT, false, PRO, EPI>, dim3(grid), dim3(waves * kWave), shmem,
+                      stream, job, th);
     }
-    const int grid = (rows + 3) / 4;
-    return launch(matvec_any_kernel<QT>, dim3(grid), dim3(256), 0, stream,
-                  static_cast<const uint8_t*>(w), (int64_t)nb * F::kBytes, x, y, rows, nb);
+    if ((n_groups + 3) / 4 > 0x7FFFFFFF / 4) return JINF_HIP_ERR_INVALID;
+    return launch(matvec_any_kernel<QT, PRO, EPI>, dim3((n_groups + 3) / 4), dim3(256), 0, stream,
+                  job, th);
+}
+
+template <int PRO, int EPI>
+static int mv_dispatch(int qtype, const MvJob& job, int cols, const MvTheta<EPI>& th,
+                       hipStream_t stream) {
+    switch (qtype) {
+        case kQ4_0: return mv_run<kQ4_0, PRO, EPI>(job, cols, th, stream);
+        case kQ8_0: return mv_run<kQ8_0, PRO, EPI>(job, cols, th, stream);
+        case kQ4_K: return mv_run<kQ4_K, PRO, EPI>(job, cols, th, stream);
+        case kQ6_K: return mv_run<kQ6_K, PRO, EPI>(job, cols, th, stream);
+        default: return JINF_HIP_ERR_INVALID;
+    }
+}
+
+static int q_elems(int qtype) {
+    switch (qtype) {
+        case kQ4_0: case kQ8_0: return 32;
+        case kQ4_K: case kQ6_K: return 256;
+        default: return 0;
+    }
+}
+
+// Common checks: a served qtype, whole blocks, 4-byte aligned vectors.
+static int mv_check(int qtype, int rows, int cols, const float* x, const float* y) {
+    const int e = q_elems(qtype);
+    if (e == 0 || rows < 0 || cols < 0) return JINF_HIP_ERR_INVALID;
+    if (rows == 0 || cols == 0) return -1;  // nothing to do
+    if (!x || !y || cols % e != 0) return JINF_HIP_ERR_INVALID;
+    if (!aligned(x, 4) || !aligned(y, 4)) return JINF_HIP_ERR_INVALID;
+    return JINF_HIP_OK;
+}
+
+static int norm_setup(MvJob& j, const void* norm_w, int norm_type, float eps) {
+    j.norm_w = norm_w;
+    j.norm_f16 = norm_type == JINF_HIP_F16;
+    j.eps = eps;
+    if (!norm_w) return JINF_HIP_OK;
+    if (norm_type != JINF_HIP_F32 && norm_type != JINF_HIP_F16) return JINF_HIP_ERR_INVALID;
+    if (!aligned(norm_w, norm_type == JINF_HIP_F16 ? 2 : 4) || !(eps >= 0.0f))
+        return JINF_HIP_ERR_INVALID;
+    return JINF_HIP_OK;
 }
 
 static int matvec(const void* w, int qtype, const float* x, float* y, int rows, int cols,
                   hipStream_t stream) {
-    int elems;
-    switch (qtype) {
-        case kQ4_0: elems = 32; break;
-        case kQ8_0: elems = 32; break;
-        case kQ4_K: elems = 256; break;
-        case kQ6_K: elems = 256; break;
-        default: return JINF_HIP_ERR_INVALID;
-    }
-    if (rows < 0 || cols < 0) return JINF_HIP_ERR_INVALID;
-    if (rows == 0 || cols == 0) return JINF_HIP_OK;
-    if (!w || !x || !y || cols % elems != 0) return JINF_HIP_ERR_INVALID;
-    if (!aligned(x, 4) || !aligned(y, 4)) return JINF_HIP_ERR_INVALID;
-    switch (qtype) {
-        case kQ4_0: return matvec_t<kQ4_0>(w, x, y, rows, cols, stream);
-        case kQ8_0: return matvec_t<kQ8_0>(w, x, y, rows, cols, stream);
-        case kQ4_K: return matvec_t<kQ4_K>(w, x, y, rows, cols, stream);
-        default: return matvec_t<kQ6_K>(w, x, y, rows, cols, stream);
-    }
+    const int c = mv_check(qtype, rows, cols, x, y);
+    if (c != JINF_HIP_OK) return c < 0 ? JINF_HIP_OK : c;
+    if (!w) return JINF_HIP_ERR_INVALID;
+    MvJob j{};
+    j.W[0] = j.W[1] = j.W[2] = static_cast<const uint8_t*>(w);
+    j.rows = rows;
+    j.x = x;
+    j.y = y;
+    return mv_dispatch<kProNone, kEpiStore>(qtype, j, cols, NoTheta{}, stream);
+}
+
+static int rmsnorm_matvec(const void* w, int qtype, const float* h, const void* norm_w,
+                          int norm_type, float eps, float* y, int rows, int cols,
+                          hipStream_t stream) {
+    const int c = mv_check(qtype, rows, cols, h, y);
+    if (c != JINF_HIP_OK) return c < 0 ? JINF_HIP_OK : c;
+    if (!w) return JINF_HIP_ERR_INVALID;
+    MvJob j{};
+    if (norm_setup(j, norm_w, norm_type, eps) != JINF_HIP_OK) return JINF_HIP_ERR_INVALID;
+    j.W[0] = j.W[1] = j.W[2] = static_cast<const uint8_t*>(w);
+    j.rows = rows;
+    j.x = h;
+    j.y = y;
+    if (!norm_w) return mv_dispatch<kProNone, kEpiStore>(qtype, j, cols, NoTheta{}, stream);
+    return mv_dispatch<kProNorm, kEpiStore>(qtype, j, cols, NoTheta{}, stream);
+}
+
+static int matvec_add(const void* w, int qtype, const float* x, float* y, int rows, int cols,
+                      hipStream_t stream) {
+    const int c = mv_check(qtype, rows, cols, x, y);
+    if (c != JINF_HIP_OK) return c < 0 ? JINF_HIP_OK : c;
+    if (!w) return JINF_HIP_ERR_INVALID;
+    MvJob j{};
+    j.W[0] = j.W[1] = j.W[2] = static_cast<const uint8_t*>(w);
+    j.rows = rows;
+    j.x = x;
+    j.y = y;
+    return mv_dispatch<kProNone, kEpiAdd>(qtype, j, cols, NoTheta{}, stream);
+}
+
+static int rmsnorm_swiglu_matvec(const void* wg, const void* wu, int qtype, const float* h,
+                                 const void* norm_w, int norm_type, float eps, float* out,
+                                 int n_ff, int cols, hipStream_t stream) {
+    const int c = mv_check(qtype, n_ff, cols, h, out);
+    if (c != JINF_HIP_OK) return c < 0 ? JINF_HIP_OK : c;
+    if (!wg || !wu) return JINF_HIP_ERR_INVALID;
+    MvJob j{};
+    if (norm_setup(j, norm_w, norm_type, eps) != JINF_HIP_OK) return JINF_HIP_ERR_INVALID;
+    j.W[0] = static_cast<const uint8_t*>(wg);
+    j.W[1] = static_cast<const uint8_t*>(wu);
+    j.W[2] = j.W[0];
+    j.rows = n_ff;
+    j.x = h;
+    j.y = out;
+    if (!norm_w) return mv_dispatch<kProNone, kEpiSwiGLU>(qtype, j, cols, NoTheta{}, stream);
+    return mv_dispatch<kProNorm, kEpiSwiGLU>(qtype, j, cols, NoTheta{}, stream);
+}
+
+static int rmsnorm_qkv_rope(const void* wq, const void* wk, const void* wv, int qtype,
+                            const float* h, const void* norm_w, int norm_type, float eps,
+                            int cols, float* q_out, void* k_cache, void* v_cache, int kv_type,
+                            const int32_t* pos, int max_ctx, int head_dim, int n_heads,
+                            int n_heads_kv, float freq_base, hipStream_t stream) {
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim / 2 > kRopeMaxHalf || n_heads < 0 ||
+        n_heads_kv < 0 || max_ctx < 0)
+        return JINF_HIP_ERR_INVALID;
+    if (kv_type != JINF_HIP_F32 && kv_type != JINF_HIP_F16) return JINF_HIP_ERR_INVALID;
+    if (!(freq_base > 0.0f)) return JINF_HIP_ERR_INVALID;
+    const int64_t qd = (int64_t)n_heads * head_dim, kvd = (int64_t)n_heads_kv * head_dim;
+    const int64_t rq = wq ? qd : 0, rk = wk ? kvd : 0, rv = wv ? kvd : 0;
+    if (rq + rk + rv > 0x7FFFFFFF) return JINF_HIP_ERR_INVALID;
+    const int rows = (int)(rq + rk + rv);
+    if (rows == 0) return JINF_HIP_OK;
+    if ((wq && !q_out) || (wk && !k_cache) || (wv && !v_cache) || !pos)
+        return JINF_HIP_ERR_INVALID;
+    if (q_out && !aligned(q_out, 4)) return JINF_HIP_ERR_INVALID;
+    const int es = kv_type == JINF_HIP_F16 ? 2 : 4;
+    if ((k_cache && !aligned(k_cache, es)) || (v_cache && !aligned(v_cache, es)))
+        return JINF_HIP_ERR_INVALID;
+    const int c = mv_check(qtype, rows, cols, h, q_out ? q_out : h);
+    if (c != JINF_HIP_OK) return c < 0 ? JINF_HIP_OK : c;
+    MvJob j{};
+    if (norm_setup(j, norm_w, norm_type, eps) != JINF_HIP_OK) return JINF_HIP_ERR_INVALID;
+    // q, k, v segments in that order; an absent one is empty
+    const void* first = wq ? wq : wk ? wk : wv;
+    j.W[0] = static_cast<const uint8_t*>(wq ? wq : first);
+    j.W[1] = static_cast<const uint8_t*>(wk ? wk : first);
+    j.W[2] = static_cast<const uint8_t*>(wv ? wv : first);
+    j.seg_end[0] = (int)rq;
+    j.seg_end[1] = (int)(rq + rk);
+    j.seg_end[2] = rows;
+    j.rows = rows;
+    j.x = h;
+    j.y = q_out;
+    j.kc = k_cache;
+    j.vc = v_cache;
+    j.pos = pos;
+    j.kv_f16 = kv_type == JINF_HIP_F16;
+    j.kv_dim = (int)kvd;
+    j.head_dim = head_dim;
+    j.max_ctx = max_ctx;
+    RopeTheta th;
+    theta_table(th, head_dim, freq_base);
+    if (!norm_w) return mv_dispatch<kProNone, kEpiQKV>(qtype, j, cols, th, stream);
+    return mv_dispatch<kProNorm, kEpiQKV>(qtype, j, cols, th, stream);
 }
 
 }  // namespace jinf
@@ -535,4 +848,34 @@ extern "C" void jinf_cuda_dequant_matvec(const void* weight, const float* input,
     if (jinf::matvec(weight, qtype, input, output, rows, cols, stream) == JINF_HIP_ERR_INVALID)
         JINF_LOG("jinf_cuda_dequant_matvec: invalid argument (rows=%d cols=%d qtype=%d)", rows,
                  cols, qtype);
+}
+
+extern "C" int jinf_rmsnorm_matvec(const void* weight, int qtype, const float* h,
+                                   const void* norm_w, int norm_type, float eps, float* y,
+                                   int rows, int cols, hipStream_t stream) {
+    return jinf::rmsnorm_matvec(weight, qtype, h, norm_w, norm_type, eps, y, rows, cols, stream);
+}
+
+extern "C" int jinf_matvec_add(const void* weight, int qtype, const float* x, float* y, int rows,
+                               int cols, hipStream_t stream) {
+    return jinf::matvec_add(weight, qtype, x, y, rows, cols, stream);
+}
+
+extern "C" int jinf_rmsnorm_swiglu_matvec(const void* w_gate, const void* w_up, int qtype,
+                                          const float* h, const void* norm_w, int norm_type,
+                                          float eps, float* out, int n_ff, int cols,
+                                          hipStream_t stream) {
+    return jinf::rmsnorm_swiglu_matvec(w_gate, w_up, qtype, h, norm_w, norm_type, eps, out, n_ff,
+                                       cols, stream);
+}
+
+extern "C" int jinf_rmsnorm_qkv_rope(const void* w_q, const void* w_k, const void* w_v, int qtype,
+                                     const float* h, const void* norm_w, int norm_type, float eps,
+                                     int cols, float* q_out, void* k_cache, void* v_cache,
+                                     int kv_type, const int32_t* pos, int max_ctx, int head_dim,
+                                     int n_heads, int n_heads_kv, float freq_base,
+                                     hipStream_t stream) {
+    return jinf::rmsnorm_qkv_rope(w_q, w_k, w_v, qtype, h, norm_w, norm_type, eps, cols, q_out,
+                                  k_cache, v_cache, kv_type, pos, max_ctx, head_dim, n_heads,
+                                  n_heads_kv, freq_base, stream);
 }

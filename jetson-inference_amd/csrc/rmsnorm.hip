@@ -67,15 +67,6 @@ __device__ __forceinline__ void wunpack(const WRaw<uint16_t, E>& r, float (&v)[E
     }
 }
 
-// rs = 1/sqrt(fl32(fl32(ss)/n) + eps), the sqrt and divide in fp64 and
-// rounded once to fp32.
-__device__ __forceinline__ float rms_scale(double ss, int n, float eps) {
-#pragma clang fp contract(off)
-    const float m = (float)ss / (float)n;
-    const float t = m + eps;
-    return (float)(1.0 / sqrt((double)t));
-}
-
 template <typename TA, typename TW, bool FUSED, int CPT = kNormCPT>
 __global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(
     TA* out, int ld_out, TA* res, int ld_res, const TA* in, int ld_in,

@@ -26,35 +26,17 @@
 #include "jinf_device.h"
 #include "jinf_host.h"
 #include "jinf/kernels.h"
+#include "rope_device.h"
 
 namespace jinf {
 
 constexpr int kRopeBlock = 128;
-constexpr int kRopeMaxHalf = 256;  // head_dim <= 512
 
-struct RopeTheta {
-    float t[kRopeMaxHalf];
-};
-
-__device__ __forceinline__ void rot(float& x0, float& x1, float c, float s) {
-#pragma clang fp contract(off)
-    const float a = x0 * c - x1 * s;
-    const float b = x0 * s + x1 * c;
-    x0 = a;
-    x1 = b;
-}
-
-// Fill cs[i] = (cos, sin) of fl32(pos * theta_i) for i < half, in fp64 then
-// rounded to fp32.  Ends with a barrier.
+// Fill cs[i] = (cos, sin) of fl32(pos * theta_i) for i < half.  Ends with a
+// barrier.
 __device__ __forceinline__ void rope_table(float2* cs, int half, int pos,
                                            const RopeTheta& th) {
-#pragma clang fp contract(off)
-    for (int i = threadIdx.x; i < half; i += blockDim.x) {
-        const float a = (float)pos * th.t[i];
-        double sn, cn;
-        sincos((double)a, &sn, &cn);
-        cs[i] = make_float2((float)cn, (float)sn);
-    }
+    for (int i = threadIdx.x; i < half; i += blockDim.x) cs[i] = rope_cs(pos, th.t[i]);
     __syncthreads();
 }
 
@@ -127,17 +109,6 @@ __global__ __launch_bounds__(kRopeBlock) void rope_scalar_kernel(
         rot(x0, x1, c.x, c.y);
         A::store1(p, x0);
         A::store1(p + 1, x1);
-    }
-}
-
-static void theta_table(RopeTheta& th, int head_dim, float base) {
-    const int half = head_dim / 2;
-    for (int i = 0; i < kRopeMaxHalf; ++i) th.t[i] = 0.0f;
-    for (int i = 0; i < half; ++i) {
-        // Exponent exactly as the reference forms it in fp32: -2.0f*i/hd.
-        volatile float e = -2.0f * (float)i;
-        e = e / (float)head_dim;
-        th.t[i] = (float)pow((double)base, (double)e);
     }
 }
 

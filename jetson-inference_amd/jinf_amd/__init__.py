@@ -25,10 +25,14 @@ from .ops import (  # noqa: F401
     dequant_rows,
     embed_q4_0,
     matvec,
+    matvec_add,
     matvec_q4_0,
     residual_add,
     residual_rmsnorm_rows,
+    rmsnorm_matvec,
+    rmsnorm_qkv_rope,
     rmsnorm_rows,
+    rmsnorm_swiglu_matvec,
     rope_rows,
     softmax_rows,
     swiglu,

@@ -175,6 +175,76 @@ def matvec(weight, x, qtype, y=None):
     return y
 
 
+def _mv_shape(weight, qtype, cols):
+    if qtype not in _GEOM:
+        raise JinfError(f"unsupported qtype {qtype}")
+    elems, nbytes = _GEOM[qtype]
+    if weight.shape[1] != cols // elems * nbytes:
+        raise JinfError("weight row bytes do not match cols")
+    return weight.shape[0]
+
+
+def _norm_args(norm_w):
+    if norm_w is None:
+        return None, F32
+    return _ptr(norm_w), (F16 if norm_w.dtype == torch.float16 else F32)
+
+
+def rmsnorm_matvec(weight, h, qtype, norm_w=None, eps=1e-5, y=None):
+    """y = W (rmsnorm(h) * g) in one launch (norm_w None: y = W h)."""
+    rows = _mv_shape(weight, qtype, h.shape[0])
+    y = torch.empty(rows, dtype=torch.float32, device=h.device) if y is None else y
+    nw, nt = _norm_args(norm_w)
+    _check(lib().jinf_rmsnorm_matvec(_ptr(weight), int(qtype), _ptr(h), nw, nt, float(eps),
+                                     _ptr(y), rows, h.shape[0], _stream()),
+           "jinf_rmsnorm_matvec")
+    return y
+
+
+def matvec_add(weight, x, qtype, y):
+    """y += W x in place (the residual add fused into the GEMV)."""
+    rows = _mv_shape(weight, qtype, x.shape[0])
+    _check(lib().jinf_matvec_add(_ptr(weight), int(qtype), _ptr(x), _ptr(y), rows, x.shape[0],
+                                 _stream()), "jinf_matvec_add")
+    return y
+
+
+def rmsnorm_swiglu_matvec(w_gate, w_up, h, qtype, norm_w=None, eps=1e-5, out=None):
+    """out = silu(W_gate x^) * (W_up x^), x^ = rmsnorm(h) * g, one launch."""
+    n_ff = _mv_shape(w_gate, qtype, h.shape[0])
+    if tuple(w_up.shape) != tuple(w_gate.shape):
+        raise JinfError("gate and up shapes differ")
+    out = torch.empty(n_ff, dtype=torch.float32, device=h.device) if out is None else out
+    nw, nt = _norm_args(norm_w)
+    _check(lib().jinf_rmsnorm_swiglu_matvec(_ptr(w_gate), _ptr(w_up), int(qtype), _ptr(h), nw,
+                                            nt, float(eps), _ptr(out), n_ff, h.shape[0],
+                                            _stream()), "jinf_rmsnorm_swiglu_matvec")
+    return out
+
+
+def rmsnorm_qkv_rope(w_q, w_k, w_v, h, qtype, pos, k_cache, v_cache, head_dim, n_heads,
+                     n_heads_kv, freq_base, norm_w=None, eps=1e-5, q_out=None):
+    """q = rope(W_q x^) (returned); rope(W_k x^) and W_v x^ stored into the
+    cache rows at device position pos[0] (caches [max_ctx, n_heads_kv *
+    head_dim], fp32 or fp16).  A None weight skips its projection."""
+    cols = h.shape[0]
+    for w in (w_q, w_k, w_v):
+        if w is not None:
+            _mv_shape(w, qtype, cols)
+    if w_q is not None and q_out is None:
+        q_out = torch.empty(n_heads * head_dim, dtype=torch.float32, device=h.device)
+    cache = k_cache if k_cache is not None else v_cache
+    kv_type = _act(cache) if cache is not None else F32
+    max_ctx = cache.shape[0] if cache is not None else 0
+    nw, nt = _norm_args(norm_w)
+    _check(lib().jinf_rmsnorm_qkv_rope(_ptr(w_q), _ptr(w_k), _ptr(w_v), int(qtype), _ptr(h), nw,
+                                       nt, float(eps), cols, _ptr(q_out), _ptr(k_cache),
+                                       _ptr(v_cache), kv_type, _ptr(pos), max_ctx, head_dim,
+                                       n_heads, n_heads_kv, float(freq_base), _stream()),
+           "jinf_rmsnorm_qkv_rope")
+    return q_out
+
+
 def dequant_rows(table, qtype, n_embd, ids=None, out_dtype=torch.float32, out=None):
     """Gather + dequantize rows of a qtype table (uint8 [n_vocab, row bytes])."""
     n_vocab = table.shape[0]

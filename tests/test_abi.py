@@ -38,7 +38,7 @@ def test_headers_include_no_gpu_runtime_header():
 
 def test_every_declared_symbol_is_exported_with_declared_arity():
     decl = declared()
-    assert len(decl) == 55
+    assert len(decl) == 59
     lib = jinf_amd.lib()
     for name, n in decl.items():
         assert hasattr(lib, name), name
@@ -91,6 +91,19 @@ FAKE = P(0x1000)  # never dereferenced: every call below is rejected on the host
     lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 0, 64, 4096, FAKE, 2, 32, 128, 2, 1, 0.0, None, 0, None),
     lambda L: L.jinf_attention_decode(FAKE, 256, FAKE, 256, FAKE, FAKE, 7, 128, 4096, FAKE, 2, 32, 128, 2, 1, 0.0, None, 0, None),
     lambda L: L.jinf_attention_decode(FAKE, 4096, FAKE, 4096, FAKE, FAKE, 0, 2048, 65536, FAKE, 2, 32, 2048, 2, 1, 0.0, None, 0, None),
+    # fused GEMVs: qtype, whole blocks, norm type, missing operands, head_dim,
+    # kv type, missing position
+    lambda L: L.jinf_rmsnorm_matvec(FAKE, 3, FAKE, FAKE, 0, 1e-5, FAKE, 16, 256, None),
+    lambda L: L.jinf_rmsnorm_matvec(FAKE, 12, FAKE, FAKE, 0, 1e-5, FAKE, 16, 128, None),
+    lambda L: L.jinf_rmsnorm_matvec(FAKE, 2, FAKE, FAKE, 2, 1e-5, FAKE, 16, 256, None),
+    lambda L: L.jinf_rmsnorm_matvec(FAKE, 2, FAKE, FAKE, 0, -1.0, FAKE, 16, 256, None),
+    lambda L: L.jinf_matvec_add(None, 2, FAKE, FAKE, 16, 256, None),
+    lambda L: L.jinf_rmsnorm_swiglu_matvec(FAKE, None, 2, FAKE, FAKE, 0, 1e-5, FAKE, 16, 256, None),
+    lambda L: L.jinf_rmsnorm_qkv_rope(FAKE, FAKE, FAKE, 2, FAKE, FAKE, 0, 1e-5, 256, FAKE, FAKE, FAKE, 1, FAKE, 64, 63, 4, 2, 1e4, None),
+    lambda L: L.jinf_rmsnorm_qkv_rope(FAKE, FAKE, FAKE, 2, FAKE, FAKE, 0, 1e-5, 256, FAKE, FAKE, FAKE, 5, FAKE, 64, 64, 4, 2, 1e4, None),
+    lambda L: L.jinf_rmsnorm_qkv_rope(FAKE, FAKE, FAKE, 2, FAKE, FAKE, 0, 1e-5, 256, FAKE, FAKE, FAKE, 1, None, 64, 64, 4, 2, 1e4, None),
+    lambda L: L.jinf_rmsnorm_qkv_rope(FAKE, FAKE, FAKE, 2, FAKE, FAKE, 0, 1e-5, 256, None, FAKE, FAKE, 1, FAKE, 64, 64, 4, 2, 1e4, None),
+    lambda L: L.jinf_rmsnorm_qkv_rope(FAKE, FAKE, FAKE, 2, FAKE, FAKE, 0, 1e-5, 256, FAKE, FAKE, FAKE, 1, FAKE, 64, 64, 4, 2, 0.0, None),
 ])
 def test_invalid_arguments_rejected_on_host(call):
     assert call(jinf_amd.lib()) == _lib.JINF_HIP_ERR_INVALID
