@@ -142,7 +142,8 @@ int jinf_matvec_q4_0(const void* weight, const float* x, float* y, int rows, int
  * fp32 rounding of the dot products.  Vectors are fp32, 4-byte aligned; the
  * fast path wants weights, h/x and g 16-byte aligned, cols a multiple of 256
  * (2048 for Q6_K) and at most 28672, any other shape runs a slower generic
- * kernel.  No output may overlap an input. ---- */
+ * kernel.  No output may overlap another argument (jinf_matvec_add's y is
+ * its own addend). ---- */
 
 /* y = W x^ with x^_j = fl32(fl32(h_j * rs) * g_j), rs = 1/sqrt(sum h^2 / cols
  * + eps) (the RMSNorm of jinf_rmsnorm_rows, computed inside the GEMV):
@@ -208,8 +209,10 @@ int jinf_dequant_rows(void* out, int ld_out, const void* table, int qtype, int n
  * (|q * scale| < 65504).  Nothing is allocated.  workspace (device memory,
  * optional: NULL or too small runs every sequence in one work item) lets an
  * fp16-cache call split long contexts (chunks of at least 256 positions)
- * over several workgroups; it needs jinf_attention_workspace_bytes(n_seq, n_heads,
- * head_dim, max_ctx) bytes, holds no state between calls, and must not be
+ * over several workgroups, which merge their partial results themselves; it
+ * needs jinf_attention_workspace_bytes(n_seq, n_heads, head_dim, max_ctx)
+ * bytes, zero-filled before its first use (every call leaves its merge
+ * counters at zero again, so it is reused without clearing), and must not be
  * shared by calls running concurrently. */
 int jinf_attention_decode(float* out, int ld_out, const float* q, int ld_q,
                           const void* k_cache, const void* v_cache, int kv_type,

@@ -317,6 +317,9 @@ typedef float am_f4 __attribute__((ext_vector_type(4)));
 constexpr int kAmChunkMin = 256;
 constexpr int kAmTargetItems = 1024;
 constexpr float kAmPScale = 32768.0f;  // 2^15
+// below this many (sequence, head group) pairs a split context is merged by
+// the attention kernel itself, at or above it by a second launch
+constexpr int kAmInKernelMerge = 128;
 
 __device__ __forceinline__ am_h4 am_h4_from(uint32_t lo, uint32_t hi) {
     const uint2 u = make_uint2(lo, hi);
@@ -324,6 +327,14 @@ __device__ __forceinline__ am_h4 am_h4_from(uint32_t lo, uint32_t hi) {
 }
 
 __device__ __forceinline__ float ror8(float v) { return dpp_f32<0x128>(v); }  // row_ror:8
+
+// Device-coherent (sc1) record store / load for the cross-workgroup merge.
+__device__ __forceinline__ void rec_store(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float rec_load(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // One 16-byte direct-to-LDS load per lane: lane l's 16 bytes from gptr land
 // at LDS byte lds_base + 16 l (lds_base wave-uniform).  Issued from inline
@@ -355,16 +366,90 @@ constexpr int waitcnt_vm() {
     return (N & 0xF) | ((N >> 4) << 14) | 0x0F70;
 }
 
-// grid (n_heads / G, n_chunks, n_seq), 256 threads.  ws == nullptr: one chunk
-// spanning the sequence, output written directly; otherwise each (sequence,
-// head, chunk) writes an unnormalised partial {O[HD], m, l} to ws and
-// attn_combine_kernel merges them.
+// The in-kernel merge of a split context (attn_mfma_kernel with MERGE): the
+// calling workgroup has stored its records for head slots [h0, h0 + G) of
+// sequence s.  `lds` is the kernel's dynamic LDS, free at this point.
 template <int HD>
+__device__ __forceinline__ void am_merge_last(float* __restrict__ out, int64_t ld_out,
+                                              float* __restrict__ ws,
+                                              unsigned* __restrict__ counters, int s, int n_heads,
+                                              int h0, int G, int nch, int used, uint8_t* lds) {
+    constexpr int MS = HD + 2;
+    // The last of the `used` workgroups of this (sequence, head group) merges
+    // their records in chunk order and returns the counter to zero.  Records
+    // are written and read with device-coherent accesses (they bypass the
+    // per-XCD L2 caches, which are not coherent with one another), each
+    // thread waits for its record stores to complete before the barrier, and
+    // the counter is a device-scope atomic: the last workgroup to count sees
+    // every record.
+    __shared__ int am_last;
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned* cnt = counters + (int64_t)s * n_heads + blockIdx.x;
+        const unsigned prev =
+            __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        am_last = prev + 1 == (unsigned)used;
+        if (am_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!am_last) return;
+    // Merge: the chunks' (m, l) pairs and weights f_c = exp(m_c - M) go
+    // through LDS (the tile buffers are free now), computed once per (chunk,
+    // head) in parallel; then each (head, dim) sums f_c O_c[d] over the chunks
+    // with the loads of several chunks in flight.  Same operations in the same
+    // order per output as a sequential merge.
+    float* mw = reinterpret_cast<float*>(lds);  // [used][8]: m, then f
+    float* ml = mw + used * 8;                  // [used][8]: l
+    float* mM = ml + used * 8;                  // [8]: M per head slot
+    for (int idx = threadIdx.x; idx < used * G; idx += blockDim.x) {
+        const int c = idx / G, g = idx % G;
+        const float* e = ws + (((int64_t)s * n_heads + h0 + g) * nch + c) * MS;
+        mw[c * 8 + g] = rec_load(e + HD);
+        ml[c * 8 + g] = rec_load(e + HD + 1);
+    }
+    __syncthreads();
+    if (threadIdx.x < G) {
+        float M = -INFINITY;
+        for (int c = 0; c < used; ++c) M = fmaxf(M, mw[c * 8 + threadIdx.x]);
+        mM[threadIdx.x] = M;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < used * G; idx += blockDim.x) {
+        const int c = idx / G, g = idx % G;
+        const float M = mM[g];
+        mw[c * 8 + g] = M > -INFINITY ? exp_neg(mw[c * 8 + g] - M) : 0.0f;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
+        const int g = idx / HD, d = idx % HD;
+        const float* rec = ws + ((int64_t)s * n_heads + h0 + g) * nch * MS + d;
+        float num = 0.0f, den = 0.0f;
+        if (mM[g] > -INFINITY) {
+#pragma unroll 8
+            for (int c = 0; c < used; ++c) {
+                const float f = mw[c * 8 + g];
+                num = fmaf(f, rec_load(rec + (int64_t)c * MS), num);
+                den = fmaf(f, ml[c * 8 + g], den);
+            }
+        }
+        out[(int64_t)s * ld_out + (int64_t)(h0 + g) * HD + d] = den > 0.0f ? num / den : 0.0f;
+    }
+}
+
+// grid (n_heads / G, n_chunks, n_seq), 256 threads.  ws == nullptr, or a
+// context that fits in one chunk: the workgroup writes the output directly;
+// otherwise each (sequence, head, chunk) writes an unnormalised partial
+// {O[HD], m, l} to ws, and either the last workgroup of the (sequence, head
+// group) to finish merges them (counters: one per (sequence, head group),
+// zero between calls) or, counters == nullptr, attn_combine_kernel does.
+template <int HD, bool MERGE>
 __global__ __launch_bounds__(256) void attn_mfma_kernel(
     float* __restrict__ out, int64_t ld_out, const float* __restrict__ q, int64_t ld_q,
     const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t ld_pos,
     int64_t ld_seq, const int32_t* __restrict__ lens, int n_past, int group, int G,
-    int n_heads, float scale, float* __restrict__ ws, int chunk) {
+    int n_heads, float scale, float* __restrict__ ws, unsigned* __restrict__ counters,
+    int chunk) {
     constexpr int KS = HD / 16;        // k-steps of the score product
     constexpr int DPG = HD / 4;        // dims per lane group in the score product
     constexpr int KLD = DPG / 8;       // 16-byte K loads per position block
@@ -385,6 +470,10 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     const int len = lens ? min(max(lens[s], 0), n_past) : n_past;
     const int c0 = blockIdx.y * chunk;
     const int c1 = min(c0 + chunk, len);
+    // chunks past the context have nothing to do (chunk 0 always runs, so an
+    // empty context still writes its zeros)
+    if (blockIdx.y > 0 && c0 >= len) return;
+    const int used = (len + chunk - 1) / chunk;  // chunks holding positions
     uint8_t* vst = am_lds + wave * 2 * kAtTile * PITCH;  // V tile, then K tile
     const uint16_t* kb = kc + (int64_t)s * ld_seq + (int64_t)j * HD;
     const uint16_t* vb = vc + (int64_t)s * ld_seq + (int64_t)j * HD;
@@ -568,6 +657,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     }
     __syncthreads();
     const int nch = gridDim.y;
+    const bool direct = !ws || used <= 1;  // this workgroup holds the whole context
     for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
         const int g = idx / HD, d = idx % HD;
         float M = -INFINITY;
@@ -581,20 +671,41 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
                 den = fmaf(f, e[HD + 1], den);
             }
         }
-        if (!ws) {
+        if (direct) {
             out[(int64_t)s * ld_out + (int64_t)(h0 + g) * HD + d] = den > 0.0f ? num / den : 0.0f;
         } else {
+            // device-coherent stores only for the in-kernel merge; the
+            // merge launch reads ordinary stores after the kernel boundary
             float* rec = ws + (((int64_t)s * n_heads + h0 + g) * nch + blockIdx.y) * MS;
-            rec[d] = num;
-            if (d == 0) {
-                rec[HD] = M;
-                rec[HD + 1] = den;
+            if constexpr (MERGE) {
+                rec_store(rec + d, num);
+                if (d == 0) {
+                    rec_store(rec + HD, M);
+                    rec_store(rec + HD + 1, den);
+                }
+            } else {
+                rec[d] = num;
+                if (d == 0) {
+                    rec[HD] = M;
+                    rec[HD + 1] = den;
+                }
             }
         }
     }
+    // Without MERGE, attn_combine_kernel merges the records.  (The merge is a
+    // separate instantiation: its code in the same kernel, even unexecuted,
+    // slowed the main loop by 6% at 64 sequences x 8192 positions.)
+    if constexpr (MERGE) {
+        if (!direct)
+            am_merge_last<HD>(out, ld_out, ws, counters, s, n_heads, h0, G, nch, used, am_lds);
+    } else {
+        (void)counters;
+    }
 }
 
-// Merge of the chunk partials: grid (n_heads, n_seq), head_dim threads.
+// Merge of the chunk partials in a separate launch: grid (n_heads, n_seq),
+// head_dim threads; sequences whose context fits in one chunk were written
+// directly by the attention kernel.
 __global__ __launch_bounds__(256) void attn_combine_kernel(
     float* __restrict__ out, int64_t ld_out, const float* __restrict__ ws,
     const int32_t* __restrict__ lens, int n_past, int n_heads, int hd, int nch, int chunk) {
@@ -602,6 +713,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(
     if (d >= hd) return;
     const int len = lens ? min(max(lens[s], 0), n_past) : n_past;
     const int used = (len + chunk - 1) / chunk;
+    if (used <= 1) return;
     const float* rec = ws + ((int64_t)s * n_heads + h) * nch * (hd + 2);
     float M = -INFINITY;
     for (int c = 0; c < used; ++c) M = fmaxf(M, rec[c * (hd + 2) + hd]);
@@ -617,9 +729,17 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(
     out[(int64_t)s * ld_out + (int64_t)h * hd + d] = den > 0.0f ? num / den : 0.0f;
 }
 
+// Workspace: one merge counter per (sequence, head group) -- n_seq * n_heads
+// slots cover any grouping -- padded to 256 bytes, then the chunk records
+// {O[HD], m, l} of every (sequence, head, chunk).
+static size_t am_counter_bytes(int n_seq, int n_heads) {
+    return ((size_t)n_seq * n_heads * sizeof(unsigned) + 255) / 256 * 256;
+}
+
 static size_t am_workspace_bytes(int n_seq, int n_heads, int head_dim, int max_ctx) {
     const int64_t nch = ((int64_t)max_ctx + kAmChunkMin - 1) / kAmChunkMin;
-    return (size_t)n_seq * n_heads * nch * (head_dim + 2) * sizeof(float);
+    return am_counter_bytes(n_seq, n_heads) +
+           (size_t)n_seq * n_heads * nch * (head_dim + 2) * sizeof(float);
 }
 
 template <int HD>
@@ -634,16 +754,28 @@ static int am_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, c
     int64_t ch = (work + kAmTargetItems - 1) / kAmTargetItems;
     ch = (ch + 63) / 64 * 64;
     if (ch < kAmChunkMin) ch = kAmChunkMin;
+    // the merge keeps 16 floats per chunk (+ 8) in the tile buffers' LDS
     const bool split = workspace && n_past > ch &&
-                       ws_bytes >= am_workspace_bytes(n_seq, n_heads, HD, n_past);
+                       ws_bytes >= am_workspace_bytes(n_seq, n_heads, HD, n_past) &&
+                       ((n_past + ch - 1) / ch * 16 + 8) * sizeof(float) <= shmem;
     const int chunk = split ? (int)ch : (n_past > 0 ? n_past : 1);
     const int nch = split ? (n_past + chunk - 1) / chunk : 1;
-    float* ws = split ? static_cast<float*>(workspace) : nullptr;
-    int st = launch(attn_mfma_kernel<HD>, dim3(n_heads / G, nch, n_seq), dim3(256), shmem, stream,
-                    out, ld_out, q, ld_q, static_cast<const uint16_t*>(k),
-                    static_cast<const uint16_t*>(v), ld_pos, ld_seq, lens, n_past, group, G,
-                    n_heads, scale, ws, chunk);
-    if (st != JINF_HIP_OK || !split) return st;
+    // Few (sequence, head group) pairs: the last workgroup of each merges in
+    // the same launch (measured at batch 1, 8192 positions: 19 us against 27
+    // with a second launch).  Many: every chunk workgroup would wait on the
+    // merge counter before retiring, so a separate wide merge launch is
+    // faster (64 sequences x 8 groups: 268 us against 290).
+    const bool in_kernel = (int64_t)n_seq * (n_heads / G) < kAmInKernelMerge;
+    unsigned* counters = split && in_kernel ? static_cast<unsigned*>(workspace) : nullptr;
+    float* ws = split ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                 am_counter_bytes(n_seq, n_heads))
+                      : nullptr;
+    auto* kern = counters ? attn_mfma_kernel<HD, true> : attn_mfma_kernel<HD, false>;
+    const int st = launch(kern, dim3(n_heads / G, nch, n_seq), dim3(256), shmem, stream, out,
+                          ld_out, q, ld_q, static_cast<const uint16_t*>(k),
+                          static_cast<const uint16_t*>(v), ld_pos, ld_seq, lens, n_past, group,
+                          G, n_heads, scale, ws, counters, chunk);
+    if (st != JINF_HIP_OK || !split || in_kernel) return st;
     return launch(attn_combine_kernel, dim3(n_heads, n_seq), dim3(HD), 0, stream, out, ld_out,
                   (const float*)ws, lens, n_past, n_heads, HD, nch, chunk);
 }

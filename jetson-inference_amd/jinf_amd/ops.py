@@ -260,9 +260,10 @@ def dequant_rows(table, qtype, n_embd, ids=None, out_dtype=torch.float32, out=No
 
 
 def attention_workspace(n_seq, n_heads, head_dim, max_ctx, device="cuda"):
-    """A workspace tensor for attention_decode's split of long contexts."""
+    """A zero-filled workspace tensor for attention_decode's split of long
+    contexts (its merge counters must start at zero; calls leave them so)."""
     nbytes = lib().jinf_attention_workspace_bytes(n_seq, n_heads, head_dim, max_ctx)
-    return torch.empty(max(nbytes, 4), dtype=torch.uint8, device=device)
+    return torch.zeros(max(nbytes, 4), dtype=torch.uint8, device=device)
 
 
 def attention_decode(q, k_cache, v_cache, lens, n_heads, n_heads_kv, scale=0.0, out=None,

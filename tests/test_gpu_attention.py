@@ -125,9 +125,11 @@ def test_explicit_scale_and_single_position(dev):
 
 # Split of long contexts over workgroups through a workspace (fp16 caches):
 # several chunks per sequence, a sequence shorter than one chunk, one that
-# ends exactly on a chunk boundary, and batch 1.
+# ends exactly on a chunk boundary, and batch 1.  Up to 127 (sequence, head
+# group) pairs merge inside the attention launch; the last case (256 pairs)
+# merges in a second launch.
 SPLIT = [(8, 8192, 64, 8, 128), (3, 3000, 32, 8, 128), (1, 8192, 32, 8, 128),
-         (5, 2500, 16, 2, 64)]
+         (5, 2500, 16, 2, 64), (32, 1024, 32, 8, 128)]
 
 
 @pytest.mark.parametrize("n_seq,max_ctx,nh,nkv,hd", SPLIT)
@@ -142,10 +144,16 @@ def test_split_contexts_with_workspace(dev, n_seq, max_ctx, nh, nkv, hd):
     q, k, v, kp, vp = make(r, n_seq, max_ctx, nh, nkv, hd, lens, np.float16, qsigma=2.0)
     ref, a = _oracle(q, k, v, lens, nh, nkv, hd, max_ctx)
     ws = jinf_amd.attention_workspace(n_seq, nh, hd, max_ctx)
-    assert ws.numel() == n_seq * nh * ((max_ctx + 255) // 256) * (hd + 2) * 4
+    counters = (n_seq * nh * 4 + 255) // 256 * 256
+    assert ws.numel() == counters + n_seq * nh * ((max_ctx + 255) // 256) * (hd + 2) * 4
     qd, kd, vd, ld = to_dev(q), to_dev(kp), to_dev(vp), to_dev(lens)
     out = host(jinf_amd.attention_decode(qd, kd, vd, ld, nh, nkv, workspace=ws))
     check(out, ref, a, f"split {n_seq}x{nh}/{nkv}x{hd}")
+    # the merge counters are back at zero, and a second call with the same
+    # workspace gives the same bits
+    assert np.all(host(ws[:counters]) == 0)
+    again = host(jinf_amd.attention_decode(qd, kd, vd, ld, nh, nkv, workspace=ws))
+    assert tu.bits_equal(again, out)
     # the same call without a workspace (one work item per sequence)
     out1 = host(jinf_amd.attention_decode(qd, kd, vd, ld, nh, nkv))
     check(out1, ref, a, "unsplit")
