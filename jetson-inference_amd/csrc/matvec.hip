@@ -45,6 +45,7 @@ namespace jinf {
 constexpr int kMvTileElems = 4096;                // values of a row per column tile
 constexpr int kMvLaneElems = kMvTileElems / kWave;  // 64 values per lane
 constexpr int kMvMaxTiles = 7;                    // x of 7 tiles (112 KiB) fits in LDS
+constexpr size_t kMvLdsBytes = 160 * 1024;        // LDS per workgroup on gfx950
 
 // ---- fp16-denormal products ----
 //
@@ -317,9 +318,16 @@ struct MvJob {
 struct NoTheta {};
 template <int EPI> using MvTheta = typename std::conditional<EPI == kEpiQKV, RopeTheta, NoTheta>::type;
 
-template <int QT, int EPI> struct MvGroup {
+// Rows per work item: a row pair for the pair epilogues; otherwise the
+// format's own count, raised to 2 when each group walks several tiles (WIDE):
+// there more rows per item shorten each wave's chain of items (Q6_K down
+// projection 4096 x 14336: 17.1 us against 20.1 with one row), while on
+// single-tile matrices one row keeps more items in flight (Q6_K 4096 x 4096:
+// 6.2 us against 7.0).
+template <int QT, int EPI, bool WIDE = false> struct MvGroup {
     static constexpr bool kPairs = EPI == kEpiSwiGLU || EPI == kEpiQKV;
-    static constexpr int R = kPairs ? 2 : MvFmt<QT>::kRows;  // rows per group
+    static constexpr int kFmtRows = MvFmt<QT>::kRows;
+    static constexpr int R = kPairs ? 2 : (WIDE && kFmtRows < 2 ? 2 : kFmtRows);
     static __device__ __host__ int groups(const MvJob& j) {
         return EPI == kEpiSwiGLU ? j.rows : (j.rows + R - 1) / R;
     }
@@ -327,9 +335,9 @@ template <int QT, int EPI> struct MvGroup {
 
 // Row r of group g (clamped into the matrix: groups past the end re-read the
 // last row, whose result is never stored).
-template <int QT, int EPI>
+template <int QT, int EPI, bool WIDE = false>
 __device__ __forceinline__ const uint8_t* mv_row(const MvJob& j, int g, int r) {
-    constexpr int R = MvGroup<QT, EPI>::R;
+    constexpr int R = MvGroup<QT, EPI, WIDE>::R;
     if constexpr (EPI == kEpiSwiGLU) {
         const int row = g < j.rows ? g : j.rows - 1;
         return j.W[r] + (int64_t)row * j.row_bytes;
@@ -359,10 +367,10 @@ __device__ __forceinline__ void cache_store(void* c, int64_t i, float a, float b
 }
 
 // Finished values v[0..R) of group g (one lane).
-template <int QT, int EPI>
+template <int QT, int EPI, bool WIDE = false>
 __device__ __forceinline__ void mv_epilogue(const MvJob& j, const MvTheta<EPI>& th, int g,
-                                            float (&v)[MvGroup<QT, EPI>::R]) {
-    constexpr int R = MvGroup<QT, EPI>::R;
+                                            float (&v)[MvGroup<QT, EPI, WIDE>::R]) {
+    constexpr int R = MvGroup<QT, EPI, WIDE>::R;
     if constexpr (EPI == kEpiStore) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -407,7 +415,8 @@ template <int QT, bool ONE_TILE, int PRO, int EPI>
 __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
                                                                       MvTheta<EPI> th) {
     using F = MvFmt<QT>;
-    constexpr int R = MvGroup<QT, EPI>::R;
+    using G = MvGroup<QT, EPI, !ONE_TILE>;
+    constexpr int R = G::R;
     using T = MvTile<QT, R>;
     constexpr int CPL = T::kCPL;
     extern __shared__ uint4 lds[];
@@ -418,7 +427,7 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
     const int nb = job.nb;
     int nt = job.nt;
     uint4* stage = lds + (nt << 10) + wave * T::kStageChunks;
-    const int n_groups = MvGroup<QT, EPI>::groups(job);
+    const int n_groups = G::groups(job);
     const int stride = gridDim.x * waves;
     if (ONE_TILE) nt = 1;
 
@@ -429,7 +438,7 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
         const int nchunk = nbt * F::kBytes / 16;  // whole by the width granule
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint8_t* src = mv_row<QT, EPI>(job, g, r) + (int64_t)tb * F::kBytes;
+            const uint8_t* src = mv_row<QT, EPI, !ONE_TILE>(job, g, r) + (int64_t)tb * F::kBytes;
 #pragma unroll
             for (int k = 0; k < CPL; ++k) {
                 // Lanes past the tile's end re-read its last chunk (never used).
@@ -556,7 +565,7 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
                 v[r] = wave_sum_f32(acc[r]);
                 acc[r] = 0.0f;
             }
-            if (lane == 0) mv_epilogue<QT, EPI>(job, th, g, v);
+            if (lane == 0) mv_epilogue<QT, EPI, !ONE_TILE>(job, th, g, v);
         }
     };
 
@@ -647,30 +656,36 @@ template <int QT, int PRO, int EPI>
 static int mv_run(MvJob job, int cols, const MvTheta<EPI>& th, hipStream_t stream) {
     using F = MvFmt<QT>;
     using G = MvGroup<QT, EPI>;
-    using T = MvTile<QT, G::R>;
+    using GW = MvGroup<QT, EPI, true>;
     job.nb = cols / F::kElems;
     job.row_bytes = (int64_t)job.nb * F::kBytes;
     job.nt = (cols + kMvTileElems - 1) / kMvTileElems;
-    const int n_groups = G::groups(job);
+    const int n_groups = job.nt == 1 ? G::groups(job) : GW::groups(job);
     bool tiled = cols % F::kColGranule == 0 && job.nt <= kMvMaxTiles && aligned(job.x, 16);
     for (int s = 0; s < 3; ++s) tiled = tiled && aligned(job.W[s], 16);
     if (PRO == kProNorm) tiled = tiled && aligned(job.norm_w, job.norm_f16 ? 8 : 16);
     if (tiled) {
-        const int waves = job.nt == 1 ? 4 : 8;
+        const int stage_chunks = job.nt == 1 ? MvTile<QT, G::R>::kStageChunks
+                                             : MvTile<QT, GW::R>::kStageChunks;
+        // wide matrices: 8 waves share one copy of x, 4 where 8 staging
+        // regions and x would not fit in the 160 KiB of LDS (7-tile Q8_0 / Q6_K)
+        int waves = job.nt == 1 ? 4 : 8;
+        if ((size_t)(job.nt * 1024 + waves * stage_chunks) * 16 > kMvLdsBytes) waves = 4;
         int grid = (n_groups + waves - 1) / waves;
         // 512 workgroups (two per CU on 256 CUs) measured best for Q4_0 at
         // 4096-14336 rows; each wave then streams several items.
         if (grid > 512) grid = 512;
-        const size_t shmem = ((size_t)job.nt * 1024 + (size_t)waves * T::kStageChunks) * 16;
+        const size_t shmem = ((size_t)job.nt * 1024 + (size_t)waves * stage_chunks) * 16;
         if (job.nt == 1)
             return launch(matvec_kernel<QT, true, PRO, EPI>, dim3(grid), dim3(waves * kWave),
                           shmem, stream, job, th);
         return launch(matvec_kernel<QT, false, PRO, EPI>, dim3(grid), dim3(waves * kWave), shmem,
                       stream, job, th);
     }
-    if ((n_groups + 3) / 4 > 0x7FFFFFFF / 4) return JINF_HIP_ERR_INVALID;
-    return launch(matvec_any_kernel<QT, PRO, EPI>, dim3((n_groups + 3) / 4), dim3(256), 0, stream,
-                  job, th);
+    const int any_groups = G::groups(job);
+    if ((any_groups + 3) / 4 > 0x7FFFFFFF / 4) return JINF_HIP_ERR_INVALID;
+    return launch(matvec_any_kernel<QT, PRO, EPI>, dim3((any_groups + 3) / 4), dim3(256), 0,
+                  stream, job, th);
 }
 
 template <int PRO, int EPI>
