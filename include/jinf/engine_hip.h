@@ -22,6 +22,7 @@
 #include <stdint.h>
 #include "gguf_hip.h"
 #include "kernels_ext.h"
+#include "nvmw_hip.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -85,6 +86,17 @@ int jinf_hip_engine_create(jinf_hip_engine** out, const jinf_hip_engine_desc* de
  * upstream ggml's element order to jinf's (jinf_hip_q4_0_repack_ggml). */
 int jinf_hip_engine_create_gguf(jinf_hip_engine** out, const jinf_hip_gguf* file,
                                 int max_context, int kv_type, int q4_0_ggml_order);
+
+/* Same from a .nvmw file (the reference engine's model format,
+ * jinf_engine_create src/engine.cpp:40-188): hyper-parameters from its
+ * header; every tensor, hot or cold, is uploaded (the whole model stays
+ * resident, so the reference's NVMe streaming of cold layers has no
+ * counterpart); layer tensors are matched by layer index and name suffix as
+ * the reference does, token_embd / output_norm / output by exact name
+ * (output absent: tied to token_embd).  A neuron-bundle index is ignored:
+ * the FFN is decoded dense. */
+int jinf_hip_engine_create_nvmw(jinf_hip_engine** out, const jinf_hip_nvmw* file,
+                                int max_context, int kv_type);
 
 void jinf_hip_engine_destroy(jinf_hip_engine* e);
 

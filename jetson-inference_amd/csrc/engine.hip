@@ -18,6 +18,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <functional>
 #include <new>
 #include <string>
 #include <vector>
@@ -482,10 +483,18 @@ int create(jinf_hip_engine** out, const jinf_hip_engine_desc* desc, void* owned)
     return JINF_HIP_OK;
 }
 
-// ---- GGUF ----
+// ---- model files ----
+
+// The layer tensors the forward loop reads, in the order the reference
+// assigns them by name (src/engine.cpp:150-158).
+constexpr const char* kLayerSlots[9] = {"attn_norm.weight", "ffn_norm.weight", "attn_q.weight",
+                                        "attn_k.weight",    "attn_v.weight",   "attn_output.weight",
+                                        "ffn_gate.weight",  "ffn_up.weight",   "ffn_down.weight"};
 
 struct Want {
-    std::string name;
+    std::string name;    // file tensor name (GGUF convention)
+    int layer = -1;      // layer tensors: layer and slot in kLayerSlots
+    int slot = -1;
     int64_t cols, rows;  // GGUF ne0, ne1 (rows 1 for a vector)
     bool matrix, optional;
     const void** ptr;
@@ -493,6 +502,111 @@ struct Want {
     int64_t index = -1;
     size_t offset = 0;
 };
+
+// What the loader needs to know about one tensor of a model file.
+struct FileTensor {
+    int qtype;
+    uint32_t n_dims;
+    const int64_t* shape;
+    uint64_t n_bytes;
+};
+
+// A model file: tensor lookup, description and upload.
+struct ModelFile {
+    std::function<int64_t(const Want&)> find;  // index or -1
+    std::function<FileTensor(int64_t)> info;
+    std::function<int(int64_t, void*, uint64_t, hipStream_t)> upload;
+};
+
+// Every tensor the forward loop reads is uploaded into one device allocation
+// the engine owns (tensor starts 256-byte aligned), shapes and formats are
+// checked, then the engine is created on them.
+int create_from_file(jinf_hip_engine** out, jinf_hip_engine_desc d, const ModelFile& file,
+                     int q4_0_ggml_order) {
+    if (d.n_layers < 0 || d.n_embd <= 0 || d.n_heads <= 0 || d.n_heads_kv <= 0 ||
+        d.n_embd % d.n_heads != 0) {
+        JINF_LOG("engine: model hyper-parameters incomplete");
+        return JINF_HIP_ERR_PARSE;
+    }
+    const int64_t n = d.n_embd, kvd = (int64_t)d.n_heads_kv * (d.n_embd / d.n_heads);
+    std::vector<jinf_hip_layer_weights> layers((size_t)d.n_layers);
+    std::vector<Want> want;
+    auto add = [&](const std::string& name, int layer, int slot, int64_t cols, int64_t rows,
+                   bool matrix, bool opt, const void** p, int32_t* t) {
+        Want w;
+        w.name = name;
+        w.layer = layer;
+        w.slot = slot;
+        w.cols = cols;
+        w.rows = rows;
+        w.matrix = matrix;
+        w.optional = opt;
+        w.ptr = p;
+        w.type = t;
+        want.push_back(w);
+    };
+    add("token_embd.weight", -1, -1, n, d.n_vocab, true, false, &d.token_embd, &d.token_embd_type);
+    for (int L = 0; L < d.n_layers; ++L) {
+        jinf_hip_layer_weights& w = layers[L];
+        const std::string b = "blk." + std::to_string(L) + ".";
+        const void** ptrs[9] = {&w.attn_norm, &w.ffn_norm, &w.attn_q, &w.attn_k, &w.attn_v,
+                                &w.attn_output, &w.ffn_gate, &w.ffn_up, &w.ffn_down};
+        int32_t* types[9] = {&w.attn_norm_type, &w.ffn_norm_type, &w.attn_q_type,
+                             &w.attn_k_type, &w.attn_v_type, &w.attn_output_type,
+                             &w.ffn_gate_type, &w.ffn_up_type, &w.ffn_down_type};
+        const int64_t cols[9] = {n, n, n, n, n, n, n, n, d.n_ff};
+        const int64_t rows[9] = {1, 1, n, kvd, kvd, n, d.n_ff, d.n_ff, n};
+        for (int k = 0; k < 9; ++k)
+            add(b + kLayerSlots[k], L, k, cols[k], rows[k], k >= 2, false, ptrs[k], types[k]);
+    }
+    add("output_norm.weight", -1, -1, n, 1, false, true, &d.output_norm, &d.output_norm_type);
+    add("output.weight", -1, -1, n, d.n_vocab, true, true, &d.output, &d.output_type);
+
+    size_t total = 0;
+    for (Want& w : want) {
+        w.index = file.find(w);
+        if (w.index < 0) {
+            if (w.optional) continue;
+            JINF_LOG("engine: tensor %s not in the file", w.name.c_str());
+            return JINF_HIP_ERR_PARSE;
+        }
+        const FileTensor t = file.info(w.index);
+        const int64_t rows = t.n_dims >= 2 ? t.shape[1] : 1;
+        bool ok = t.shape[0] == w.cols && rows == w.rows && t.n_dims <= 2;
+        ok = ok && (w.matrix ? (is_matrix_type(t.qtype) || is_dense_type(t.qtype))
+                             : is_dense_type(t.qtype));
+        ok = ok && weight_bytes(t.qtype, rows, t.shape[0]) == t.n_bytes;
+        if (!ok) {
+            JINF_LOG("engine: tensor %s: shape or type %d not usable", w.name.c_str(), t.qtype);
+            return JINF_HIP_ERR_INVALID;
+        }
+        w.offset = total;
+        total = up_to(total + t.n_bytes, kAlign);
+        *w.type = t.qtype;
+    }
+    void* dev = nullptr;
+    hipStream_t s = nullptr;
+    int rc = hip_ok(hipMalloc(&dev, total ? total : kAlign), "hipMalloc");
+    if (rc == JINF_HIP_OK)
+        rc = hip_ok(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+    for (Want& w : want) {
+        if (rc != JINF_HIP_OK) break;
+        if (w.index < 0) continue;
+        const FileTensor t = file.info(w.index);
+        char* p = static_cast<char*>(dev) + w.offset;
+        rc = file.upload(w.index, p, t.n_bytes, s);
+        if (rc == JINF_HIP_OK && q4_0_ggml_order && t.qtype == kQ4_0)
+            rc = jinf_hip_q4_0_repack_ggml(p, (int64_t)(t.n_bytes / 18), s);
+        *w.ptr = p;
+    }
+    if (rc == JINF_HIP_OK) rc = hip_ok(hipStreamSynchronize(s), "hipStreamSynchronize");
+    if (s) (void)hipStreamDestroy(s);
+    d.layers = layers.data();
+    if (rc == JINF_HIP_OK) rc = validate(&d);
+    if (rc == JINF_HIP_OK) rc = create(out, &d, dev);
+    else if (dev) (void)hipFree(dev);
+    return rc;
+}
 
 }  // namespace
 
@@ -520,87 +634,64 @@ extern "C" int jinf_hip_engine_create_gguf(jinf_hip_engine** out, const jinf_hip
     d.rms_norm_eps = hp->rms_norm_eps;
     d.rope_freq_base = hp->rope_freq_base;
     d.kv_type = kv_type;
-    if (d.n_layers < 0 || d.n_embd <= 0 || d.n_heads <= 0 || d.n_heads_kv <= 0 ||
-        d.n_embd % d.n_heads != 0) {
-        JINF_LOG("engine: GGUF hyper-parameters incomplete");
-        return JINF_HIP_ERR_PARSE;
-    }
-    const int64_t n = d.n_embd, kvd = (int64_t)d.n_heads_kv * (d.n_embd / d.n_heads);
-    std::vector<jinf_hip_layer_weights> layers((size_t)d.n_layers);
-    std::vector<Want> want;
-    auto add = [&](const std::string& name, int64_t cols, int64_t rows, bool matrix, bool opt,
-                   const void** p, int32_t* t) {
-        Want w;
-        w.name = name;
-        w.cols = cols;
-        w.rows = rows;
-        w.matrix = matrix;
-        w.optional = opt;
-        w.ptr = p;
-        w.type = t;
-        want.push_back(w);
+    ModelFile f;
+    f.find = [&](const Want& w) { return jinf_hip_gguf_find_tensor(file, w.name.c_str()); };
+    f.info = [&](int64_t i) {
+        const jinf_hip_gguf_tensor* t = jinf_hip_gguf_tensor_at(file, (uint64_t)i);
+        return FileTensor{t->qtype, t->n_dims, t->shape, t->n_bytes};
     };
-    add("token_embd.weight", n, d.n_vocab, true, false, &d.token_embd, &d.token_embd_type);
-    for (int L = 0; L < d.n_layers; ++L) {
-        jinf_hip_layer_weights& w = layers[L];
-        const std::string b = "blk." + std::to_string(L) + ".";
-        add(b + "attn_norm.weight", n, 1, false, false, &w.attn_norm, &w.attn_norm_type);
-        add(b + "attn_q.weight", n, n, true, false, &w.attn_q, &w.attn_q_type);
-        add(b + "attn_k.weight", n, kvd, true, false, &w.attn_k, &w.attn_k_type);
-        add(b + "attn_v.weight", n, kvd, true, false, &w.attn_v, &w.attn_v_type);
-        add(b + "attn_output.weight", n, n, true, false, &w.attn_output, &w.attn_output_type);
-        add(b + "ffn_norm.weight", n, 1, false, false, &w.ffn_norm, &w.ffn_norm_type);
-        add(b + "ffn_gate.weight", n, d.n_ff, true, false, &w.ffn_gate, &w.ffn_gate_type);
-        add(b + "ffn_up.weight", n, d.n_ff, true, false, &w.ffn_up, &w.ffn_up_type);
-        add(b + "ffn_down.weight", d.n_ff, n, true, false, &w.ffn_down, &w.ffn_down_type);
-    }
-    add("output_norm.weight", n, 1, false, true, &d.output_norm, &d.output_norm_type);
-    add("output.weight", n, d.n_vocab, true, true, &d.output, &d.output_type);
+    f.upload = [&](int64_t i, void* dst, uint64_t bytes, hipStream_t s) {
+        return jinf_hip_gguf_upload(file, (uint64_t)i, dst, bytes, s);
+    };
+    return create_from_file(out, d, f, q4_0_ggml_order);
+}
 
-    size_t total = 0;
-    for (Want& w : want) {
-        w.index = jinf_hip_gguf_find_tensor(file, w.name.c_str());
-        if (w.index < 0) {
-            if (w.optional) continue;
-            JINF_LOG("engine: tensor %s not in the file", w.name.c_str());
-            return JINF_HIP_ERR_PARSE;
-        }
-        const jinf_hip_gguf_tensor* t = jinf_hip_gguf_tensor_at(file, (uint64_t)w.index);
-        const int64_t rows = t->n_dims >= 2 ? t->shape[1] : 1;
-        bool ok = t->shape[0] == w.cols && rows == w.rows && t->n_dims <= 2;
-        ok = ok && (w.matrix ? (is_matrix_type(t->qtype) || is_dense_type(t->qtype))
-                             : is_dense_type(t->qtype));
-        ok = ok && weight_bytes(t->qtype, rows, t->shape[0]) == t->n_bytes;
-        if (!ok) {
-            JINF_LOG("engine: tensor %s: shape or type %d not usable", w.name.c_str(), t->qtype);
-            return JINF_HIP_ERR_INVALID;
-        }
-        w.offset = total;
-        total = up_to(total + t->n_bytes, kAlign);
-        *w.type = t->qtype;
+extern "C" int jinf_hip_engine_create_nvmw(jinf_hip_engine** out, const jinf_hip_nvmw* file,
+                                           int max_context, int kv_type) {
+    if (!out || !file || max_context <= 0) return JINF_HIP_ERR_INVALID;
+    *out = nullptr;
+    const jinf_hip_nvmw_header* h = jinf_hip_nvmw_header_of(file);
+    jinf_hip_engine_desc d{};
+    d.n_layers = (int)h->n_layers;
+    d.n_embd = (int)h->n_embd;
+    d.n_heads = (int)h->n_heads;
+    d.n_heads_kv = (int)h->n_heads_kv;
+    d.n_ff = (int)h->n_ff;
+    d.n_vocab = (int)h->n_vocab;
+    d.max_context = max_context;
+    d.rms_norm_eps = h->rms_norm_eps;
+    d.rope_freq_base = h->rope_freq_base;
+    d.kv_type = kv_type;
+    // Layer tensors by layer index and name, the reference's rule
+    // (src/engine.cpp:135-159): an entry of layer L whose name contains a
+    // slot's suffix fills that slot (the first suffix that matches; a later
+    // entry for the same slot replaces an earlier one).  The others by exact
+    // name (src/engine.cpp:170-188).
+    const int n_layers = d.n_layers > 0 ? d.n_layers : 0;
+    std::vector<int64_t> slot((size_t)n_layers * 9, -1);
+    const uint64_t nt = jinf_hip_nvmw_n_tensors(file);
+    for (uint64_t i = 0; i < nt; ++i) {
+        const jinf_hip_nvmw_tensor* t = jinf_hip_nvmw_tensor_at(file, i);
+        if (t->layer_index < 0 || t->layer_index >= n_layers) continue;
+        for (int k = 0; k < 9; ++k)
+            if (strstr(t->name, kLayerSlots[k])) {
+                slot[(size_t)t->layer_index * 9 + k] = (int64_t)i;
+                break;
+            }
     }
-    void* dev = nullptr;
-    hipStream_t s = nullptr;
-    int rc = hip_ok(hipMalloc(&dev, total ? total : kAlign), "hipMalloc");
-    if (rc == JINF_HIP_OK)
-        rc = hip_ok(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
-    for (Want& w : want) {
-        if (rc != JINF_HIP_OK) break;
-        if (w.index < 0) continue;
-        const jinf_hip_gguf_tensor* t = jinf_hip_gguf_tensor_at(file, (uint64_t)w.index);
-        char* p = static_cast<char*>(dev) + w.offset;
-        rc = jinf_hip_gguf_upload(file, (uint64_t)w.index, p, t->n_bytes, s);
-        if (rc == JINF_HIP_OK && q4_0_ggml_order && t->qtype == kQ4_0)
-            rc = jinf_hip_q4_0_repack_ggml(p, (int64_t)(t->n_bytes / 18), s);
-        *w.ptr = p;
-    }
-    if (rc == JINF_HIP_OK) rc = hip_ok(hipStreamSynchronize(s), "hipStreamSynchronize");
-    if (s) (void)hipStreamDestroy(s);
-    d.layers = layers.data();
-    if (rc == JINF_HIP_OK) rc = validate(&d);
-    if (rc == JINF_HIP_OK) rc = create(out, &d, dev);
-    else if (dev) (void)hipFree(dev);
-    return rc;
+    ModelFile f;
+    f.find = [&](const Want& w) -> int64_t {
+        if (w.layer >= 0) return slot[(size_t)w.layer * 9 + w.slot];
+        return jinf_hip_nvmw_find_tensor(file, w.name.c_str());
+    };
+    f.info = [&](int64_t i) {
+        const jinf_hip_nvmw_tensor* t = jinf_hip_nvmw_tensor_at(file, (uint64_t)i);
+        return FileTensor{t->qtype, t->n_dims, t->shape, t->n_bytes};
+    };
+    f.upload = [&](int64_t i, void* dst, uint64_t bytes, hipStream_t s) {
+        return jinf_hip_nvmw_upload(file, (uint64_t)i, dst, bytes, s);
+    };
+    return create_from_file(out, d, f, 0);
 }
 
 extern "C" void jinf_hip_engine_destroy(jinf_hip_engine* e) { release(e); }

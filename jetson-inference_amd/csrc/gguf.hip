@@ -37,6 +37,7 @@
 #include <string>
 #include <vector>
 
+#include "file_io.h"
 #include "jinf_device.h"
 #include "jinf_host.h"
 #include "jinf/gguf_hip.h"
@@ -399,52 +400,8 @@ extern "C" int jinf_hip_gguf_upload(const jinf_hip_gguf* g, uint64_t i, void* ds
     if (!g || i >= g->tensors.size() || !dst) return JINF_HIP_ERR_INVALID;
     const jinf_hip_gguf_tensor& t = g->tensors[i];
     if (dst_bytes < t.n_bytes) return JINF_HIP_ERR_INVALID;
-    if (t.n_bytes == 0) return JINF_HIP_OK;
-    const int fd = open(g->path.c_str(), O_RDONLY);
-    if (fd < 0) {
-        JINF_LOG("Failed to open %s: %s", g->path.c_str(), strerror(errno));
-        return JINF_HIP_ERR_IO;
-    }
-    constexpr size_t kChunk = 32u << 20;
-    void* stage[2] = {nullptr, nullptr};
-    hipEvent_t done[2] = {nullptr, nullptr};
-    int rc = JINF_HIP_OK;
-    for (int b = 0; b < 2 && rc == JINF_HIP_OK; ++b) {
-        if (hipHostMalloc(&stage[b], kChunk, hipHostMallocDefault) != hipSuccess ||
-            hipEventCreateWithFlags(&done[b], hipEventDisableTiming) != hipSuccess)
-            rc = JINF_HIP_ERR_DEVICE;
-    }
-    const uint64_t base = g->data_offset + t.offset;
-    for (uint64_t off = 0, k = 0; rc == JINF_HIP_OK && off < t.n_bytes; off += kChunk, ++k) {
-        const int b = (int)(k & 1);
-        const size_t n = (size_t)(t.n_bytes - off < kChunk ? t.n_bytes - off : kChunk);
-        if (k >= 2 && hipEventSynchronize(done[b]) != hipSuccess) {  // buffer b free again
-            rc = JINF_HIP_ERR_DEVICE;
-            break;
-        }
-        size_t got = 0;
-        while (got < n) {
-            const ssize_t r = pread(fd, (char*)stage[b] + got, n - got, (off_t)(base + off + got));
-            if (r <= 0) break;
-            got += (size_t)r;
-        }
-        if (got != n) {
-            rc = JINF_HIP_ERR_IO;
-            break;
-        }
-        if (hipMemcpyAsync((char*)dst + off, stage[b], n, hipMemcpyHostToDevice, stream) !=
-                hipSuccess ||
-            hipEventRecord(done[b], stream) != hipSuccess)
-            rc = JINF_HIP_ERR_DEVICE;
-    }
-    // the staging buffers are released only after every copy from them ended
-    if (hipStreamSynchronize(stream) != hipSuccess && rc == JINF_HIP_OK) rc = JINF_HIP_ERR_DEVICE;
-    for (int b = 0; b < 2; ++b) {
-        if (done[b]) (void)hipEventDestroy(done[b]);
-        if (stage[b]) (void)hipHostFree(stage[b]);
-    }
-    close(fd);
-    return rc;
+    return jinf::upload_file_range(g->path.c_str(), g->data_offset + t.offset, t.n_bytes, dst,
+                                   stream);
 }
 
 extern "C" int jinf_hip_q4_0_repack_ggml(void* blocks, int64_t n_blocks, hipStream_t stream) {

@@ -2,8 +2,8 @@
 reduction path -- RMSNorm (+ fused residual add), interleaved GQA RoPE,
 SwiGLU, masked row softmax and the GGUF Q4_0 token-embedding gather -- and,
 beside them, the dequant-GEMV and row dequant for GGUF Q4_0 / Q8_0 / Q4_K /
-Q6_K weights, GQA decode attention, GGUF files and the decode engine that
-runs them all per token.
+Q6_K weights, GQA decode attention, GGUF and .nvmw model files and the
+decode engine that runs them all per token.
 
 The kernels live in libjinf_hip.so behind the C-ABI of include/jinf/*.h;
 this package is a thin ctypes/torch front end used by tests and bench.py.
@@ -38,4 +38,5 @@ from .ops import (  # noqa: F401
     swiglu,
 )
 from . import gguf  # noqa: F401,E402
+from . import nvmw  # noqa: F401,E402
 from .engine import Engine, EngineError  # noqa: F401,E402

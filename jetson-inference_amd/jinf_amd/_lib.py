@@ -84,9 +84,21 @@ SIGNATURES = {
     "jinf_hip_gguf_tensor_at": (_P, [_P, ctypes.c_uint64]),
     "jinf_hip_gguf_upload": (_I, [_P, ctypes.c_uint64, _P, ctypes.c_uint64, _P]),
     "jinf_hip_q4_0_repack_ggml": (_I, [_P, ctypes.c_int64, _P]),
+    # .nvmw files (include/jinf/nvmw_hip.h)
+    "jinf_hip_nvmw_load": (_I, [ctypes.POINTER(_P), ctypes.c_char_p]),
+    "jinf_hip_nvmw_free": (None, [_P]),
+    "jinf_hip_nvmw_header_of": (_P, [_P]),
+    "jinf_hip_nvmw_n_tensors": (ctypes.c_uint64, [_P]),
+    "jinf_hip_nvmw_tensor_at": (_P, [_P, ctypes.c_uint64]),
+    "jinf_hip_nvmw_find_tensor": (ctypes.c_int64, [_P, ctypes.c_char_p]),
+    "jinf_hip_nvmw_layer_cold_range": (_I, [_P, _I, ctypes.POINTER(ctypes.c_uint64),
+                                            ctypes.POINTER(ctypes.c_uint64)]),
+    "jinf_hip_nvmw_has_bundles": (_I, [_P]),
+    "jinf_hip_nvmw_upload": (_I, [_P, ctypes.c_uint64, _P, ctypes.c_uint64, _P]),
     # decode engine (include/jinf/engine_hip.h)
     "jinf_hip_engine_create": (_I, [ctypes.POINTER(_P), _P]),
     "jinf_hip_engine_create_gguf": (_I, [ctypes.POINTER(_P), _P, _I, _I, _I]),
+    "jinf_hip_engine_create_nvmw": (_I, [ctypes.POINTER(_P), _P, _I, _I]),
     "jinf_hip_engine_destroy": (None, [_P]),
     "jinf_hip_engine_reset": (_I, [_P]),
     "jinf_hip_engine_n_past": (_I, [_P]),

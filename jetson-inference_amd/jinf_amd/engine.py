@@ -48,7 +48,8 @@ def _check(what, rc):
 
 class Engine:
     """A jinf_hip_engine.  Build it from device weights (``Engine(...)``) or
-    from a GGUF file (``Engine.from_gguf``); ``close()`` frees it."""
+    from a GGUF or .nvmw file (``Engine.from_gguf``, ``Engine.from_nvmw``);
+    ``close()`` frees it."""
 
     def __init__(self, hparams, weights, max_context, kv_type=F32, _handle=None):
         self._keep = []
@@ -103,6 +104,18 @@ class Engine:
                lib().jinf_hip_engine_create_gguf(ctypes.byref(h), f._h, int(max_context),
                                                  int(kv_type), int(bool(q4_0_ggml_order))))
         return cls(f.hparams, None, max_context, kv_type, _handle=h)
+
+    @classmethod
+    def from_nvmw(cls, nvmw_file, max_context, kv_type=F16):
+        """nvmw_file: a jinf_amd.nvmw.NVMWFile (or a path)."""
+        from .nvmw import NVMWFile
+
+        f = nvmw_file if isinstance(nvmw_file, NVMWFile) else NVMWFile(nvmw_file)
+        h = ctypes.c_void_p()
+        _check("jinf_hip_engine_create_nvmw",
+               lib().jinf_hip_engine_create_nvmw(ctypes.byref(h), f._h, int(max_context),
+                                                 int(kv_type)))
+        return cls(f.header, None, max_context, kv_type, _handle=h)
 
     def close(self):
         if getattr(self, "_h", None):

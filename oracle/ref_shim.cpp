@@ -95,3 +95,55 @@ extern "C" int jref_gguf_dump(const char* path, char* out, int cap) {
     out[n] = 0;
     return (int)st;
 }
+
+// ---- .nvmw reader (src/nvmw.cpp) ----
+// jref_nvmw_dump: open a file with the reference reader and print what it
+// parsed, one item per line, in the format the tests build from this
+// repository's reader.  Returns the jinf_status of the open.
+#include "jinf/nvmw.h"
+
+extern "C" int jref_nvmw_dump(const char* path, char* out, int cap) {
+    jinf_nvmw_reader* r = nullptr;
+    const jinf_status st = jinf_nvmw_open(&r, path);
+    std::string s;
+    if (st == JINF_OK) {
+        char b[512];
+        const jinf_nvmw_header* h = jinf_nvmw_get_header(r);
+        snprintf(b, sizeof b,
+                 "header %u %u %u %u %llu %llu %llu %llu %llu %llu\n"
+                 "hparams %u %u %u %u %u %u %.9g %.9g %d %llu\n",
+                 h->magic, h->version, h->n_layers, h->n_tensors,
+                 (unsigned long long)h->index_offset, (unsigned long long)h->index_size,
+                 (unsigned long long)h->hot_offset, (unsigned long long)h->hot_size,
+                 (unsigned long long)h->cold_start_offset, (unsigned long long)h->cold_total_size,
+                 h->n_embd, h->n_heads, h->n_heads_kv, h->n_ff, h->n_vocab, h->n_ctx_train,
+                 (double)h->rope_freq_base, (double)h->rms_norm_eps, (int)h->primary_type,
+                 (unsigned long long)h->bundle_index_offset);
+        s += b;
+        for (int L = 0; L < (int)h->n_layers; ++L) {
+            uint64_t off = 0, size = 0;
+            jinf_nvmw_get_layer_cold_range(r, L, &off, &size);
+            snprintf(b, sizeof b, "layer %d %llu %llu\n", L, (unsigned long long)off,
+                     (unsigned long long)size);
+            s += b;
+        }
+        int n = 0;
+        const jinf_nvmw_tensor_entry* te = jinf_nvmw_get_tensor_entries(r, &n);
+        for (int i = 0; i < n; ++i) {
+            const jinf_nvmw_tensor_entry& t = te[i];
+            snprintf(b, sizeof b, "tensor %s %d %lld %lld %lld %lld %u %llu %llu %d %d\n", t.name,
+                     (int)t.type, (long long)t.shape[0], (long long)t.shape[1],
+                     (long long)t.shape[2], (long long)t.shape[3], t.n_dims,
+                     (unsigned long long)t.offset, (unsigned long long)t.n_bytes, t.layer_index,
+                     (int)t.is_hot);
+            s += b;
+        }
+        snprintf(b, sizeof b, "bundles %d\n", jinf_nvmw_has_bundles(r) ? 1 : 0);
+        s += b;
+        jinf_nvmw_close(r);
+    }
+    const size_t n = s.size() < (size_t)cap - 1 ? s.size() : (size_t)cap - 1;
+    memcpy(out, s.data(), n);
+    out[n] = 0;
+    return (int)st;
+}

@@ -110,3 +110,54 @@ def write_gguf(path, hp, W, q4_0_ggml_order=False, alignment=32):
         data = q4_0_to_ggml_order(a) if (qt == Q4_0 and q4_0_ggml_order) else a
         tensors.append((name, shape, qt, np.ascontiguousarray(data).tobytes()))
     return gw.write(path, kvs, tensors, alignment=alignment)
+
+
+def gguf_shape(hp, name, a):
+    """GGUF dimensions (ne0 = cols first) of a weight of the tiny model."""
+    if name.endswith("norm.weight"):
+        return [a.shape[0]]
+    cols = hp["n_ff"] if name.endswith("ffn_down.weight") else hp["n_embd"]
+    return [cols, a.shape[0]]
+
+
+def _layer_of(name):
+    return int(name.split(".")[1]) if name.startswith("blk.") else -1
+
+
+def write_nvmw(path, hp, W, cold_layers=(), bundled=False, primary_type=None, order=None):
+    """A .nvmw file of the model as prepare_model lays it out: the tensors of
+    layers in cold_layers in their layer's cold region, everything else hot.
+    bundled: also the version-2 neuron bundles (gate row, up row, and the
+    down column as fp32, padded to 4 KiB; tools/prepare_model.cpp:296-490).
+    order: tensor names in file order (default: W's order)."""
+    import nvmw_writer as nw
+
+    names = list(W) if order is None else list(order)
+    tensors = []
+    for name in names:
+        a, qt = W[name]
+        L = _layer_of(name)
+        tensors.append((name, qt, gguf_shape(hp, name, a), np.ascontiguousarray(a).tobytes(), L,
+                        L not in cold_layers))
+    if primary_type is None:
+        primary_type = W["blk.0.ffn_gate.weight"][1]
+    bundles = None
+    if bundled:
+        n_embd, n_ff = hp["n_embd"], hp["n_ff"]
+        bs, bb = oracle.qtype_geometry(primary_type)
+        row = (n_embd + bs - 1) // bs * bb
+        size = nw.align4k(2 * row + 4 * n_embd)
+        per_layer = []
+        for L in range(hp["n_layers"]):
+            g, gq = W[f"blk.{L}.ffn_gate.weight"]
+            u, uq = W[f"blk.{L}.ffn_up.weight"]
+            dn, dq = W[f"blk.{L}.ffn_down.weight"]
+            gb = np.ascontiguousarray(g).view(np.uint8).reshape(n_ff, -1)
+            ub = np.ascontiguousarray(u).view(np.uint8).reshape(n_ff, -1)
+            dense = dq in (F32, F16)
+            dcol = (dn.astype(np.float32) if dense else oracle.dequant(dq, dn)).reshape(n_embd, n_ff)
+            per_layer.append([(gb[j].tobytes() + ub[j].tobytes() +
+                               np.ascontiguousarray(dcol[:, j]).tobytes()).ljust(size, b"\0")
+                              for j in range(n_ff)])
+        bundles = (size, n_ff, per_layer)
+    return nw.write(path, hp, tensors, primary_type=primary_type, bundles=bundles)
