@@ -28,11 +28,9 @@
 // in its high nibble.  jinf_hip_q4_0_repack_ggml rewrites blocks written in
 // the upstream order into jinf's order on the GPU, in place.
 #include <errno.h>
-#include <fcntl.h>
 #include <stdio.h>
 #include <string.h>
 #include <sys/stat.h>
-#include <unistd.h>
 
 #include <string>
 #include <vector>
