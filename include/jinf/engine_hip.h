@@ -133,6 +133,46 @@ int jinf_hip_engine_use_graph(jinf_hip_engine* e, int on);
  * row, the norms): the numerator of the decode bandwidth. */
 uint64_t jinf_hip_engine_step_weight_bytes(const jinf_hip_engine* e);
 
+/* ---- Batched decode: n_seq (1..64) sequences decoded together on one
+ * engine's weights (the engine must outlive the batch).  Each sequence has
+ * its own position and its own region of a batched KV cache
+ * [n_layers][n_seq][max_context][n_heads_kv * head_dim] of kv_type; one step
+ * decodes one token for every sequence that has one, with every GEMV run for
+ * all of them at once on the matrix cores (jinf_*_batch), so each weight
+ * byte is read once per step.  The reference has no counterpart: it decodes
+ * one sequence (src/engine.cpp:684-805); per sequence the arithmetic is that
+ * loop's.  Needs n_embd and n_ff multiples of 256. ---- */
+typedef struct jinf_hip_batch jinf_hip_batch;
+
+int  jinf_hip_batch_create(jinf_hip_batch** out, const jinf_hip_engine* engine, int n_seq,
+                           int max_context, int kv_type);
+void jinf_hip_batch_destroy(jinf_hip_batch* b);
+
+/* Clears sequence seq's KV region and position (every sequence when seq < 0). */
+int  jinf_hip_batch_reset(jinf_hip_batch* b, int seq);
+int  jinf_hip_batch_n_past(const jinf_hip_batch* b, int seq);
+
+/* One step: tokens[s] (n_seq ids, -1 = sequence s idle this step) decoded at
+ * each sequence's position; *logits receives the device pointer of the
+ * [n_seq][n_vocab] fp32 logits (an idle sequence's row is unspecified).
+ * Returns after the work has finished.  Status 5 for an id outside
+ * [-1, n_vocab) or a token for a sequence whose context is full. */
+int  jinf_hip_batch_forward(jinf_hip_batch* b, const int32_t* tokens, const float** logits);
+
+/* Greedy generation for `steps` steps (jinf_hip_engine_generate per
+ * sequence): at each step every sequence emits its last argmax (the one
+ * computed by the previous forward or generate step) into output[step *
+ * n_seq + s] and decodes it; a sequence that emits token 2 (end of
+ * sequence), has no token, or has a full context stops and emits -1 from
+ * then on. */
+int  jinf_hip_batch_generate(jinf_hip_batch* b, int32_t* output, int steps);
+
+/* Copies the last step's [n_seq][n_vocab] logits to dst (host or device). */
+int  jinf_hip_batch_copy_logits(const jinf_hip_batch* b, float* dst);
+
+/* 1 (default): replay the captured step as a HIP graph; 0: launch eagerly. */
+int  jinf_hip_batch_use_graph(jinf_hip_batch* b, int on);
+
 #ifdef __cplusplus
 }
 #endif

@@ -184,6 +184,69 @@ int jinf_rmsnorm_qkv_rope(const void* w_q, const void* w_k, const void* w_v, int
                           const int32_t* pos, int max_ctx, int head_dim, int n_heads,
                           int n_heads_kv, float freq_base, hipStream_t stream);
 
+/* ---- Batched dequant-GEMVs on the matrix cores: the per-token products of
+ * src/engine.cpp:429-508 for n_batch (1..64) sequences decoded together, so
+ * that each weight byte read serves all of them.  Row b of x / h / y is
+ * ld_x / ld_h / ld_y elements after row b - 1.  Same weights and formats as
+ * jinf_matvec with cols a multiple of 256 and every matrix 16-byte aligned
+ * (the bytes up to the next 16-byte boundary past a matrix's end are read, as
+ * any device allocation allows; other shapes return 5), x / h 16-byte aligned
+ * with ld a multiple of 4.  Products are exact fp16 x fp16 on the matrix
+ * cores with x split into two fp16 halves under a power-of-two scale per 256
+ * columns (about 22 significant bits); each result equals the fp32 dot
+ * product up to the fp32 rounding of the sums.
+ *
+ * RMSNorm variants: x^ = fl32(fl32(h * rs) * g) exactly as jinf_rmsnorm_rows
+ * computes it (norm_w NULL: x^ = h); norm_type 0 fp32, 1 fp16.
+ *
+ * Workspace (required): jinf_matvec_batch_workspace_bytes(rows, cols,
+ * n_batch) bytes, 256-byte aligned and zero-filled before its first use.  It
+ * holds x prepared for the matrix cores and, for launches that split the
+ * columns over several workgroups, their partial sums and counters (the
+ * counters return to zero at the end of every call, so the workspace is
+ * reused without clearing, also across graph replays).  One workspace must
+ * not be used by two calls that may run at the same time. ---- */
+
+size_t jinf_matvec_batch_workspace_bytes(int rows, int cols, int n_batch);
+
+/* y[b] = W x[b]. */
+int jinf_matvec_batch(const void* weight, int qtype, const float* x, int ld_x, float* y,
+                      int ld_y, int rows, int cols, int n_batch, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream);
+
+/* y[b] += W x[b] (output projection / down projection + residual add,
+ * src/engine.cpp:461-466, :504-508). */
+int jinf_matvec_batch_add(const void* weight, int qtype, const float* x, int ld_x, float* y,
+                          int ld_y, int rows, int cols, int n_batch, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream);
+
+/* y[b] = W x^[b]: RMSNorm + GEMV (src/engine.cpp:738+744). */
+int jinf_rmsnorm_matvec_batch(const void* weight, int qtype, const float* h, int ld_h,
+                              const void* norm_w, int norm_type, float eps, float* y, int ld_y,
+                              int rows, int cols, int n_batch, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream);
+
+/* y[b][i] = silu((W_gate x^[b])_i) * (W_up x^[b])_i (src/engine.cpp:487-502);
+ * i < n_ff. */
+int jinf_rmsnorm_swiglu_matvec_batch(const void* w_gate, const void* w_up, int qtype,
+                                     const float* h, int ld_h, const void* norm_w, int norm_type,
+                                     float eps, float* y, int ld_y, int n_ff, int cols,
+                                     int n_batch, void* workspace, size_t workspace_bytes,
+                                     hipStream_t stream);
+
+/* jinf_rmsnorm_qkv_rope for n_batch sequences: sequence b's q row goes to
+ * q + b * ld_q, its K / V rows to k_cache / v_cache + b * ld_seq +
+ * positions[b] * n_heads_kv * head_dim (elements of kv_type), RoPE at
+ * positions[b]; a position outside [0, max_ctx) skips that sequence's cache
+ * stores.  cols = n_embd. */
+int jinf_rmsnorm_qkv_rope_batch(const void* w_q, const void* w_k, const void* w_v, int qtype,
+                                const float* h, int ld_h, const void* norm_w, int norm_type,
+                                float eps, int cols, float* q, int ld_q, void* k_cache,
+                                void* v_cache, int kv_type, int64_t ld_seq,
+                                const int32_t* positions, int max_ctx, int head_dim, int n_heads,
+                                int n_heads_kv, float freq_base, int n_batch, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream);
+
 /* Gather + dequant of table rows for any qtype above (the engine's embedding
  * dispatch by table type, src/engine.cpp:311-334): output row i (ld_out
  * elements apart) is table row ids[i] (row i when ids is NULL), n_embd values

@@ -27,6 +27,8 @@
 #include "jinf_device.h"
 #include "jinf_host.h"
 #include "quant_device.h"
+#include "argmax_device.h"
+#include "engine_internal.h"
 
 namespace jinf {
 namespace {
@@ -34,7 +36,6 @@ namespace {
 // Words of the device state block.
 enum { kPos = 0, kLen = 1, kTok = 2, kBest = 3, kFillEnd = 4, kStateWords = 64 };
 constexpr int kEos = 2;            // end-of-sequence id (src/engine.cpp:796-797)
-constexpr int kArgThreads = 256;
 constexpr int kArgMaxParts = 256;
 constexpr size_t kAlign = 256;
 
@@ -67,35 +68,6 @@ __global__ __launch_bounds__(256) void eng_embed_dense_kernel(float* __restrict_
             v = table[(int64_t)id * n + i];
     }
     out[i] = v;
-}
-
-// (bv, bi) <- (v, i) if v is larger, or equal with a smaller index.  A NaN v
-// is never taken, and bv never becomes NaN.
-__device__ __forceinline__ void take(float& bv, int& bi, float v, int i) {
-    if (v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
-    }
-}
-
-// Workgroup-wide best (value, index) into thread 0.
-__device__ void block_best(float& bv, int& bi) {
-    __shared__ float sv[kArgThreads / kWave];
-    __shared__ int si[kArgThreads / kWave];
-#pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
-        take(bv, bi, ov, oi);
-    }
-    const int w = threadIdx.x / kWave;
-    if (threadIdx.x % kWave == 0) {
-        sv[w] = bv;
-        si[w] = bi;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0)
-        for (int k = 1; k < kArgThreads / kWave; ++k) take(bv, bi, sv[k], si[k]);
 }
 
 // Greedy argmax, part 1: each workgroup's best over a strided slice.
@@ -695,6 +667,8 @@ extern "C" int jinf_hip_engine_create_nvmw(jinf_hip_engine** out, const jinf_hip
 }
 
 extern "C" void jinf_hip_engine_destroy(jinf_hip_engine* e) { release(e); }
+
+const jinf_hip_engine_desc* jinf::engine_desc(const jinf_hip_engine* e) { return e ? &e->d : nullptr; }
 
 extern "C" int jinf_hip_engine_reset(jinf_hip_engine* e) {
     if (!e) return JINF_HIP_ERR_INVALID;

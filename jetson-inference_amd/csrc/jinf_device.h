@@ -238,4 +238,42 @@ __device__ __forceinline__ float block_max(float v, float* lds) {
     return m;
 }
 
+// Device-coherent (sc1) record store / load for the cross-workgroup merge.
+__device__ __forceinline__ void rec_store(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float rec_load(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One 16-byte direct-to-LDS load per lane: lane l's 16 bytes from gptr land
+// at LDS byte lds_base + 16 l (lds_base wave-uniform).  Issued from inline
+// assembly so that the compiler's wait-count tracking, which cannot tell
+// this wave's K and V regions apart, adds no wait for it; the kernel waits
+// for these loads itself (an uncounted load can only make the compiler's
+// own waits longer, never shorter).
+// M0 (the LDS destination register) is saved and restored around the load,
+// so the statement leaves every register the compiler knows about intact.
+__device__ __forceinline__ void lds_load16(const void* gptr, const void* lds_base) {
+    const uint32_t off = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_base;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(gptr), "s"(__builtin_amdgcn_readfirstlane(off))
+        : "memory");
+}
+
+// s_waitcnt immediate that waits until at most N vector-memory operations
+// are outstanding (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt and
+// lgkmcnt left at their maxima).
+template <int N>
+constexpr int waitcnt_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    return (N & 0xF) | ((N >> 4) << 14) | 0x0F70;
+}
+
 }  // namespace jinf

@@ -1,0 +1,897 @@
+// Batched dequant-GEMV on the matrix cores: the reference's per-token
+// matrix-vector products (cuda/matmul_kernels.cu:8-225, called per token at
+// src/engine.cpp:429-508) for up to 64 sequences decoded together, so that
+// every weight byte read from HBM serves all of them.
+//
+//   y[b, r] = sum_c W[r, c] x[b, c]        b < n_batch, W in Q4_0 / Q8_0 /
+//                                          Q4_K / Q6_K blocks along c
+//
+// Arithmetic.  The products run on v_mfma_f32_32x32x16_f16 (A = 32 tokens x
+// 16 columns, B = 16 columns x 32 weight rows, fp32 accumulate):
+//   - B holds the weights' integer codes, exact in fp16: q - 8 (Q4_0), q
+//     (Q8_0), sc * q <= 945 (Q4_K, the 6-bit sub-block scale folded in) and
+//     q - 32 (Q6_K); the block scales multiply the fp32 partial sums;
+//   - A holds x * s split into fp16 hi + lo (hi = fp16(v), lo = fp16(v - hi)),
+//     s a power of two per (token, 256-column slab) that puts the slab's
+//     largest |x| in [2^14, 2^15): about 22 significant bits, fp16's range
+//     never exceeded, and the 1/s applied exactly to the slab's fp32 sum;
+//   - Q4_K's minimum term dmin * m * sum(x) uses per-(token, sub-block) sums
+//     of the scaled x.
+// The result equals the fp32 dot product up to the fp32 rounding of the sums
+// (the order differs from the reference's sequential sum).
+//
+// Data movement.  A workgroup (4 waves) owns 64 weight rows (two 32-row
+// tiles) and a range of 256-column slabs.  Per slab every lane copies its
+// share of the 64 rows' bytes (the aligned 16-byte chunks covering each row's
+// slab: with a 16-byte aligned matrix they start inside it and end before the
+// next 16-byte boundary past its last byte) and of
+// x into LDS, converting x to the scaled hi / lo halves on the way; the next
+// slab's loads are issued before the current slab is multiplied, so they are
+// in flight during the matrix-core work.  Wave w multiplies columns
+// 64 w .. 64 w + 63 of the slab for both row tiles.  Within a 16-column
+// k-step, lane l supplies token / row l % 32 and columns 8 (l / 32) .. + 7 in
+// the order (0, 4, 1, 5, 2, 6, 3, 7), the order in which four bytes of
+// packed 4-bit codes unpack into fp16 pairs with two masks; A uses the same
+// order, so each fragment is one 16-byte LDS read.
+//
+// Split over the columns.  Small row counts give few workgroups, so the
+// slabs are split over k_splits workgroups per row group; each writes its
+// fp32 partial to the workspace with device-coherent stores and bumps the
+// group's counter, and the last one sums the partials in split order (the
+// result does not depend on which finished last), applies the epilogue and
+// resets the counter to zero.
+//
+// Epilogues (per output row r, token b): store; add into y (the residual
+// stream) and write the 64 rows' fp64 sum of squares per token, which the
+// next RMSNorm consumes; SiLU(gate) * up for a gate / up pair; RoPE at the
+// token's position and the K / V cache stores for fused q / k / v rows.
+// Prologue: RMSNorm of x from such sums of squares -- x * g is multiplied and
+// the 1 / rms factor, a per-token scalar, is applied to the final sum.
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include <type_traits>
+
+#include "jinf_device.h"
+#include "jinf_host.h"
+#include "jinf/kernels_ext.h"
+#include "quant_device.h"
+#include "rope_device.h"
+
+namespace jinf {
+namespace {
+
+typedef _Float16 mb_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mb_h2 __attribute__((ext_vector_type(2)));
+typedef float mb_f16 __attribute__((ext_vector_type(16)));
+
+constexpr int kMbThreads = 256;
+constexpr int kMbRows = 64;       // weight rows per workgroup: two 32-row tiles
+constexpr int kMbCols = 256;      // columns per slab
+constexpr int kMbMaxBatch = 64;
+constexpr int kMbTargetItems = 512;  // split the columns until this many workgroups
+
+enum MbEpi { kMbEpiStore = 0, kMbEpiAdd = 1, kMbEpiSwiGLU = 2, kMbEpiQKV = 3 };
+
+// Bytes of one row's 256-column slab.
+template <int QT> struct MbFmt;
+template <> struct MbFmt<kQ4_0> { static constexpr int SB = 144; };
+template <> struct MbFmt<kQ8_0> { static constexpr int SB = 272; };
+template <> struct MbFmt<kQ4_K> { static constexpr int SB = 144; };
+template <> struct MbFmt<kQ6_K> { static constexpr int SB = 210; };
+// 16-byte chunks that cover one row's slab: Q4_0, Q8_0 and Q4_K slabs
+// (144 / 272 / 144 bytes) start 16-byte aligned in a 16-byte aligned matrix;
+// a Q6_K slab (210 bytes) starts at an even offset, so 14 chunks cover it.
+template <int QT> constexpr int mb_nch() { return QT == kQ6_K ? 14 : MbFmt<QT>::SB / 16; }
+
+struct MbJob {
+    const uint8_t* W[3];   // segment matrices (same format and width)
+    int seg_end[3];        // virtual row where each segment ends
+    int64_t row_bytes;
+    int rows;              // virtual rows; kMbEpiSwiGLU: output rows
+    int n_slabs, n_groups, k_splits, slabs_per_split;
+    const float* x;        // [n_batch][ld_x]
+    int ld_x, n_batch;
+    const uint8_t* xrec;   // prepared x records [n_slabs][mb_rec(MT)]
+    float* y;              // [n_batch][ld_y]
+    int ld_y;
+    void* kc;              // kMbEpiQKV: caches [n_batch][ld_seq], rows [max_ctx][kv_dim]
+    void* vc;
+    const int32_t* pos;    // kMbEpiQKV: [n_batch] positions (outside [0, max_ctx): no store)
+    int kv_f16, kv_dim, head_dim, max_ctx;
+    int64_t ld_seq;
+    float* part;           // split partials [n_groups][k_splits][2 * MT * 1024]
+    uint32_t* counters;    // [n_groups]
+};
+
+struct MbNoTheta {};
+template <int EPI>
+using MbTheta = typename std::conditional<EPI == kMbEpiQKV, RopeTheta, MbNoTheta>::type;
+
+// Weight row `vr` of the virtual matrix (clamped to the last row).
+template <int EPI>
+__device__ __forceinline__ const uint8_t* mb_row(const MbJob& j, int group, int local) {
+    if constexpr (EPI == kMbEpiSwiGLU) {
+        // rows 0..31: gate rows 32 g .. ; rows 32..63: the same up rows
+        int r = group * 32 + (local & 31);
+        if (r >= j.rows) r = j.rows - 1;
+        return j.W[local >> 5] + (int64_t)r * j.row_bytes;
+    } else {
+        int v = group * kMbRows + local;
+        if (v >= j.rows) v = j.rows - 1;
+        const int s = v < j.seg_end[0] ? 0 : v < j.seg_end[1] ? 1 : 2;
+        const int start = s == 0 ? 0 : j.seg_end[s - 1];
+        return j.W[s] + (int64_t)(v - start) * j.row_bytes;
+    }
+}
+
+// Two 16-bit LDS reads (2-byte aligned) as one word.
+__device__ __forceinline__ uint32_t lds_u32(const uint8_t* p) {
+    const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
+    return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+}
+__device__ __forceinline__ uint32_t lds_u16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+
+__device__ __forceinline__ mb_h2 as_h2(uint32_t u) { return __builtin_bit_cast(mb_h2, u); }
+
+// Eight 4-bit codes (four bytes, element 2 i in the low nibble of byte i)
+// as fp16 (q + bias) in the order (0, 4, 1, 5, 2, 6, 3, 7); `hi2` adds two
+// high bits per element (Q6_K: the pair masks of element i and i + 4).
+__device__ __forceinline__ mb_h8 mb_nibbles(uint32_t w, uint32_t hi2, float bias) {
+    const mb_h2 b = mb_h2{(_Float16)(-1024.0f + bias), (_Float16)(-1024.0f + bias)};
+    mb_h2 p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t v = ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+        v |= ((hi2 >> (2 * i)) & 0x00030003u) << 4;
+        p[i] = as_h2(v) + b;  // (1024 + q) + (bias - 1024): exact
+    }
+    return mb_h8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
+}
+
+// Eight int8 codes (two words) as fp16 in the order (0, 4, 1, 5, 2, 6, 3, 7).
+__device__ __forceinline__ mb_h8 mb_int8(uint32_t w0, uint32_t w1) {
+    const mb_h2 b = mb_h2{(_Float16)-1152.0f, (_Float16)-1152.0f};
+    mb_h2 p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // byte i of w0 -> byte 0, byte i of w1 -> byte 2, zero elsewhere
+        const uint32_t sel = (uint32_t)i | 0x0C00u | ((uint32_t)(4 + i) << 16) | 0x0C000000u;
+        const uint32_t v = __builtin_amdgcn_perm(w1, w0, sel);
+        p[i] = as_h2((v ^ 0x00800080u) | 0x64006400u) + b;  // 1024 + (q + 128) - 1152
+    }
+    return mb_h8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
+}
+
+__device__ __forceinline__ mb_f16 mfma(mb_h8 a, mb_h8 b, mb_f16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Token of accumulator register r in lane half h of M-tile mt
+// (v_mfma_f32_32x32x* D layout: row 8 (r / 4) + 4 h + r % 4).
+__device__ __forceinline__ int mb_token(int mt, int r, int h) {
+    return 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
+}
+
+// ---- x preparation ----
+//
+// One record per 256-column slab, in the order the GEMV copies it into LDS:
+//   [MT M-tiles][16 k-steps][hi, lo][64 lanes] 16-byte fragments, lane
+//   (token % 32) + 32 h holding columns 16 t + 8 h .. + 7 in the order
+//   (0, 4, 1, 5, 2, 6, 3, 7);
+//   then the slab data: inv_s[32 MT] (1/s per token) and Q4_K's
+//   xs[8 sub-blocks][32 MT tokens] (sums of the scaled x over 32 columns).
+// Slab data after the fragments: inv_s[32 MT] floats, then xs[8][32 MT].
+__host__ __device__ constexpr int mb_meta(int mt) { return 2048 * mt; }
+__host__ __device__ constexpr int mb_rec(int mt) { return mt * 32768 + mb_meta(mt); }
+
+// grid (ceil(n_slabs / 4), 32 MT): each wave converts one slab of one token
+// (tokens >= n_batch get zeros, unit scale); with norm_w the row is first
+// RMS-normalised exactly as jinf_rmsnorm_rows does (x^ = fl32(fl32(x rs) g)).
+template <int MT>
+__global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict__ x, int ld_x,
+                                                          int n_batch, int cols,
+                                                          const void* __restrict__ norm_w,
+                                                          int norm_f16, float eps,
+                                                          uint8_t* __restrict__ rec) {
+    __shared__ double red[4];
+    const int b = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n_slabs = cols / kMbCols;
+    const bool live = b < n_batch;
+    const float* xr = x + (int64_t)(live ? b : 0) * ld_x;
+    float rs = 1.0f;
+    if (norm_w && live) {
+        double ss = 0.0;
+        for (int c = threadIdx.x; c < cols; c += 256) ss = fma((double)xr[c], (double)xr[c], ss);
+        ss = block_sum(ss, red);
+        rs = rms_scale(ss, cols, eps);
+    }
+    const int slab = blockIdx.x * 4 + wave;
+    if (slab >= n_slabs) return;
+    const int c0 = slab * kMbCols + 4 * lane;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) {
+        const float4 q = *reinterpret_cast<const float4*>(xr + c0);
+        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+        if (norm_w) {
+#pragma clang fp contract(off)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float g = norm_f16 ? h2f(static_cast<const uint16_t*>(norm_w)[c0 + i])
+                                         : static_cast<const float*>(norm_w)[c0 + i];
+                v[i] = (v[i] * rs) * g;
+            }
+        }
+    }
+    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    m = wave_max(m);
+    int e = 15;
+    if (m > 0.0f && m <= 3.4e38f) {
+        (void)frexpf(m, &e);  // m < 2^e
+        e = e < -100 ? -100 : e;
+    }
+    const float sc = ldexpf(1.0f, 15 - e);
+    uint8_t* r = rec + (int64_t)slab * mb_rec(MT);
+    // columns cs = 4 lane .. + 3 of the slab: k-step cs / 16, half (cs % 16) / 8,
+    // fragment slot of column e8 = cs % 8 in the order (0, 4, 1, 5, 2, 6, 3, 7)
+    const int cs = 4 * lane, t = cs >> 4, h = (cs >> 3) & 1;
+    const int lf = (b & 31) + 32 * h;
+    uint16_t* fh = reinterpret_cast<uint16_t*>(r + (((b >> 5) * 16 + t) * 2) * 1024 + lf * 16);
+    uint16_t* fl = fh + 512;  // lo half: 1024 bytes further
+    const int e0 = cs & 7;    // 0 or 4
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = v[i] * sc;
+        const _Float16 hh = (_Float16)a;
+        const _Float16 ll = (_Float16)(a - (float)hh);
+        const int slot = 2 * (e0 + i) - (e0 ? 7 : 0);  // 0,2,4,6 / 1,3,5,7
+        fh[slot] = __builtin_bit_cast(uint16_t, hh);
+        fl[slot] = __builtin_bit_cast(uint16_t, ll);
+        sum += a;
+    }
+    float* meta = reinterpret_cast<float*>(r + MT * 32768);
+    if (lane == 0) meta[b] = ldexpf(1.0f, e - 15);
+    // Q4_K sub-block sums: lanes 8 j .. 8 j + 7 hold sub-block j's 32 columns
+    sum += __shfl_xor(sum, 1, kWave);
+    sum += __shfl_xor(sum, 2, kWave);
+    sum += __shfl_xor(sum, 4, kWave);
+    if ((lane & 7) == 0) meta[32 * MT + (lane >> 3) * 32 * MT + b] = sum;
+}
+
+// ---- the GEMV ----
+//
+// Per 256-column slab a workgroup copies, with direct-to-LDS loads, its 64
+// weight rows' bytes (the aligned 16-byte chunks covering each row's slab)
+// and the slab's prepared x record into one of NBUF LDS slots; loads run
+// NBUF - 1 slabs ahead of the matrix-core work.
+// LDS slot: the weight chunks (NWI KiB), then the x record (NXI KiB).  The
+// slot is filled by 1 KiB direct-to-LDS instructions dealt round-robin to the
+// four waves.
+template <int QT> constexpr int mb_nwi() { return (kMbRows * mb_nch<QT>() * 16 + 1023) / 1024; }
+template <int MT> constexpr int mb_nxi() { return mb_rec(MT) / 1024; }
+template <int QT, int MT> constexpr int mb_slot() { return (mb_nwi<QT>() + mb_nxi<MT>()) * 1024; }
+constexpr int kMbLdsBudget = 160 * 1024 - 512;  // room for the kernel's static LDS
+template <int QT, int MT> constexpr int mb_nbuf() {
+    return 3 * mb_slot<QT, MT>() <= kMbLdsBudget ? 3 : 2 * mb_slot<QT, MT>() <= kMbLdsBudget ? 2 : 1;
+}
+template <int QT, int MT> constexpr int mb_lds_bytes() {
+    return mb_nbuf<QT, MT>() * mb_slot<QT, MT>() > 4 * 2 * MT * 4096
+               ? mb_nbuf<QT, MT>() * mb_slot<QT, MT>()
+               : 4 * 2 * MT * 4096;
+}
+// loads per lane per slab for wave w
+constexpr int mb_share(int n, int w) { return (n - w + 3) / 4; }
+
+template <int N>
+__device__ __forceinline__ void mb_wait_n(int after) {
+    // at most `after` slabs' loads (N per slab) still outstanding
+    if (after >= 2)
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm<(2 * N < 63 ? 2 * N : 63)>());
+    else if (after == 1)
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm<N>());
+    else
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
+}
+
+template <int NWI, int NXI>
+__device__ __forceinline__ void mb_wait_slabs(int wave, int after) {
+    constexpr int P0 = mb_share(NWI, 0) + mb_share(NXI, 0);
+    constexpr int P1 = mb_share(NWI, 1) + mb_share(NXI, 1);
+    constexpr int P2 = mb_share(NWI, 2) + mb_share(NXI, 2);
+    constexpr int P3 = mb_share(NWI, 3) + mb_share(NXI, 3);
+    switch (wave) {
+        case 0: mb_wait_n<P0>(after); break;
+        case 1: mb_wait_n<P1>(after); break;
+        case 2: mb_wait_n<P2>(after); break;
+        default: mb_wait_n<P3>(after); break;
+    }
+}
+
+template <int QT, int MT, int EPI>
+__global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbTheta<EPI> th) {
+    constexpr int NCH = mb_nch<QT>();
+    constexpr int SB = MbFmt<QT>::SB;
+    constexpr int NWI = mb_nwi<QT>();
+    constexpr int NXI = mb_nxi<MT>();
+    constexpr int WB = NWI * 1024;
+    constexpr int REC = mb_rec(MT);
+    constexpr int SLOT = mb_slot<QT, MT>();
+    constexpr int NBUF = mb_nbuf<QT, MT>();
+    constexpr int NWL = (NWI + 3) / 4;  // most weight loads of one lane per slab
+    static_assert(NBUF < 3 || 2 * (NWL + (NXI + 3) / 4) < 64, "vmcnt range");
+    extern __shared__ __attribute__((aligned(16))) uint8_t mb_lds[];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, h = lane >> 5, col = lane & 31;
+    const int group = blockIdx.x % j.n_groups;
+    const int split = blockIdx.x / j.n_groups;
+    const int s0 = split * j.slabs_per_split;
+    const int s1 = min(j.n_slabs, s0 + j.slabs_per_split);
+
+    // this lane's weight chunks: instruction wave + 4 k covers chunks
+    // 64 (wave + 4 k) + lane -> (row, chunk)
+    const uint8_t* wrow[NWL];
+    int wch[NWL];
+#pragma unroll
+    for (int k = 0; k < NWL; ++k) {
+        const int ci = (wave + 4 * k) * 64 + lane;
+        const int row = ci / NCH;
+        wch[k] = row < kMbRows ? ci % NCH : 0;
+        wrow[k] = mb_row<EPI>(j, group, row < kMbRows ? row : kMbRows - 1);
+    }
+    auto issue = [&](int s) {
+        uint8_t* slot = mb_lds + ((s - s0) % NBUF) * SLOT;
+#pragma unroll
+        for (int k = 0; k < NWL; ++k) {
+            const int ins = wave + 4 * k;
+            if (ins >= NWI) break;  // wave-uniform
+            const uintptr_t a = (uintptr_t)(wrow[k] + (int64_t)s * SB);
+            const uintptr_t a0 = a & ~(uintptr_t)15;
+            const int last = (int)((a + SB - 1 - a0) >> 4);  // last chunk of this row's slab
+            const int c = wch[k] < last ? wch[k] : last;
+            lds_load16(reinterpret_cast<const void*>(a0 + 16 * (uintptr_t)c), slot + ins * 1024);
+        }
+        const uint8_t* src = j.xrec + (int64_t)s * REC;
+#pragma unroll
+        for (int k = 0; k < (NXI + 3) / 4; ++k) {
+            const int ins = wave + 4 * k;
+            if (ins >= NXI) break;
+            lds_load16(src + ins * 1024 + 16 * lane, slot + WB + ins * 1024);
+        }
+    };
+
+    mb_f16 acc[2][MT];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[nt][mt][r] = 0.0f;
+
+    int issued = s0;
+    for (; issued < s1 && issued < s0 + NBUF - 1; ++issued) issue(issued);
+    for (int s = s0; s < s1; ++s) {
+        if (issued < s1) {
+            issue(issued);
+            ++issued;
+        }
+        mb_wait_slabs<NWI, NXI>(wave, issued - 1 - s);
+        __syncthreads();
+        const uint8_t* slot = mb_lds + ((s - s0) % NBUF) * SLOT;
+        const uint8_t* xa = slot + WB + lane * 16;
+        const float* meta = reinterpret_cast<const float*>(slot + WB + MT * 32768);
+
+        float invs[MT][16];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) invs[mt][r] = meta[mb_token(mt, r, h)];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const int row = nt * 32 + col;
+            const uintptr_t a = (uintptr_t)(mb_row<EPI>(j, group, row) + (int64_t)s * SB);
+            const uint8_t* rb = slot + row * NCH * 16 + (int)(a & 15);
+            mb_f16 sacc[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[mt][r] = 0.0f;
+
+            if constexpr (QT == kQ4_0 || QT == kQ8_0) {
+                constexpr int BB = QT == kQ4_0 ? 18 : 34;
+#pragma unroll
+                for (int bi = 0; bi < 2; ++bi) {
+                    const int blk = 2 * wave + bi;
+                    const uint8_t* bp = rb + BB * blk;
+                    const float d = h2f((uint16_t)lds_u16(bp));
+                    mb_f16 tmp[MT];
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) tmp[mt][r] = 0.0f;
+#pragma unroll
+                    for (int part = 0; part < 2; ++part) {
+                        const int t = 2 * blk + part;
+                        mb_h8 B;
+                        if constexpr (QT == kQ4_0) {
+                            B = mb_nibbles(lds_u32(bp + 2 + 8 * part + 4 * h), 0u, -8.0f);
+                        } else {
+                            const uint8_t* qp = bp + 2 + 16 * part + 8 * h;
+                            B = mb_int8(lds_u32(qp), lds_u32(qp + 4));
+                        }
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) {
+                            const uint8_t* xp = xa + (mt * 16 + t) * 2048;
+                            tmp[mt] = mfma(*reinterpret_cast<const mb_h8*>(xp), B, tmp[mt]);
+                            tmp[mt] = mfma(*reinterpret_cast<const mb_h8*>(xp + 1024), B, tmp[mt]);
+                        }
+                    }
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) sacc[mt][r] = fmaf(d, tmp[mt][r], sacc[mt][r]);
+                }
+            } else if constexpr (QT == kQ4_K) {
+                const float d = h2f((uint16_t)lds_u16(rb));
+                const float dmin = h2f((uint16_t)lds_u16(rb + 2));
+                uint32_t sw[3];
+#pragma unroll
+                for (int k = 0; k < 3; ++k) sw[k] = lds_u32(rb + 4 + 4 * k);
+                int sc[2], mn[2];
+                q4_K_scale_min(sw, 2 * wave, sc[0], mn[0]);
+                q4_K_scale_min(sw, 2 * wave + 1, sc[1], mn[1]);
+                mb_f16 tmp[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) tmp[mt][r] = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int t = 4 * wave + k;
+                    const _Float16 f = (_Float16)(float)sc[k >> 1];
+                    mb_h8 B = mb_nibbles(lds_u32(rb + 16 + 8 * t + 4 * h), 0u, 0.0f);
+                    B = B * mb_h8{f, f, f, f, f, f, f, f};  // sc * q <= 945: exact
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const uint8_t* xp = xa + (mt * 16 + t) * 2048;
+                        tmp[mt] = mfma(*reinterpret_cast<const mb_h8*>(xp), B, tmp[mt]);
+                        tmp[mt] = mfma(*reinterpret_cast<const mb_h8*>(xp + 1024), B, tmp[mt]);
+                    }
+                }
+                const float m0 = dmin * (float)mn[0], m1 = dmin * (float)mn[1];
+                const float* xs = meta + 32 * MT;
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int b = mb_token(mt, r, h);
+                        const float mins = m0 * xs[(2 * wave) * 32 * MT + b] +
+                                           m1 * xs[(2 * wave + 1) * 32 * MT + b];
+                        sacc[mt][r] = d * tmp[mt][r] - mins;
+                    }
+            } else {
+                static_assert(QT == kQ6_K, "format");
+                const float d = h2f((uint16_t)lds_u16(rb + 208));
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int t = 4 * wave + k;
+                    const float ds = d * (float)(int8_t)rb[192 + t];
+                    const uint32_t hq = lds_u16(rb + 128 + 4 * t + 2 * h);
+                    const uint32_t hs = (hq & 0xFFu) | ((hq & 0xFF00u) << 8);
+                    const mb_h8 B = mb_nibbles(lds_u32(rb + 8 * t + 4 * h), hs, -32.0f);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const uint8_t* xp = xa + (mt * 16 + t) * 2048;
+                        mb_f16 tmp = mfma(*reinterpret_cast<const mb_h8*>(xp), B, mb_f16{});
+                        tmp = mfma(*reinterpret_cast<const mb_h8*>(xp + 1024), B, tmp);
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) sacc[mt][r] = fmaf(ds, tmp[r], sacc[mt][r]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    acc[nt][mt][r] = fmaf(sacc[mt][r], invs[mt][r], acc[nt][mt][r]);
+        }
+        __syncthreads();  // the slot is refilled by a later issue
+    }
+
+    // ---- reduce the four waves (wave order) ----
+    float* red = reinterpret_cast<float*>(mb_lds);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                red[((wave * 2 + nt) * MT + mt) * 1024 + r * 64 + lane] = acc[nt][mt][r];
+    __syncthreads();
+    constexpr int NV = 2 * MT * 1024;   // values per workgroup
+    constexpr int PV = NV / kMbThreads;
+    float val[PV];
+#pragma unroll
+    for (int i = 0; i < PV; ++i) {
+        const int idx = tid + kMbThreads * i;
+        val[i] = ((red[idx] + red[NV + idx]) + red[2 * NV + idx]) + red[3 * NV + idx];
+    }
+    if (j.k_splits > 1) {
+        float* mine = j.part + ((int64_t)group * j.k_splits + split) * NV;
+#pragma unroll
+        for (int i = 0; i < PV; ++i) rec_store(mine + tid + kMbThreads * i, val[i]);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        __shared__ int last;
+        if (tid == 0) {
+            const uint32_t prev = __hip_atomic_fetch_add(j.counters + group, 1u, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+            last = prev == (uint32_t)(j.k_splits - 1);
+            if (last)
+                __hip_atomic_store(j.counters + group, 0u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last) return;
+        const float* all = j.part + (int64_t)group * j.k_splits * NV;
+#pragma unroll
+        for (int i = 0; i < PV; ++i) {
+            const int idx = tid + kMbThreads * i;
+            float v = rec_load(all + idx);
+            for (int sp = 1; sp < j.k_splits; ++sp) v += rec_load(all + (int64_t)sp * NV + idx);
+            val[i] = v;
+        }
+    }
+
+    // ---- epilogue ----
+    __syncthreads();  // the reduction area is free again
+    auto token_of = [](int idx) {
+        const int mt = (idx >> 10) % MT, r = (idx >> 6) & 15, ln = idx & 63;
+        return mb_token(mt, r, ln >> 5);
+    };
+    auto local_of = [](int idx) { return (idx / (MT * 1024)) * 32 + (idx & 31); };
+
+    if constexpr (EPI == kMbEpiStore || EPI == kMbEpiAdd) {
+#pragma unroll
+        for (int i = 0; i < PV; ++i) {
+            const int idx = tid + kMbThreads * i;
+            const int b = token_of(idx);
+            const int row = group * kMbRows + local_of(idx);
+            if (b < j.n_batch && row < j.rows) {
+                float* yp = j.y + (int64_t)b * j.ld_y + row;
+                if constexpr (EPI == kMbEpiAdd)
+                    *yp = *yp + val[i];
+                else
+                    *yp = val[i];
+            }
+        }
+    } else if constexpr (EPI == kMbEpiSwiGLU) {
+        // gate values idx < MT * 1024, up values at idx + MT * 1024 (same lane / register)
+        static_assert(PV % 2 == 0, "pairs");
+#pragma unroll
+        for (int i = 0; i < PV / 2; ++i) {
+            const int idx = tid + kMbThreads * i;
+            const int b = token_of(idx);
+            const int row = group * 32 + (idx & 31);
+            if (b < j.n_batch && row < j.rows)
+                j.y[(int64_t)b * j.ld_y + row] = swiglu_exact(val[i], val[i + PV / 2]);
+        }
+    } else {
+        // RoPE pairs: rows 2p, 2p + 1 are lanes 2p, 2p + 1 of one register;
+        // exchanged through LDS so that each thread holds both halves
+        float* pv = reinterpret_cast<float*>(mb_lds);
+#pragma unroll
+        for (int i = 0; i < PV; ++i) pv[tid + kMbThreads * i] = val[i];
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < PV / 2; ++i) {
+            const int idx = 2 * (tid + kMbThreads * i);  // even lane of the pair
+            const int b = token_of(idx);
+            const int v0 = group * kMbRows + local_of(idx);
+            if (b >= j.n_batch || v0 >= j.rows) continue;
+            float a = pv[idx], c = pv[idx + 1];
+            const int sgi = v0 < j.seg_end[0] ? 0 : v0 < j.seg_end[1] ? 1 : 2;
+            const int local = v0 - (sgi == 0 ? 0 : j.seg_end[sgi - 1]);
+            const int pos = j.pos[b];
+            if (sgi < 2) {
+                const float2 cs = rope_cs(pos, th.t[(local % j.head_dim) / 2]);
+                rot(a, c, cs.x, cs.y);
+            }
+            if (sgi == 0) {
+                float* yp = j.y + (int64_t)b * j.ld_y + local;
+                yp[0] = a;
+                yp[1] = c;
+            } else if (pos >= 0 && pos < j.max_ctx) {
+                const int64_t ci = (int64_t)b * j.ld_seq + (int64_t)pos * j.kv_dim + local;
+                void* cp = sgi == 1 ? j.kc : j.vc;
+                if (j.kv_f16) {
+                    uint16_t* p = static_cast<uint16_t*>(cp) + ci;
+                    p[0] = f2h(a);
+                    p[1] = f2h(c);
+                } else {
+                    float* p = static_cast<float*>(cp) + ci;
+                    p[0] = a;
+                    p[1] = c;
+                }
+            }
+        }
+    }
+}
+
+// ---- host side ----
+
+int mb_split(int n_groups, int n_slabs, int* slabs_per_split) {
+    int k = (kMbTargetItems + n_groups - 1) / n_groups;
+    if (k > n_slabs) k = n_slabs;
+    if (k < 1) k = 1;
+    const int per = (n_slabs + k - 1) / k;
+    *slabs_per_split = per;
+    return (n_slabs + per - 1) / per;
+}
+
+size_t mb_ctr_bytes(int n_groups) { return ((size_t)n_groups * 4 + 255) / 256 * 256; }
+
+// Workspace: the groups' counters, the x records, then the split partials.
+size_t mb_ws_bytes(int n_groups, int n_slabs, int mt) {
+    int per;
+    const int k = mb_split(n_groups, n_slabs, &per);
+    const size_t parts = k > 1 ? (size_t)n_groups * k * 2 * mt * 1024 * 4 : 0;
+    return mb_ctr_bytes(n_groups) + (size_t)n_slabs * mb_rec(mt) + parts;
+}
+
+template <int QT, int MT, int EPI>
+int mb_launch_t(MbJob& j, const MbTheta<EPI>& th, const void* norm_w, int norm_f16, float eps,
+                hipStream_t stream) {
+    const dim3 pgrid((unsigned)((j.n_slabs + 3) / 4), (unsigned)(32 * MT));
+    const int rc = launch(mb_prepare_kernel<MT>, pgrid, dim3(256), 0, stream, j.x, j.ld_x,
+                          j.n_batch, j.n_slabs * kMbCols, norm_w, norm_f16, eps,
+                          const_cast<uint8_t*>(j.xrec));
+    if (rc != JINF_HIP_OK) return rc;
+    const dim3 grid((unsigned)(j.n_groups * j.k_splits));
+    return launch(matvec_batch_kernel<QT, MT, EPI>, grid, dim3(kMbThreads),
+                  mb_lds_bytes<QT, MT>(), stream, j, th);
+}
+
+// Sequences 32 .. n_batch - 1 of a job as a job of their own.
+template <int EPI>
+MbJob mb_upper(const MbJob& j) {
+    MbJob u = j;
+    u.n_batch = j.n_batch - 32;
+    u.x = j.x + (int64_t)32 * j.ld_x;
+    u.y = j.y + (int64_t)32 * j.ld_y;
+    if constexpr (EPI == kMbEpiQKV) {
+        u.pos = j.pos + 32;
+        const int64_t es = j.kv_f16 ? 2 : 4;
+        if (j.kc) u.kc = static_cast<char*>(j.kc) + 32 * j.ld_seq * es;
+        if (j.vc) u.vc = static_cast<char*>(j.vc) + 32 * j.ld_seq * es;
+    }
+    return u;
+}
+
+// More than 32 sequences run as one launch over two M-tiles when the LDS
+// holds two slots of that size, else as two launches of at most 32.
+template <int QT, int EPI>
+int mb_dispatch_t(MbJob& j, const MbTheta<EPI>& th, const void* norm_w, int norm_f16, float eps,
+                  hipStream_t stream) {
+    if (j.n_batch <= 32) return mb_launch_t<QT, 1, EPI>(j, th, norm_w, norm_f16, eps, stream);
+    if constexpr (mb_nbuf<QT, 2>() >= 2) {
+        return mb_launch_t<QT, 2, EPI>(j, th, norm_w, norm_f16, eps, stream);
+    } else {
+        MbJob lo = j;
+        lo.n_batch = 32;
+        const int rc = mb_launch_t<QT, 1, EPI>(lo, th, norm_w, norm_f16, eps, stream);
+        if (rc != JINF_HIP_OK) return rc;
+        MbJob hi = mb_upper<EPI>(j);
+        return mb_launch_t<QT, 1, EPI>(hi, th, norm_w, norm_f16, eps, stream);
+    }
+}
+
+template <int EPI>
+int mb_dispatch(int qtype, MbJob& j, const MbTheta<EPI>& th, const void* norm_w, int norm_f16,
+                float eps, hipStream_t stream) {
+    switch (qtype) {
+        case kQ4_0: return mb_dispatch_t<kQ4_0, EPI>(j, th, norm_w, norm_f16, eps, stream);
+        case kQ8_0: return mb_dispatch_t<kQ8_0, EPI>(j, th, norm_w, norm_f16, eps, stream);
+        case kQ4_K: return mb_dispatch_t<kQ4_K, EPI>(j, th, norm_w, norm_f16, eps, stream);
+        case kQ6_K: return mb_dispatch_t<kQ6_K, EPI>(j, th, norm_w, norm_f16, eps, stream);
+        default: return JINF_HIP_ERR_INVALID;
+    }
+}
+
+int mb_row_bytes(int qtype, int cols, int64_t* rb) {
+    int e, b;
+    switch (qtype) {
+        case kQ4_0: e = 32; b = 18; break;
+        case kQ8_0: e = 32; b = 34; break;
+        case kQ4_K: e = 256; b = 144; break;
+        case kQ6_K: e = 256; b = 210; break;
+        default: return JINF_HIP_ERR_INVALID;
+    }
+    *rb = (int64_t)(cols / e) * b;
+    return JINF_HIP_OK;
+}
+
+// Shared checks and job set-up; `group_rows` output rows per workgroup.
+int mb_prepare(MbJob& j, int qtype, int rows, int cols, int n_batch, const float* x, int ld_x,
+               float* y, int ld_y, void* ws, size_t ws_bytes, int group_rows) {
+    if (rows <= 0 || cols <= 0 || n_batch <= 0 || n_batch > kMbMaxBatch || cols % kMbCols != 0)
+        return JINF_HIP_ERR_INVALID;
+    if (!x || !y || !aligned(x, 16) || ld_x % 4 != 0 || ld_x < cols || ld_y <= 0)
+        return JINF_HIP_ERR_INVALID;
+    if (mb_row_bytes(qtype, cols, &j.row_bytes) != JINF_HIP_OK) return JINF_HIP_ERR_INVALID;
+    j.rows = rows;
+    j.n_slabs = cols / kMbCols;
+    j.n_groups = (rows + group_rows - 1) / group_rows;
+    const int mt = n_batch > 32 ? 2 : 1;
+    if (!ws || !aligned(ws, 256) || ws_bytes < mb_ws_bytes(j.n_groups, j.n_slabs, mt)) {
+        JINF_LOG("batched GEMV: workspace missing, unaligned or smaller than "
+                 "jinf_matvec_batch_workspace_bytes()");
+        return JINF_HIP_ERR_INVALID;
+    }
+    j.k_splits = mb_split(j.n_groups, j.n_slabs, &j.slabs_per_split);
+    char* w = static_cast<char*>(ws);
+    j.counters = reinterpret_cast<uint32_t*>(w);
+    j.xrec = reinterpret_cast<uint8_t*>(w + mb_ctr_bytes(j.n_groups));
+    j.part = reinterpret_cast<float*>(w + mb_ctr_bytes(j.n_groups) +
+                                      (size_t)j.n_slabs * mb_rec(mt));
+    j.x = x;
+    j.ld_x = ld_x;
+    j.n_batch = n_batch;
+    j.y = y;
+    j.ld_y = ld_y;
+    return JINF_HIP_OK;
+}
+
+int mb_norm_type(const void* norm_w, int norm_type, float eps, int* f16) {
+    if (!norm_w) {
+        *f16 = 0;
+        return JINF_HIP_OK;
+    }
+    if ((norm_type != JINF_HIP_F32 && norm_type != JINF_HIP_F16) || !(eps >= 0.0f))
+        return JINF_HIP_ERR_INVALID;
+    *f16 = norm_type == JINF_HIP_F16;
+    return JINF_HIP_OK;
+}
+
+bool w_ok(const void* w) { return w && aligned(w, 16); }
+
+}  // namespace
+
+size_t matvec_batch_ws_bytes(int rows, int cols, int n_batch, int group_rows) {
+    if (rows <= 0 || cols <= 0 || cols % kMbCols != 0 || n_batch <= 0 || n_batch > kMbMaxBatch)
+        return 0;
+    const int groups = (rows + group_rows - 1) / group_rows;
+    return mb_ws_bytes(groups, cols / kMbCols, n_batch > 32 ? 2 : 1);
+}
+
+}  // namespace jinf
+
+using namespace jinf;
+
+extern "C" size_t jinf_matvec_batch_workspace_bytes(int rows, int cols, int n_batch) {
+    // the SwiGLU variant groups 32 output rows per workgroup
+    const size_t a = matvec_batch_ws_bytes(rows, cols, n_batch, kMbRows);
+    const size_t b = matvec_batch_ws_bytes(rows, cols, n_batch, 32);
+    return a > b ? a : b;
+}
+
+extern "C" int jinf_matvec_batch(const void* weight, int qtype, const float* x, int ld_x, float* y,
+                                 int ld_y, int rows, int cols, int n_batch, void* workspace,
+                                 size_t workspace_bytes, hipStream_t stream) {
+    MbJob j{};
+    if (!w_ok(weight)) return JINF_HIP_ERR_INVALID;
+    const int rc = mb_prepare(j, qtype, rows, cols, n_batch, x, ld_x, y, ld_y, workspace,
+                              workspace_bytes, kMbRows);
+    if (rc != JINF_HIP_OK) return rc;
+    if (ld_y < rows) return JINF_HIP_ERR_INVALID;
+    j.W[0] = j.W[1] = j.W[2] = static_cast<const uint8_t*>(weight);
+    j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = rows;
+    return mb_dispatch<kMbEpiStore>(qtype, j, MbNoTheta{}, nullptr, 0, 0.0f, stream);
+}
+
+extern "C" int jinf_matvec_batch_add(const void* weight, int qtype, const float* x, int ld_x,
+                                     float* y, int ld_y, int rows, int cols, int n_batch,
+                                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    MbJob j{};
+    if (!w_ok(weight)) return JINF_HIP_ERR_INVALID;
+    const int rc = mb_prepare(j, qtype, rows, cols, n_batch, x, ld_x, y, ld_y, workspace,
+                              workspace_bytes, kMbRows);
+    if (rc != JINF_HIP_OK) return rc;
+    if (ld_y < rows) return JINF_HIP_ERR_INVALID;
+    j.W[0] = j.W[1] = j.W[2] = static_cast<const uint8_t*>(weight);
+    j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = rows;
+    return mb_dispatch<kMbEpiAdd>(qtype, j, MbNoTheta{}, nullptr, 0, 0.0f, stream);
+}
+
+extern "C" int jinf_rmsnorm_matvec_batch(const void* weight, int qtype, const float* h, int ld_h,
+                                         const void* norm_w, int norm_type, float eps, float* y,
+                                         int ld_y, int rows, int cols, int n_batch,
+                                         void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream) {
+    MbJob j{};
+    int f16 = 0;
+    if (!w_ok(weight)) return JINF_HIP_ERR_INVALID;
+    int rc = mb_prepare(j, qtype, rows, cols, n_batch, h, ld_h, y, ld_y, workspace,
+                        workspace_bytes, kMbRows);
+    if (rc == JINF_HIP_OK) rc = mb_norm_type(norm_w, norm_type, eps, &f16);
+    if (rc != JINF_HIP_OK) return rc;
+    if (ld_y < rows) return JINF_HIP_ERR_INVALID;
+    j.W[0] = j.W[1] = j.W[2] = static_cast<const uint8_t*>(weight);
+    j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = rows;
+    return mb_dispatch<kMbEpiStore>(qtype, j, MbNoTheta{}, norm_w, f16, eps, stream);
+}
+
+extern "C" int jinf_rmsnorm_swiglu_matvec_batch(const void* w_gate, const void* w_up, int qtype,
+                                                const float* h, int ld_h, const void* norm_w,
+                                                int norm_type, float eps, float* y, int ld_y,
+                                                int n_ff, int cols, int n_batch, void* workspace,
+                                                size_t workspace_bytes, hipStream_t stream) {
+    MbJob j{};
+    int f16 = 0;
+    if (!w_ok(w_gate) || !w_ok(w_up)) return JINF_HIP_ERR_INVALID;
+    int rc = mb_prepare(j, qtype, n_ff, cols, n_batch, h, ld_h, y, ld_y, workspace,
+                        workspace_bytes, 32);
+    if (rc == JINF_HIP_OK) rc = mb_norm_type(norm_w, norm_type, eps, &f16);
+    if (rc != JINF_HIP_OK) return rc;
+    if (ld_y < n_ff) return JINF_HIP_ERR_INVALID;
+    j.W[0] = static_cast<const uint8_t*>(w_gate);
+    j.W[1] = static_cast<const uint8_t*>(w_up);
+    j.W[2] = j.W[0];
+    j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = n_ff;
+    return mb_dispatch<kMbEpiSwiGLU>(qtype, j, MbNoTheta{}, norm_w, f16, eps, stream);
+}
+
+extern "C" int jinf_rmsnorm_qkv_rope_batch(const void* wq, const void* wk, const void* wv,
+                                           int qtype, const float* h, int ld_h,
+                                           const void* norm_w, int norm_type, float eps,
+                                           int n_embd, float* q, int ld_q, void* k_cache,
+                                           void* v_cache, int kv_type, int64_t ld_seq,
+                                           const int32_t* positions, int max_ctx, int head_dim,
+                                           int n_heads, int n_heads_kv, float freq_base,
+                                           int n_batch, void* workspace, size_t workspace_bytes,
+                                           hipStream_t stream) {
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim / 2 > kRopeMaxHalf || n_heads < 0 ||
+        n_heads_kv < 0 || !(freq_base > 0.0f) || !positions)
+        return JINF_HIP_ERR_INVALID;
+    const int qd = wq ? n_heads * head_dim : 0;
+    const int kvd = n_heads_kv * head_dim;
+    const int rows = qd + (wk ? kvd : 0) + (wv ? kvd : 0);
+    if (rows == 0) return JINF_HIP_OK;
+    if ((wq && !w_ok(wq)) || (wk && !w_ok(wk)) || (wv && !w_ok(wv))) return JINF_HIP_ERR_INVALID;
+    if ((wk && !k_cache) || (wv && !v_cache) || (wq && (!q || ld_q < qd)))
+        return JINF_HIP_ERR_INVALID;
+    if (kv_type != JINF_HIP_F32 && kv_type != JINF_HIP_F16) return JINF_HIP_ERR_INVALID;
+    if ((wk || wv) && (max_ctx <= 0 || ld_seq < (int64_t)max_ctx * kvd)) return JINF_HIP_ERR_INVALID;
+    MbJob j{};
+    int f16 = 0;
+    float* yq = q ? q : const_cast<float*>(h);
+    int rc = mb_prepare(j, qtype, rows, n_embd, n_batch, h, ld_h, yq, wq ? ld_q : 1, workspace,
+                        workspace_bytes, kMbRows);
+    if (rc == JINF_HIP_OK) rc = mb_norm_type(norm_w, norm_type, eps, &f16);
+    if (rc != JINF_HIP_OK) return rc;
+    // segments in q, k, v order; absent matrices take no rows
+    const uint8_t* Ws[3] = {static_cast<const uint8_t*>(wq), static_cast<const uint8_t*>(wk),
+                            static_cast<const uint8_t*>(wv)};
+    const int len[3] = {qd, wk ? kvd : 0, wv ? kvd : 0};
+    int end = 0;
+    for (int s = 0; s < 3; ++s) {
+        end += len[s];
+        j.seg_end[s] = end;
+        j.W[s] = Ws[s] ? Ws[s] : (Ws[0] ? Ws[0] : Ws[1] ? Ws[1] : Ws[2]);
+    }
+    j.kc = k_cache;
+    j.vc = v_cache;
+    j.pos = positions;
+    j.kv_f16 = kv_type == JINF_HIP_F16;
+    j.kv_dim = kvd;
+    j.head_dim = head_dim;
+    j.max_ctx = max_ctx;
+    j.ld_seq = ld_seq;
+    RopeTheta th;
+    theta_table(th, head_dim, freq_base);
+    return mb_dispatch<kMbEpiQKV>(qtype, j, th, norm_w, f16, eps, stream);
+}

@@ -26,17 +26,23 @@ from .ops import (  # noqa: F401
     embed_q4_0,
     matvec,
     matvec_add,
+    matvec_batch,
+    matvec_batch_add,
+    matvec_batch_workspace,
     matvec_q4_0,
     residual_add,
     residual_rmsnorm_rows,
     rmsnorm_matvec,
+    rmsnorm_matvec_batch,
     rmsnorm_qkv_rope,
+    rmsnorm_qkv_rope_batch,
     rmsnorm_rows,
     rmsnorm_swiglu_matvec,
+    rmsnorm_swiglu_matvec_batch,
     rope_rows,
     softmax_rows,
     swiglu,
 )
 from . import gguf  # noqa: F401,E402
 from . import nvmw  # noqa: F401,E402
-from .engine import Engine, EngineError  # noqa: F401,E402
+from .engine import Batch, Engine, EngineError  # noqa: F401,E402

@@ -61,6 +61,18 @@ SIGNATURES = {
     "jinf_rmsnorm_swiglu_matvec": (_I, [_P, _P, _I, _P, _P, _I, _F, _P, _I, _I, _P]),
     "jinf_rmsnorm_qkv_rope": (_I, [_P, _P, _P, _I, _P, _P, _I, _F, _I, _P, _P, _P, _I, _P, _I,
                                    _I, _I, _I, _F, _P]),
+    # batched GEMVs on the matrix cores
+    "jinf_matvec_batch_workspace_bytes": (ctypes.c_size_t, [_I, _I, _I]),
+    "jinf_matvec_batch": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P]),
+    "jinf_matvec_batch_add": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P, ctypes.c_size_t,
+                                   _P]),
+    "jinf_rmsnorm_matvec_batch": (_I, [_P, _I, _P, _I, _P, _I, _F, _P, _I, _I, _I, _I, _P,
+                                       ctypes.c_size_t, _P]),
+    "jinf_rmsnorm_swiglu_matvec_batch": (_I, [_P, _P, _I, _P, _I, _P, _I, _F, _P, _I, _I, _I,
+                                              _I, _P, ctypes.c_size_t, _P]),
+    "jinf_rmsnorm_qkv_rope_batch": (_I, [_P, _P, _P, _I, _P, _I, _P, _I, _F, _I, _P, _I, _P,
+                                         _P, _I, ctypes.c_int64, _P, _I, _I, _I, _I, _F, _I,
+                                         _P, ctypes.c_size_t, _P]),
     # GGUF files (include/jinf/gguf_hip.h)
     "jinf_hip_gguf_load": (_I, [ctypes.POINTER(_P), ctypes.c_char_p]),
     "jinf_hip_gguf_free": (None, [_P]),
@@ -107,6 +119,15 @@ SIGNATURES = {
     "jinf_hip_engine_copy_logits": (_I, [_P, _P, _I]),
     "jinf_hip_engine_use_graph": (_I, [_P, _I]),
     "jinf_hip_engine_step_weight_bytes": (ctypes.c_uint64, [_P]),
+    # batched decode (include/jinf/engine_hip.h)
+    "jinf_hip_batch_create": (_I, [ctypes.POINTER(_P), _P, _I, _I, _I]),
+    "jinf_hip_batch_destroy": (None, [_P]),
+    "jinf_hip_batch_reset": (_I, [_P, _I]),
+    "jinf_hip_batch_n_past": (_I, [_P, _I]),
+    "jinf_hip_batch_forward": (_I, [_P, _P, ctypes.POINTER(_P)]),
+    "jinf_hip_batch_generate": (_I, [_P, _P, _I]),
+    "jinf_hip_batch_copy_logits": (_I, [_P, _P]),
+    "jinf_hip_batch_use_graph": (_I, [_P, _I]),
 }
 
 _lib = None

@@ -177,5 +177,71 @@ class Engine:
         return [int(x) for x in out[:n.value]]
 
 
-__all__ = ["Engine", "EngineError", "EngineDesc", "LayerWeights", "LAYER_TENSORS", "EOS", "F16",
+class Batch:
+    """A jinf_hip_batch: n_seq sequences decoded together on an Engine's
+    weights (keep the Engine alive while the batch exists)."""
+
+    def __init__(self, engine, n_seq, max_context, kv_type=F16):
+        h = ctypes.c_void_p()
+        _check("jinf_hip_batch_create",
+               lib().jinf_hip_batch_create(ctypes.byref(h), engine._h, int(n_seq),
+                                           int(max_context), int(kv_type)))
+        self._h = h
+        self._engine = engine
+        self.n_seq = int(n_seq)
+        self.n_vocab = engine.n_vocab
+        self.max_context = int(max_context)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().jinf_hip_batch_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self, seq=-1):
+        _check("jinf_hip_batch_reset", lib().jinf_hip_batch_reset(self._h, int(seq)))
+
+    def n_past(self, seq):
+        return lib().jinf_hip_batch_n_past(self._h, int(seq))
+
+    def use_graph(self, on=True):
+        _check("jinf_hip_batch_use_graph", lib().jinf_hip_batch_use_graph(self._h, int(bool(on))))
+
+    def forward(self, tokens):
+        """One step: tokens[s] (-1 = idle) for every sequence."""
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(-1))
+        if t.size != self.n_seq:
+            raise ValueError("one token per sequence")
+        p = ctypes.c_void_p()
+        _check("jinf_hip_batch_forward",
+               lib().jinf_hip_batch_forward(self._h, t.ctypes.data, ctypes.byref(p)))
+        return p.value
+
+    def logits(self):
+        """The last step's logits, fp32 [n_seq, n_vocab] (host copy)."""
+        out = np.empty((self.n_seq, self.n_vocab), np.float32)
+        _check("jinf_hip_batch_copy_logits",
+               lib().jinf_hip_batch_copy_logits(self._h, out.ctypes.data))
+        return out
+
+    def generate(self, steps):
+        """Greedy steps: int32 [steps, n_seq] emitted tokens (-1 after a stop)."""
+        out = np.zeros((max(1, int(steps)), self.n_seq), np.int32)
+        _check("jinf_hip_batch_generate",
+               lib().jinf_hip_batch_generate(self._h, out.ctypes.data, int(steps)))
+        return out[:int(steps)]
+
+
+__all__ = ["Engine", "EngineError", "Batch", "EngineDesc", "LayerWeights", "LAYER_TENSORS", "EOS", "F16",
            "F32"]

@@ -245,6 +245,108 @@ def rmsnorm_qkv_rope(w_q, w_k, w_v, h, qtype, pos, k_cache, v_cache, head_dim, n
     return q_out
 
 
+def matvec_batch_workspace(rows, cols, n_batch, device="cuda"):
+    """A zero-filled workspace tensor for the batched GEMVs (prepared x, and
+    the split partials and counters; counters must start at zero, calls
+    leave them so)."""
+    nbytes = lib().jinf_matvec_batch_workspace_bytes(rows, cols, n_batch)
+    return torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+
+
+def _ws(workspace, rows, cols, n_batch, device):
+    if workspace is None:
+        workspace = matvec_batch_workspace(rows, cols, n_batch, device)
+    return _ptr(workspace), workspace.numel()
+
+
+def _mb_rows(weight, qtype, x):
+    if x.dim() != 2 or x.dtype != torch.float32:
+        raise JinfError("x must be fp32 [n_batch, cols]")
+    return _mv_shape(weight, qtype, x.shape[1])
+
+
+def matvec_batch(weight, x, qtype, y=None, workspace=None):
+    """y[b] = W x[b] on the matrix cores; x fp32 [n_batch, cols]."""
+    rows = _mb_rows(weight, qtype, x)
+    n_batch, cols = x.shape
+    y = torch.empty((n_batch, rows), dtype=torch.float32, device=x.device) if y is None else y
+    wp, wn = _ws(workspace, rows, cols, n_batch, x.device)
+    _check(lib().jinf_matvec_batch(_ptr(weight), int(qtype), _ptr(x), x.stride(0), _ptr(y),
+                                   y.stride(0), rows, cols, n_batch, wp, wn, _stream()),
+           "jinf_matvec_batch")
+    return y
+
+
+def matvec_batch_add(weight, x, qtype, y, workspace=None):
+    """y[b] += W x[b] in place."""
+    rows = _mb_rows(weight, qtype, x)
+    n_batch, cols = x.shape
+    wp, wn = _ws(workspace, rows, cols, n_batch, x.device)
+    _check(lib().jinf_matvec_batch_add(_ptr(weight), int(qtype), _ptr(x), x.stride(0), _ptr(y),
+                                       y.stride(0), rows, cols, n_batch, wp, wn, _stream()),
+           "jinf_matvec_batch_add")
+    return y
+
+
+def rmsnorm_matvec_batch(weight, h, qtype, norm_w, eps=1e-5, y=None, workspace=None):
+    """y[b] = W (rmsnorm(h[b]) * g)."""
+    rows = _mb_rows(weight, qtype, h)
+    n_batch, cols = h.shape
+    y = torch.empty((n_batch, rows), dtype=torch.float32, device=h.device) if y is None else y
+    nw, nt = _norm_args(norm_w)
+    wp, wn = _ws(workspace, rows, cols, n_batch, h.device)
+    _check(lib().jinf_rmsnorm_matvec_batch(_ptr(weight), int(qtype), _ptr(h), h.stride(0), nw,
+                                           nt, float(eps), _ptr(y), y.stride(0), rows, cols,
+                                           n_batch, wp, wn, _stream()),
+           "jinf_rmsnorm_matvec_batch")
+    return y
+
+
+def rmsnorm_swiglu_matvec_batch(w_gate, w_up, h, qtype, norm_w, eps=1e-5, out=None,
+                                workspace=None):
+    """out[b] = silu(W_gate x^[b]) * (W_up x^[b])."""
+    n_ff = _mb_rows(w_gate, qtype, h)
+    if tuple(w_up.shape) != tuple(w_gate.shape):
+        raise JinfError("gate and up shapes differ")
+    n_batch, cols = h.shape
+    out = torch.empty((n_batch, n_ff), dtype=torch.float32, device=h.device) if out is None else out
+    nw, nt = _norm_args(norm_w)
+    wp, wn = _ws(workspace, n_ff, cols, n_batch, h.device)
+    _check(lib().jinf_rmsnorm_swiglu_matvec_batch(_ptr(w_gate), _ptr(w_up), int(qtype), _ptr(h),
+                                                  h.stride(0), nw, nt, float(eps), _ptr(out),
+                                                  out.stride(0), n_ff, cols, n_batch, wp, wn,
+                                                  _stream()),
+           "jinf_rmsnorm_swiglu_matvec_batch")
+    return out
+
+
+def rmsnorm_qkv_rope_batch(w_q, w_k, w_v, h, qtype, norm_w, positions, k_cache, v_cache,
+                           head_dim, n_heads, n_heads_kv, freq_base, eps=1e-5, q_out=None,
+                           workspace=None):
+    """Per sequence b: q[b] = rope(W_q x^[b]) (returned); rope(W_k x^[b]) and
+    W_v x^[b] stored at positions[b] of k_cache / v_cache [n_batch, max_ctx,
+    n_heads_kv * head_dim] (fp32 or fp16)."""
+    n_batch, cols = h.shape
+    rows = 0
+    for w in (w_q, w_k, w_v):
+        if w is not None:
+            rows += _mv_shape(w, qtype, cols)
+    if w_q is not None and q_out is None:
+        q_out = torch.empty((n_batch, n_heads * head_dim), dtype=torch.float32, device=h.device)
+    cache = k_cache if k_cache is not None else v_cache
+    kv_type = _act(cache) if cache is not None else F32
+    max_ctx = cache.shape[1] if cache is not None else 0
+    ld_seq = cache.stride(0) if cache is not None else 0
+    nw, nt = _norm_args(norm_w)
+    wp, wn = _ws(workspace, max(rows, 1), cols, n_batch, h.device)
+    _check(lib().jinf_rmsnorm_qkv_rope_batch(
+        _ptr(w_q), _ptr(w_k), _ptr(w_v), int(qtype), _ptr(h), h.stride(0), nw, nt, float(eps),
+        cols, _ptr(q_out), q_out.stride(0) if q_out is not None else 0, _ptr(k_cache),
+        _ptr(v_cache), kv_type, ld_seq, _ptr(positions), max_ctx, head_dim, n_heads, n_heads_kv,
+        float(freq_base), n_batch, wp, wn, _stream()), "jinf_rmsnorm_qkv_rope_batch")
+    return q_out
+
+
 def dequant_rows(table, qtype, n_embd, ids=None, out_dtype=torch.float32, out=None):
     """Gather + dequantize rows of a qtype table (uint8 [n_vocab, row bytes])."""
     n_vocab = table.shape[0]

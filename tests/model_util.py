@@ -161,3 +161,30 @@ def write_nvmw(path, hp, W, cold_layers=(), bundled=False, primary_type=None, or
                               for j in range(n_ff)])
         bundles = (size, n_ff, per_layer)
     return nw.write(path, hp, tensors, primary_type=primary_type, bundles=bundles)
+
+
+def pass_through_model(n_vocab=64, n_embd=256):
+    """Every layer matrix zero (the residual stream keeps the embedding), an
+    output norm keeping only element 0, and an output matrix whose row 2 reads
+    element 0: token 2 (end of sequence) wins for every input."""
+    hp = dict(n_layers=2, n_embd=n_embd, n_heads=4, n_heads_kv=2, n_ff=256, n_vocab=n_vocab,
+              rope_freq_base=10000.0, rms_norm_eps=1e-5)
+    kvd = 2 * (n_embd // 4)
+    zeros = lambda r, c: (np.zeros((r, c // 32 * 18), np.uint8), Q4_0)  # noqa: E731
+    W = {"token_embd.weight": (np.abs(np.random.default_rng(1).normal(size=(n_vocab, n_embd)))
+                               .astype(np.float32) + 0.1, F32)}
+    shapes = {"attn_q": (n_embd, n_embd), "attn_k": (kvd, n_embd), "attn_v": (kvd, n_embd),
+              "attn_output": (n_embd, n_embd), "ffn_gate": (256, n_embd),
+              "ffn_up": (256, n_embd), "ffn_down": (n_embd, 256)}
+    for L in range(2):
+        for n in LAYER_TENSORS:
+            W[f"blk.{L}.{n}.weight"] = ((np.ones(n_embd, np.float32), F32) if n.endswith("norm")
+                                        else zeros(*shapes[n]))
+    g = np.zeros(n_embd, np.float32)
+    g[0] = 1.0
+    W["output_norm.weight"] = (g, F32)
+    out = np.zeros((n_vocab, n_embd // 32, 34), np.uint8)
+    out[2, 0, 0:2] = np.array([1.0], np.float16).view(np.uint8)
+    out[2, 0, 2] = 1
+    W["output.weight"] = (out.reshape(n_vocab, -1), Q8_0)
+    return hp, W
