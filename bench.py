@@ -347,6 +347,12 @@ ENGINE_MODELS = {
                                              ffn_gate=12, ffn_up=12, ffn_down=14),
                                     embd=12, out=14,
                                     desc="Q4_K weights, Q6_K for attn_v, ffn_down and output"),
+    # the same Q4_0 model decoding 32 sequences at once (jinf_hip_batch_*)
+    "llama3-8b-decode-batch": dict(mat=dict.fromkeys(("attn_q", "attn_k", "attn_v",
+                                                      "attn_output", "ffn_gate", "ffn_up",
+                                                      "ffn_down"), 2),
+                                   embd=2, out=14, batch=32,
+                                   desc="Q4_0 weights, Q6_K output"),
 }
 LLAMA3_8B = dict(n_layers=32, n_embd=4096, n_heads=32, n_heads_kv=8, n_ff=14336,
                  n_vocab=128256, rope_freq_base=500000.0, rms_norm_eps=1e-5)
@@ -395,8 +401,106 @@ def engine_cpu_baseline(W, hp, spec, threads, budget_s):
     return med, len(times)
 
 
+def batch_bench(args, torch, jinf_amd, spec):
+    """n_seq sequences decoded together: prompt through forward, then
+    `steps` greedy steps through jinf_hip_batch_generate (tokens fed back on
+    the device, one synchronization at the end)."""
+    hp = dict(LLAMA3_8B)
+    n_seq = args.batch or spec["batch"]
+    max_ctx = 1024
+    g = torch.Generator(device="cuda")
+    g.manual_seed(args.seed)
+    W = engine_weights(torch, g, spec, hp)
+    torch.cuda.synchronize()
+    from jinf_amd.engine import Batch, Engine
+
+    e = Engine(hp, W, 16, jinf_amd.F16)
+    b = Batch(e, n_seq, max_ctx, jinf_amd.F16)
+    b.use_graph(not args.no_graph)
+    wbytes = e.step_weight_bytes - weight_row_bytes(spec["embd"], hp["n_embd"])
+    wbytes += n_seq * weight_row_bytes(spec["embd"], hp["n_embd"])  # one embedding row each
+    kvd = hp["n_heads_kv"] * hp["n_embd"] // hp["n_heads"]
+    log(f"batch of {n_seq} ready: {wbytes / 1e9:.3f} GB of weights read per step")
+    t0 = time.perf_counter()
+    for tok in PROMPT:
+        b.forward([tok] * n_seq)
+    prefill_s = time.perf_counter() - t0
+    b.generate(max(1, args.warmup))
+    start_pos = b.n_past(0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = b.generate(args.steps)
+    dec_s = time.perf_counter() - t0
+    emitted = int((out >= 0).sum())
+    ms_step = dec_s / args.steps * 1e3
+    mean_ctx = start_pos + (args.steps + 1) / 2
+    kv_bytes = n_seq * 2 * hp["n_layers"] * kvd * 2 * mean_ctx  # fp16 K and V rows read
+    step_bytes = wbytes + kv_bytes
+    gbs = step_bytes / (ms_step * 1e-3) / 1e9
+    tok_s = emitted / dec_s
+    log(f"{args.steps} steps x {n_seq} sequences: {ms_step:.3f} ms per step, "
+        f"{tok_s:.0f} tokens/s")
+    b.close()
+    e.close()
+    cpu = None
+    if args.cpu_seconds > 0:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        try:
+            med, runs = engine_cpu_baseline(W, hp, spec, threads, args.cpu_seconds)
+            cpu = {"value": round(1.0 / med, 4), "unit": "tokens/s", "cores": threads,
+                   "kind": "port", "runs": runs,
+                   "sample": f"oracle decode loop (oracle/engine.py, C kernels -O3, {threads} "
+                             f"OpenMP threads), one sequence on a host copy of the same weights: "
+                             f"median of {runs} tokens, {args.cpu_seconds:.0f} s budget (the "
+                             f"reference decodes one sequence at a time)",
+                   "cpu_model": cpu_model()}
+        except Exception as exc:  # the baseline is reported, never required
+            log(f"cpu baseline failed: {exc!r}")
+    out_line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 math (fp16 x fp16 products on the matrix cores), " + spec["desc"] +
+                 ", f16 KV cache",
+        "data": "synthetic: random Llama-3-8B-shaped weights (seeded torch RNG on device), "
+                "the reference prompt for every sequence, then greedy tokens",
+        "config": {"workload": args.workload,
+                   "shapes": "Llama-3-8B: 32 layers, hidden 4096, 32/8 heads x 128, FFN 14336, "
+                             f"vocab 128256, {n_seq} sequences decoded together",
+                   "storage": spec["desc"] + f", f16 KV cache (max_context {max_ctx} per sequence)",
+                   "step": "one token for every sequence through every layer, captured HIP "
+                           "graph replayed per step (jinf_hip_batch_generate)",
+                   "tokens_per_s": round(tok_s, 1),
+                   "prefill_6_steps_ms": round(prefill_s * 1e3, 3),
+                   "weight_bytes_per_step": wbytes,
+                   "kv_bytes_per_step_mean": int(kv_bytes),
+                   "context": [start_pos, start_pos + args.steps],
+                   "note": "SURVEY 8(f) f4, the engine forward loop with a batched-decode KV cache"},
+        "frac_of_peak": round(gbs / PEAK_GBS, 4),
+        "launch": "eager stream" if args.no_graph else "HIP graph per step",
+        "wall_s_timed": round(dec_s, 4),
+        "roofline": {"bound": "hbm", "kernel": "decode step (every kernel of one batched step)",
+                     "achieved": round(gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_GBS, 4), "bytes_per_launch": int(step_bytes),
+                     "avg_launch_us": round(ms_step * 1e3, 3),
+                     "traffic": traffic_from_profiles("decode_step", args.workload)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out_line), flush=True)
+
+
+def weight_row_bytes(qtype, n):
+    elems, nbytes = {2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}[qtype]
+    return n // elems * nbytes
+
+
 def engine_bench(args, torch, jinf_amd):
     spec = ENGINE_MODELS[args.workload]
+    if "batch" in spec:
+        return batch_bench(args, torch, jinf_amd, spec)
     hp = dict(LLAMA3_8B)
     max_ctx = 8192
     g = torch.Generator(device="cuda")
@@ -692,6 +796,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="llama3-8b-layer")
+    ap.add_argument("--batch", type=int, default=0,
+                    help="sequences of llama3-8b-decode-batch (default 32, at most 64)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bounded CPU-baseline sample (0 = skip)")

@@ -158,8 +158,11 @@ struct jinf_hip_batch {
     int32_t* h_io = nullptr;  // pinned: n_seq tokens, then 16 words
     std::vector<int> h_pos;   // host copy of the positions
     hipStream_t stream = nullptr;
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
+    // captured steps, one per attention bound (a power of two >= 64, at most
+    // max_ctx): the bound sets the attention's launch geometry and covers
+    // every length the step can see
+    std::vector<std::pair<int, hipGraphExec_t>> graphs;
+    int bound = 0;
     bool use_graph = true;
 };
 
@@ -217,7 +220,7 @@ int bat_enqueue_step(jinf_hip_batch* b) {
         BAT_TRY(bat_qkv(b, w, kc, vc));
         BAT_TRY(jinf_attention_decode(b->attn, b->q_dim, b->q, b->q_dim, kc, vc, b->kv_type,
                                       b->kv_dim, (int64_t)b->max_ctx * b->kv_dim, b->lens, ns,
-                                      b->max_ctx, b->head_dim, d.n_heads, d.n_heads_kv, 0.0f,
+                                      b->bound, b->head_dim, d.n_heads, d.n_heads_kv, 0.0f,
                                       b->aws, b->aws_bytes, s));
         BAT_TRY(jinf_matvec_batch_add(w.attn_output, w.attn_output_type, b->attn, b->q_dim,
                                       b->hidden, n, n, b->q_dim, ns, b->mws, b->mws_bytes, s));
@@ -247,7 +250,7 @@ int bat_enqueue_step(jinf_hip_batch* b) {
                   b->part_v, b->part_i, b->arg_parts, b->st, b->acts, b->pos, b->cur);
 }
 
-int bat_capture(jinf_hip_batch* b) {
+int bat_capture(jinf_hip_batch* b, hipGraphExec_t* out) {
     BAT_TRY(hip_rc(hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal),
                    "hipStreamBeginCapture"));
     const int rc = bat_enqueue_step(b);
@@ -259,26 +262,38 @@ int bat_capture(jinf_hip_batch* b) {
     }
     hipGraphExec_t x = nullptr;
     const int ic = hip_rc(hipGraphInstantiate(&x, g, nullptr, nullptr, 0), "hipGraphInstantiate");
-    if (ic != JINF_HIP_OK) {
-        (void)hipGraphDestroy(g);
-        return ic;
-    }
-    b->graph = g;
-    b->exec = x;
+    (void)hipGraphDestroy(g);
+    if (ic != JINF_HIP_OK) return ic;
+    *out = x;
     return JINF_HIP_OK;
+}
+
+int bat_bound(const jinf_hip_batch* b, int len) {
+    int v = 64;
+    while (v < len) v *= 2;
+    return v < b->max_ctx ? v : b->max_ctx;
+}
+
+int bat_max_pos(const jinf_hip_batch* b) {
+    int m = 0;
+    for (int p : b->h_pos) m = p > m ? p : m;
+    return m;
 }
 
 int bat_step(jinf_hip_batch* b) {
     if (!b->use_graph) return bat_enqueue_step(b);
-    if (!b->exec) BAT_TRY(bat_capture(b));
-    return hip_rc(hipGraphLaunch(b->exec, b->stream), "hipGraphLaunch");
+    for (const auto& g : b->graphs)
+        if (g.first == b->bound) return hip_rc(hipGraphLaunch(g.second, b->stream), "hipGraphLaunch");
+    hipGraphExec_t x = nullptr;
+    BAT_TRY(bat_capture(b, &x));
+    b->graphs.emplace_back(b->bound, x);
+    return hip_rc(hipGraphLaunch(x, b->stream), "hipGraphLaunch");
 }
 
 void bat_release(jinf_hip_batch* b) {
     if (!b) return;
     if (b->stream) (void)hipStreamSynchronize(b->stream);
-    if (b->exec) (void)hipGraphExecDestroy(b->exec);
-    if (b->graph) (void)hipGraphDestroy(b->graph);
+    for (const auto& g : b->graphs) (void)hipGraphExecDestroy(g.second);
     if (b->h_io) (void)hipHostFree(b->h_io);
     if (b->kv) (void)hipFree(b->kv);
     if (b->act) (void)hipFree(b->act);
@@ -450,6 +465,7 @@ extern "C" int jinf_hip_batch_forward(jinf_hip_batch* b, const int32_t* tokens,
                                   b->stream),
                    "hipMemcpyAsync"));
     BAT_TRY(bat_set_mode(b, 0));
+    b->bound = bat_bound(b, bat_max_pos(b) + 1);
     const int rc = bat_step(b);
     const int sc = hip_rc(hipStreamSynchronize(b->stream), "hipStreamSynchronize");
     if (rc != JINF_HIP_OK) return rc;
@@ -467,13 +483,20 @@ extern "C" int jinf_hip_batch_generate(jinf_hip_batch* b, int32_t* output, int s
     for (int done = 0; done < steps && rc == JINF_HIP_OK;) {
         const int n = steps - done < b->hist_rows ? steps - done : b->hist_rows;
         rc = bat_set_mode(b, 1);
+        b->bound = bat_bound(b, bat_max_pos(b) + n);
         for (int k = 0; k < n && rc == JINF_HIP_OK; ++k) rc = bat_step(b);
         if (rc == JINF_HIP_OK)
             rc = hip_rc(hipMemcpyAsync(output + (size_t)done * b->n_seq, b->hist,
                                        (size_t)n * b->n_seq * 4, hipMemcpyDefault, b->stream),
                         "hipMemcpyAsync");
         if (rc == JINF_HIP_OK)
+            rc = hip_rc(hipMemcpyAsync(b->h_io, b->pos, (size_t)b->n_seq * 4,
+                                       hipMemcpyDeviceToHost, b->stream),
+                        "hipMemcpyAsync");
+        if (rc == JINF_HIP_OK)
             rc = hip_rc(hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+        if (rc == JINF_HIP_OK)
+            for (int s = 0; s < b->n_seq; ++s) b->h_pos[s] = b->h_io[s];
         done += n;
     }
     // refresh the host positions

@@ -156,8 +156,11 @@ struct jinf_hip_engine {
     size_t ws_bytes = 0;
     int32_t* h_tokens = nullptr;  // pinned staging: max_ctx token ids, then one word
     hipStream_t stream = nullptr;
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
+    // captured token steps, one per attention bound (a power of two >= 64,
+    // at most max_context): the bound sets the attention's launch geometry
+    // and must cover every length the step can see
+    std::vector<std::pair<int, hipGraphExec_t>> graphs;
+    int bound = 0;
     bool use_graph = true;
 };
 
@@ -238,7 +241,7 @@ int enqueue_step(jinf_hip_engine* e) {
         // attention over n_past + 1 positions (:455-459)
         ENG_TRY(jinf_attention_decode(e->attn, qd, e->q, qd, kc, vc, d.kv_type, kvd,
                                       (int64_t)d.max_context * kvd, e->state + kLen, 1,
-                                      d.max_context, hd, d.n_heads, d.n_heads_kv, 0.0f, e->ws,
+                                      e->bound, hd, d.n_heads, d.n_heads_kv, 0.0f, e->ws,
                                       e->ws_bytes, s));
         // output projection + residual add (:461-466)
         ENG_TRY(jinf_matvec_add(w.attn_output, w.attn_output_type, e->attn, e->hidden, n, qd, s));
@@ -268,7 +271,7 @@ int enqueue_step(jinf_hip_engine* e) {
                   e->part_v, e->part_i, e->arg_parts, e->state, e->tokens, d.max_context);
 }
 
-int capture(jinf_hip_engine* e) {
+int capture(jinf_hip_engine* e, hipGraphExec_t* out) {
     ENG_TRY(hip_ok(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal),
                    "hipStreamBeginCapture"));
     const int rc = enqueue_step(e);
@@ -280,20 +283,29 @@ int capture(jinf_hip_engine* e) {
     }
     hipGraphExec_t x = nullptr;
     const int ic = hip_ok(hipGraphInstantiate(&x, g, nullptr, nullptr, 0), "hipGraphInstantiate");
-    if (ic != JINF_HIP_OK) {
-        (void)hipGraphDestroy(g);
-        return ic;
-    }
-    e->graph = g;
-    e->exec = x;
+    (void)hipGraphDestroy(g);
+    if (ic != JINF_HIP_OK) return ic;
+    *out = x;
     return JINF_HIP_OK;
 }
 
-// One token step on the engine's stream (the captured graph, or the launches).
+// The attention bound for steps whose lengths reach at most `len`.
+int bound_for(int len, int max_ctx) {
+    int b = 64;
+    while (b < len) b *= 2;
+    return b < max_ctx ? b : max_ctx;
+}
+
+// One token step on the engine's stream (the captured graph for the current
+// bound, or the launches).
 int step(jinf_hip_engine* e) {
     if (!e->use_graph) return enqueue_step(e);
-    if (!e->exec) ENG_TRY(capture(e));
-    return hip_ok(hipGraphLaunch(e->exec, e->stream), "hipGraphLaunch");
+    for (const auto& g : e->graphs)
+        if (g.first == e->bound) return hip_ok(hipGraphLaunch(g.second, e->stream), "hipGraphLaunch");
+    hipGraphExec_t x = nullptr;
+    ENG_TRY(capture(e, &x));
+    e->graphs.emplace_back(e->bound, x);
+    return hip_ok(hipGraphLaunch(x, e->stream), "hipGraphLaunch");
 }
 
 int check_matrix(const void* p, int t, int rows, int cols, const char* what, int L) {
@@ -362,8 +374,7 @@ int validate(const jinf_hip_engine_desc* d) {
 void release(jinf_hip_engine* e) {
     if (!e) return;
     if (e->stream) (void)hipStreamSynchronize(e->stream);
-    if (e->exec) (void)hipGraphExecDestroy(e->exec);
-    if (e->graph) (void)hipGraphDestroy(e->graph);
+    for (const auto& g : e->graphs) (void)hipGraphExecDestroy(g.second);
     if (e->h_tokens) (void)hipHostFree(e->h_tokens);
     if (e->kv) (void)hipFree(e->kv);
     if (e->act) (void)hipFree(e->act);
@@ -709,6 +720,7 @@ extern "C" int jinf_hip_engine_forward(jinf_hip_engine* e, const int32_t* tokens
     ENG_TRY(hip_ok(hipMemcpyAsync(e->state + kFillEnd, fill_end, 4, hipMemcpyHostToDevice,
                                   e->stream),
                    "hipMemcpyAsync"));
+    e->bound = bound_for(e->n_past + n_tokens, d.max_context);
     int rc = JINF_HIP_OK;
     for (int t = 0; t < n_tokens && rc == JINF_HIP_OK; ++t) {
         rc = step(e);
@@ -733,6 +745,7 @@ extern "C" int jinf_hip_engine_generate(jinf_hip_engine* e, const int32_t* promp
     }
     int32_t* best = e->h_tokens + e->d.max_context + 1;
     int generated = 0;
+    e->bound = bound_for(e->n_past + (max_tokens > 0 ? max_tokens : 0), e->d.max_context);
     for (int i = 0; i < max_tokens; ++i) {
         // the argmax of the last step (already the token at position n_past)
         ENG_TRY(hip_ok(hipMemcpyAsync(best, e->state + kBest, 4, hipMemcpyDeviceToHost,

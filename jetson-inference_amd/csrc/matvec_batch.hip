@@ -275,8 +275,13 @@ template <int QT> constexpr int mb_nwi() { return (kMbRows * mb_nch<QT>() * 16 +
 template <int MT> constexpr int mb_nxi() { return mb_rec(MT) / 1024; }
 template <int QT, int MT> constexpr int mb_slot() { return (mb_nwi<QT>() + mb_nxi<MT>()) * 1024; }
 constexpr int kMbLdsBudget = 160 * 1024 - 512;  // room for the kernel's static LDS
+#ifndef MB_NBUF_MAX
+#define MB_NBUF_MAX 1
+#endif
 template <int QT, int MT> constexpr int mb_nbuf() {
-    return 3 * mb_slot<QT, MT>() <= kMbLdsBudget ? 3 : 2 * mb_slot<QT, MT>() <= kMbLdsBudget ? 2 : 1;
+    return MB_NBUF_MAX >= 3 && 3 * mb_slot<QT, MT>() <= kMbLdsBudget   ? 3
+           : MB_NBUF_MAX >= 2 && 2 * mb_slot<QT, MT>() <= kMbLdsBudget ? 2
+                                                                        : 1;
 }
 template <int QT, int MT> constexpr int mb_lds_bytes() {
     return mb_nbuf<QT, MT>() * mb_slot<QT, MT>() > 4 * 2 * MT * 4096
@@ -390,115 +395,156 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) invs[mt][r] = meta[mb_token(mt, r, h)];
+        // both 32-row tiles advance together: their matrix-core chains are
+        // independent, and each x fragment is read once per k-step
+        const uint8_t* rb[2];
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
             const int row = nt * 32 + col;
             const uintptr_t a = (uintptr_t)(mb_row<EPI>(j, group, row) + (int64_t)s * SB);
-            const uint8_t* rb = slot + row * NCH * 16 + (int)(a & 15);
-            mb_f16 sacc[MT];
+            rb[nt] = slot + row * NCH * 16 + (int)(a & 15);
+        }
+        mb_f16 sacc[2][MT];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[mt][r] = 0.0f;
+                for (int r = 0; r < 16; ++r) sacc[nt][mt][r] = 0.0f;
+        // k-steps t: tmp[nt][mt] += A(t) B[nt](t) for the hi and lo halves of A
+        auto mfma_step = [&](int t, const mb_h8 (&B)[2], mb_f16 (&tmp)[2][MT]) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const uint8_t* xp = xa + (mt * 16 + t) * 2048;
+                const mb_h8 ah = *reinterpret_cast<const mb_h8*>(xp);
+                const mb_h8 al = *reinterpret_cast<const mb_h8*>(xp + 1024);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) tmp[nt][mt] = mfma(ah, B[nt], tmp[nt][mt]);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) tmp[nt][mt] = mfma(al, B[nt], tmp[nt][mt]);
+            }
+        };
+        auto zero = [](mb_f16 (&tmp)[2][MT]) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) tmp[nt][mt][r] = 0.0f;
+        };
 
-            if constexpr (QT == kQ4_0 || QT == kQ8_0) {
-                constexpr int BB = QT == kQ4_0 ? 18 : 34;
+        if constexpr (QT == kQ4_0 || QT == kQ8_0) {
+            constexpr int BB = QT == kQ4_0 ? 18 : 34;
 #pragma unroll
-                for (int bi = 0; bi < 2; ++bi) {
-                    const int blk = 2 * wave + bi;
-                    const uint8_t* bp = rb + BB * blk;
-                    const float d = h2f((uint16_t)lds_u16(bp));
-                    mb_f16 tmp[MT];
+            for (int bi = 0; bi < 2; ++bi) {
+                const int blk = 2 * wave + bi;
+                float d[2];
+                mb_f16 tmp[2][MT];
+                zero(tmp);
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt)
+                for (int part = 0; part < 2; ++part) {
+                    mb_h8 B[2];
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) tmp[mt][r] = 0.0f;
-#pragma unroll
-                    for (int part = 0; part < 2; ++part) {
-                        const int t = 2 * blk + part;
-                        mb_h8 B;
+                    for (int nt = 0; nt < 2; ++nt) {
+                        const uint8_t* bp = rb[nt] + BB * blk;
+                        if (part == 0) d[nt] = h2f((uint16_t)lds_u16(bp));
                         if constexpr (QT == kQ4_0) {
-                            B = mb_nibbles(lds_u32(bp + 2 + 8 * part + 4 * h), 0u, -8.0f);
+                            B[nt] = mb_nibbles(lds_u32(bp + 2 + 8 * part + 4 * h), 0u, -8.0f);
                         } else {
                             const uint8_t* qp = bp + 2 + 16 * part + 8 * h;
-                            B = mb_int8(lds_u32(qp), lds_u32(qp + 4));
-                        }
-#pragma unroll
-                        for (int mt = 0; mt < MT; ++mt) {
-                            const uint8_t* xp = xa + (mt * 16 + t) * 2048;
-                            tmp[mt] = mfma(*reinterpret_cast<const mb_h8*>(xp), B, tmp[mt]);
-                            tmp[mt] = mfma(*reinterpret_cast<const mb_h8*>(xp + 1024), B, tmp[mt]);
+                            B[nt] = mb_int8(lds_u32(qp), lds_u32(qp + 4));
                         }
                     }
+                    mfma_step(2 * blk + part, B, tmp);
+                }
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) sacc[mt][r] = fmaf(d, tmp[mt][r], sacc[mt][r]);
-                }
-            } else if constexpr (QT == kQ4_K) {
-                const float d = h2f((uint16_t)lds_u16(rb));
-                const float dmin = h2f((uint16_t)lds_u16(rb + 2));
+                        for (int r = 0; r < 16; ++r)
+                            sacc[nt][mt][r] = fmaf(d[nt], tmp[nt][mt][r], sacc[nt][mt][r]);
+            }
+        } else if constexpr (QT == kQ4_K) {
+            float d[2], m0[2], m1[2];
+            _Float16 f[2][2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                d[nt] = h2f((uint16_t)lds_u16(rb[nt]));
+                const float dmin = h2f((uint16_t)lds_u16(rb[nt] + 2));
                 uint32_t sw[3];
 #pragma unroll
-                for (int k = 0; k < 3; ++k) sw[k] = lds_u32(rb + 4 + 4 * k);
-                int sc[2], mn[2];
-                q4_K_scale_min(sw, 2 * wave, sc[0], mn[0]);
-                q4_K_scale_min(sw, 2 * wave + 1, sc[1], mn[1]);
-                mb_f16 tmp[MT];
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) tmp[mt][r] = 0.0f;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const int t = 4 * wave + k;
-                    const _Float16 f = (_Float16)(float)sc[k >> 1];
-                    mb_h8 B = mb_nibbles(lds_u32(rb + 16 + 8 * t + 4 * h), 0u, 0.0f);
-                    B = B * mb_h8{f, f, f, f, f, f, f, f};  // sc * q <= 945: exact
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        const uint8_t* xp = xa + (mt * 16 + t) * 2048;
-                        tmp[mt] = mfma(*reinterpret_cast<const mb_h8*>(xp), B, tmp[mt]);
-                        tmp[mt] = mfma(*reinterpret_cast<const mb_h8*>(xp + 1024), B, tmp[mt]);
-                    }
-                }
-                const float m0 = dmin * (float)mn[0], m1 = dmin * (float)mn[1];
-                const float* xs = meta + 32 * MT;
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int b = mb_token(mt, r, h);
-                        const float mins = m0 * xs[(2 * wave) * 32 * MT + b] +
-                                           m1 * xs[(2 * wave + 1) * 32 * MT + b];
-                        sacc[mt][r] = d * tmp[mt][r] - mins;
-                    }
-            } else {
-                static_assert(QT == kQ6_K, "format");
-                const float d = h2f((uint16_t)lds_u16(rb + 208));
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const int t = 4 * wave + k;
-                    const float ds = d * (float)(int8_t)rb[192 + t];
-                    const uint32_t hq = lds_u16(rb + 128 + 4 * t + 2 * h);
-                    const uint32_t hs = (hq & 0xFFu) | ((hq & 0xFF00u) << 8);
-                    const mb_h8 B = mb_nibbles(lds_u32(rb + 8 * t + 4 * h), hs, -32.0f);
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        const uint8_t* xp = xa + (mt * 16 + t) * 2048;
-                        mb_f16 tmp = mfma(*reinterpret_cast<const mb_h8*>(xp), B, mb_f16{});
-                        tmp = mfma(*reinterpret_cast<const mb_h8*>(xp + 1024), B, tmp);
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) sacc[mt][r] = fmaf(ds, tmp[r], sacc[mt][r]);
-                    }
-                }
+                for (int k = 0; k < 3; ++k) sw[k] = lds_u32(rb[nt] + 4 + 4 * k);
+                int sc0, mn0, sc1, mn1;
+                q4_K_scale_min(sw, 2 * wave, sc0, mn0);
+                q4_K_scale_min(sw, 2 * wave + 1, sc1, mn1);
+                f[nt][0] = (_Float16)(float)sc0;
+                f[nt][1] = (_Float16)(float)sc1;
+                m0[nt] = dmin * (float)mn0;
+                m1[nt] = dmin * (float)mn1;
             }
+            mb_f16 tmp[2][MT];
+            zero(tmp);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int t = 4 * wave + k;
+                mb_h8 B[2];
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    const _Float16 g = f[nt][k >> 1];
+                    B[nt] = mb_nibbles(lds_u32(rb[nt] + 16 + 8 * t + 4 * h), 0u, 0.0f) *
+                            mb_h8{g, g, g, g, g, g, g, g};  // sc * q <= 945: exact
+                }
+                mfma_step(t, B, tmp);
+            }
+            const float* xs = meta + 32 * MT;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int b = mb_token(mt, r, h);
+                    const float xa0 = xs[(2 * wave) * 32 * MT + b];
+                    const float xa1 = xs[(2 * wave + 1) * 32 * MT + b];
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt)
+                        sacc[nt][mt][r] = d[nt] * tmp[nt][mt][r] - (m0[nt] * xa0 + m1[nt] * xa1);
+                }
+        } else {
+            static_assert(QT == kQ6_K, "format");
+            float d[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) d[nt] = h2f((uint16_t)lds_u16(rb[nt] + 208));
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int t = 4 * wave + k;
+                mb_h8 B[2];
+                float ds[2];
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    ds[nt] = d[nt] * (float)(int8_t)rb[nt][192 + t];
+                    const uint32_t hq = lds_u16(rb[nt] + 128 + 4 * t + 2 * h);
+                    const uint32_t hs = (hq & 0xFFu) | ((hq & 0xFF00u) << 8);
+                    B[nt] = mb_nibbles(lds_u32(rb[nt] + 8 * t + 4 * h), hs, -32.0f);
+                }
+                mb_f16 tmp[2][MT];
+                zero(tmp);
+                mfma_step(t, B, tmp);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            sacc[nt][mt][r] = fmaf(ds[nt], tmp[nt][mt][r], sacc[nt][mt][r]);
+            }
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    acc[nt][mt][r] = fmaf(sacc[mt][r], invs[mt][r], acc[nt][mt][r]);
-        }
+                    acc[nt][mt][r] = fmaf(sacc[nt][mt][r], invs[mt][r], acc[nt][mt][r]);
         __syncthreads();  // the slot is refilled by a later issue
     }
 
