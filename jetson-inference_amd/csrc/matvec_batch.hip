@@ -64,12 +64,14 @@ namespace {
 typedef _Float16 mb_h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 mb_h2 __attribute__((ext_vector_type(2)));
 typedef float mb_f16 __attribute__((ext_vector_type(16)));
+typedef float mb_f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kMbThreads = 256;
-constexpr int kMbRows = 64;       // weight rows per workgroup: two 32-row tiles
+// Cache policy of the split partials' buffer accesses: sc1, device-coherent
+// across the XCDs' L2s (as agent-scope atomics are).
+constexpr int kMbSc1 = 16;
+
 constexpr int kMbCols = 256;      // columns per slab
 constexpr int kMbMaxBatch = 64;
-constexpr int kMbTargetItems = 512;  // split the columns until this many workgroups
 
 enum MbEpi { kMbEpiStore = 0, kMbEpiAdd = 1, kMbEpiSwiGLU = 2, kMbEpiQKV = 3 };
 
@@ -108,16 +110,18 @@ struct MbNoTheta {};
 template <int EPI>
 using MbTheta = typename std::conditional<EPI == kMbEpiQKV, RopeTheta, MbNoTheta>::type;
 
-// Weight row `vr` of the virtual matrix (clamped to the last row).
-template <int EPI>
+// Weight row `local` of workgroup `group` (ROWS rows per workgroup), clamped
+// to the last row.  kMbEpiSwiGLU: the first ROWS / 2 are gate rows, the next
+// ROWS / 2 the same rows of the up matrix.
+template <int EPI, int ROWS>
 __device__ __forceinline__ const uint8_t* mb_row(const MbJob& j, int group, int local) {
     if constexpr (EPI == kMbEpiSwiGLU) {
-        // rows 0..31: gate rows 32 g .. ; rows 32..63: the same up rows
-        int r = group * 32 + (local & 31);
+        constexpr int HALF = ROWS / 2;
+        int r = group * HALF + local % HALF;
         if (r >= j.rows) r = j.rows - 1;
-        return j.W[local >> 5] + (int64_t)r * j.row_bytes;
+        return j.W[local / HALF] + (int64_t)r * j.row_bytes;
     } else {
-        int v = group * kMbRows + local;
+        int v = group * ROWS + local;
         if (v >= j.rows) v = j.rows - 1;
         const int s = v < j.seg_end[0] ? 0 : v < j.seg_end[1] ? 1 : 2;
         const int start = s == 0 ? 0 : j.seg_end[s - 1];
@@ -268,91 +272,98 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
 // weight rows' bytes (the aligned 16-byte chunks covering each row's slab)
 // and the slab's prepared x record into one of NBUF LDS slots; loads run
 // NBUF - 1 slabs ahead of the matrix-core work.
-// LDS slot: the weight chunks (NWI KiB), then the x record (NXI KiB).  The
-// slot is filled by 1 KiB direct-to-LDS instructions dealt round-robin to the
-// four waves.
-template <int QT> constexpr int mb_nwi() { return (kMbRows * mb_nch<QT>() * 16 + 1023) / 1024; }
+// Workgroup shapes: NT 32-row tiles (ROWS = 32 NT weight rows) and WV waves;
+// the 16 k-steps of a slab are split into KSW parts, wave w taking k-part
+// w / (WV / KSW) of TPW = NT KSW / WV tiles.
+//   narrow: NT 2, WV 4, KSW 4 -- 64 rows, each wave both tiles over 4 k-steps
+//           (few rows: many workgroups, one LDS slot, three per CU);
+//   wide:   NT 8 (Q4_0, Q4_K) or 4 (Q8_0, Q6_K), WV 8 -- 256 / 128 rows that
+//           share each x record, two LDS slots so that the next slab's
+//           weights are in flight during the matrix-core work.
+// LDS slot: the weight chunks (NWI KiB), then the x record (NXI KiB), filled
+// by 1 KiB direct-to-LDS instructions dealt round-robin to the waves.
+template <int QT, int NT> constexpr int mb_nwi() { return (32 * NT * mb_nch<QT>() * 16 + 1023) / 1024; }
 template <int MT> constexpr int mb_nxi() { return mb_rec(MT) / 1024; }
-template <int QT, int MT> constexpr int mb_slot() { return (mb_nwi<QT>() + mb_nxi<MT>()) * 1024; }
+template <int QT, int MT, int NT> constexpr int mb_slot() {
+    return (mb_nwi<QT, NT>() + mb_nxi<MT>()) * 1024;
+}
 constexpr int kMbLdsBudget = 160 * 1024 - 512;  // room for the kernel's static LDS
-#ifndef MB_NBUF_MAX
-#define MB_NBUF_MAX 1
-#endif
-template <int QT, int MT> constexpr int mb_nbuf() {
-    return MB_NBUF_MAX >= 3 && 3 * mb_slot<QT, MT>() <= kMbLdsBudget   ? 3
-           : MB_NBUF_MAX >= 2 && 2 * mb_slot<QT, MT>() <= kMbLdsBudget ? 2
-                                                                        : 1;
+template <int QT, int MT, int NT, int WV> constexpr int mb_nbuf() {
+    return WV == 4 ? 1 : 2 * mb_slot<QT, MT, NT>() <= kMbLdsBudget ? 2 : 1;
 }
-template <int QT, int MT> constexpr int mb_lds_bytes() {
-    return mb_nbuf<QT, MT>() * mb_slot<QT, MT>() > 4 * 2 * MT * 4096
-               ? mb_nbuf<QT, MT>() * mb_slot<QT, MT>()
-               : 4 * 2 * MT * 4096;
+template <int QT, int MT, int NT, int WV> constexpr int mb_lds_bytes() {
+    return mb_nbuf<QT, MT, NT, WV>() * mb_slot<QT, MT, NT>() > (8 * MT * 4096)
+               ? mb_nbuf<QT, MT, NT, WV>() * mb_slot<QT, MT, NT>()
+               : (8 * MT * 4096);
 }
-// loads per lane per slab for wave w
-constexpr int mb_share(int n, int w) { return (n - w + 3) / 4; }
+// loads per lane per slab for wave w of WV
+constexpr int mb_share(int n, int w, int wv) { return (n - w + wv - 1) / wv; }
 
 template <int N>
 __device__ __forceinline__ void mb_wait_n(int after) {
     // at most `after` slabs' loads (N per slab) still outstanding
-    if (after >= 2)
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm<(2 * N < 63 ? 2 * N : 63)>());
-    else if (after == 1)
+    if (after >= 1)
         __builtin_amdgcn_s_waitcnt(waitcnt_vm<N>());
     else
         __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
 }
 
-template <int NWI, int NXI>
+template <int NWI, int NXI, int WV, int W = 0>
 __device__ __forceinline__ void mb_wait_slabs(int wave, int after) {
-    constexpr int P0 = mb_share(NWI, 0) + mb_share(NXI, 0);
-    constexpr int P1 = mb_share(NWI, 1) + mb_share(NXI, 1);
-    constexpr int P2 = mb_share(NWI, 2) + mb_share(NXI, 2);
-    constexpr int P3 = mb_share(NWI, 3) + mb_share(NXI, 3);
-    switch (wave) {
-        case 0: mb_wait_n<P0>(after); break;
-        case 1: mb_wait_n<P1>(after); break;
-        case 2: mb_wait_n<P2>(after); break;
-        default: mb_wait_n<P3>(after); break;
+    if constexpr (W < WV) {
+        if (wave == W) {
+            mb_wait_n<mb_share(NWI, W, WV) + mb_share(NXI, W, WV)>(after);
+            return;
+        }
+        mb_wait_slabs<NWI, NXI, WV, W + 1>(wave, after);
     }
 }
 
-template <int QT, int MT, int EPI>
-__global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbTheta<EPI> th) {
+template <int QT, int MT, int EPI, int NT, int WV, int KSW>
+__global__ __launch_bounds__(64 * WV) void matvec_batch_kernel(MbJob j, MbTheta<EPI> th) {
+    constexpr int THREADS = 64 * WV;
+    constexpr int ROWS = 32 * NT;
     constexpr int NCH = mb_nch<QT>();
     constexpr int SB = MbFmt<QT>::SB;
-    constexpr int NWI = mb_nwi<QT>();
+    constexpr int NWI = mb_nwi<QT, NT>();
     constexpr int NXI = mb_nxi<MT>();
     constexpr int WB = NWI * 1024;
     constexpr int REC = mb_rec(MT);
-    constexpr int SLOT = mb_slot<QT, MT>();
-    constexpr int NBUF = mb_nbuf<QT, MT>();
-    constexpr int NWL = (NWI + 3) / 4;  // most weight loads of one lane per slab
-    static_assert(NBUF < 3 || 2 * (NWL + (NXI + 3) / 4) < 64, "vmcnt range");
+    constexpr int SLOT = mb_slot<QT, MT, NT>();
+    constexpr int NBUF = mb_nbuf<QT, MT, NT, WV>();
+    constexpr int NWL = (NWI + WV - 1) / WV;  // most weight loads of one lane per slab
+    constexpr int TPW = NT * KSW / WV;        // tiles per wave
+    constexpr int KPW = 16 / KSW;             // k-steps per wave
+    static_assert(TPW >= 1 && NT * KSW == TPW * WV && KPW % 4 == 0, "shape");
+    static_assert(NBUF < 2 || NWL + (NXI + WV - 1) / WV < 64, "vmcnt range");
     extern __shared__ __attribute__((aligned(16))) uint8_t mb_lds[];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, h = lane >> 5, col = lane & 31;
+    const int kpart = wave / (WV / KSW);
+    const int tile0 = (wave % (WV / KSW)) * TPW;
+    const int k0 = kpart * KPW;
     const int group = blockIdx.x % j.n_groups;
     const int split = blockIdx.x / j.n_groups;
     const int s0 = split * j.slabs_per_split;
     const int s1 = min(j.n_slabs, s0 + j.slabs_per_split);
 
-    // this lane's weight chunks: instruction wave + 4 k covers chunks
-    // 64 (wave + 4 k) + lane -> (row, chunk)
+    // this lane's weight chunks: instruction wave + WV k covers chunks
+    // 64 (wave + WV k) + lane -> (row, chunk)
     const uint8_t* wrow[NWL];
     int wch[NWL];
 #pragma unroll
     for (int k = 0; k < NWL; ++k) {
-        const int ci = (wave + 4 * k) * 64 + lane;
+        const int ci = (wave + WV * k) * 64 + lane;
         const int row = ci / NCH;
-        wch[k] = row < kMbRows ? ci % NCH : 0;
-        wrow[k] = mb_row<EPI>(j, group, row < kMbRows ? row : kMbRows - 1);
+        wch[k] = row < ROWS ? ci % NCH : 0;
+        wrow[k] = mb_row<EPI, ROWS>(j, group, row < ROWS ? row : ROWS - 1);
     }
     auto issue = [&](int s) {
         uint8_t* slot = mb_lds + ((s - s0) % NBUF) * SLOT;
 #pragma unroll
         for (int k = 0; k < NWL; ++k) {
-            const int ins = wave + 4 * k;
+            const int ins = wave + WV * k;
             if (ins >= NWI) break;  // wave-uniform
             const uintptr_t a = (uintptr_t)(wrow[k] + (int64_t)s * SB);
             const uintptr_t a0 = a & ~(uintptr_t)15;
@@ -362,16 +373,16 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
         }
         const uint8_t* src = j.xrec + (int64_t)s * REC;
 #pragma unroll
-        for (int k = 0; k < (NXI + 3) / 4; ++k) {
-            const int ins = wave + 4 * k;
+        for (int k = 0; k < (NXI + WV - 1) / WV; ++k) {
+            const int ins = wave + WV * k;
             if (ins >= NXI) break;
             lds_load16(src + ins * 1024 + 16 * lane, slot + WB + ins * 1024);
         }
     };
 
-    mb_f16 acc[2][MT];
+    mb_f16 acc[TPW][MT];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < TPW; ++nt)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -384,7 +395,7 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
             issue(issued);
             ++issued;
         }
-        mb_wait_slabs<NWI, NXI>(wave, issued - 1 - s);
+        mb_wait_slabs<NWI, NXI, WV>(wave, issued - 1 - s);
         __syncthreads();
         const uint8_t* slot = mb_lds + ((s - s0) % NBUF) * SLOT;
         const uint8_t* xa = slot + WB + lane * 16;
@@ -395,38 +406,38 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) invs[mt][r] = meta[mb_token(mt, r, h)];
-        // both 32-row tiles advance together: their matrix-core chains are
+        // the wave's tiles advance together: their matrix-core chains are
         // independent, and each x fragment is read once per k-step
-        const uint8_t* rb[2];
+        const uint8_t* rb[TPW];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            const int row = nt * 32 + col;
-            const uintptr_t a = (uintptr_t)(mb_row<EPI>(j, group, row) + (int64_t)s * SB);
+        for (int nt = 0; nt < TPW; ++nt) {
+            const int row = (tile0 + nt) * 32 + col;
+            const uintptr_t a = (uintptr_t)(mb_row<EPI, ROWS>(j, group, row) + (int64_t)s * SB);
             rb[nt] = slot + row * NCH * 16 + (int)(a & 15);
         }
-        mb_f16 sacc[2][MT];
+        mb_f16 sacc[TPW][MT];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < TPW; ++nt)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) sacc[nt][mt][r] = 0.0f;
-        // k-steps t: tmp[nt][mt] += A(t) B[nt](t) for the hi and lo halves of A
-        auto mfma_step = [&](int t, const mb_h8 (&B)[2], mb_f16 (&tmp)[2][MT]) {
+        // k-step t: tmp[nt][mt] += A(t) B[nt](t) for the hi and lo halves of A
+        auto mfma_step = [&](int t, const mb_h8 (&B)[TPW], mb_f16 (&tmp)[TPW][MT]) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const uint8_t* xp = xa + (mt * 16 + t) * 2048;
                 const mb_h8 ah = *reinterpret_cast<const mb_h8*>(xp);
                 const mb_h8 al = *reinterpret_cast<const mb_h8*>(xp + 1024);
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) tmp[nt][mt] = mfma(ah, B[nt], tmp[nt][mt]);
+                for (int nt = 0; nt < TPW; ++nt) tmp[nt][mt] = mfma(ah, B[nt], tmp[nt][mt]);
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) tmp[nt][mt] = mfma(al, B[nt], tmp[nt][mt]);
+                for (int nt = 0; nt < TPW; ++nt) tmp[nt][mt] = mfma(al, B[nt], tmp[nt][mt]);
             }
         };
-        auto zero = [](mb_f16 (&tmp)[2][MT]) {
+        auto zero = [](mb_f16 (&tmp)[TPW][MT]) {
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
+            for (int nt = 0; nt < TPW; ++nt)
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -436,16 +447,16 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
         if constexpr (QT == kQ4_0 || QT == kQ8_0) {
             constexpr int BB = QT == kQ4_0 ? 18 : 34;
 #pragma unroll
-            for (int bi = 0; bi < 2; ++bi) {
-                const int blk = 2 * wave + bi;
-                float d[2];
-                mb_f16 tmp[2][MT];
+            for (int bi = 0; bi < KPW / 2; ++bi) {
+                const int blk = k0 / 2 + bi;
+                float d[TPW];
+                mb_f16 tmp[TPW][MT];
                 zero(tmp);
 #pragma unroll
                 for (int part = 0; part < 2; ++part) {
-                    mb_h8 B[2];
+                    mb_h8 B[TPW];
 #pragma unroll
-                    for (int nt = 0; nt < 2; ++nt) {
+                    for (int nt = 0; nt < TPW; ++nt) {
                         const uint8_t* bp = rb[nt] + BB * blk;
                         if (part == 0) d[nt] = h2f((uint16_t)lds_u16(bp));
                         if constexpr (QT == kQ4_0) {
@@ -458,7 +469,7 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
                     mfma_step(2 * blk + part, B, tmp);
                 }
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
+                for (int nt = 0; nt < TPW; ++nt)
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -466,31 +477,32 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
                             sacc[nt][mt][r] = fmaf(d[nt], tmp[nt][mt][r], sacc[nt][mt][r]);
             }
         } else if constexpr (QT == kQ4_K) {
-            float d[2], m0[2], m1[2];
-            _Float16 f[2][2];
+            constexpr int NSB = KPW / 2;  // sub-blocks of this wave
+            float d[TPW], mn[TPW][NSB];
+            _Float16 f[TPW][NSB];
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
+            for (int nt = 0; nt < TPW; ++nt) {
                 d[nt] = h2f((uint16_t)lds_u16(rb[nt]));
                 const float dmin = h2f((uint16_t)lds_u16(rb[nt] + 2));
                 uint32_t sw[3];
 #pragma unroll
                 for (int k = 0; k < 3; ++k) sw[k] = lds_u32(rb[nt] + 4 + 4 * k);
-                int sc0, mn0, sc1, mn1;
-                q4_K_scale_min(sw, 2 * wave, sc0, mn0);
-                q4_K_scale_min(sw, 2 * wave + 1, sc1, mn1);
-                f[nt][0] = (_Float16)(float)sc0;
-                f[nt][1] = (_Float16)(float)sc1;
-                m0[nt] = dmin * (float)mn0;
-                m1[nt] = dmin * (float)mn1;
+#pragma unroll
+                for (int q = 0; q < NSB; ++q) {
+                    int sc, m;
+                    q4_K_scale_min(sw, k0 / 2 + q, sc, m);
+                    f[nt][q] = (_Float16)(float)sc;
+                    mn[nt][q] = dmin * (float)m;
+                }
             }
-            mb_f16 tmp[2][MT];
+            mb_f16 tmp[TPW][MT];
             zero(tmp);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int t = 4 * wave + k;
-                mb_h8 B[2];
+            for (int k = 0; k < KPW; ++k) {
+                const int t = k0 + k;
+                mb_h8 B[TPW];
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
+                for (int nt = 0; nt < TPW; ++nt) {
                     const _Float16 g = f[nt][k >> 1];
                     B[nt] = mb_nibbles(lds_u32(rb[nt] + 16 + 8 * t + 4 * h), 0u, 0.0f) *
                             mb_h8{g, g, g, g, g, g, g, g};  // sc * q <= 945: exact
@@ -503,34 +515,39 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int b = mb_token(mt, r, h);
-                    const float xa0 = xs[(2 * wave) * 32 * MT + b];
-                    const float xa1 = xs[(2 * wave + 1) * 32 * MT + b];
+                    float xq[NSB];
 #pragma unroll
-                    for (int nt = 0; nt < 2; ++nt)
-                        sacc[nt][mt][r] = d[nt] * tmp[nt][mt][r] - (m0[nt] * xa0 + m1[nt] * xa1);
+                    for (int q = 0; q < NSB; ++q) xq[q] = xs[(k0 / 2 + q) * 32 * MT + b];
+#pragma unroll
+                    for (int nt = 0; nt < TPW; ++nt) {
+                        float mins = 0.0f;
+#pragma unroll
+                        for (int q = 0; q < NSB; ++q) mins = fmaf(mn[nt][q], xq[q], mins);
+                        sacc[nt][mt][r] = d[nt] * tmp[nt][mt][r] - mins;
+                    }
                 }
         } else {
             static_assert(QT == kQ6_K, "format");
-            float d[2];
+            float d[TPW];
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) d[nt] = h2f((uint16_t)lds_u16(rb[nt] + 208));
+            for (int nt = 0; nt < TPW; ++nt) d[nt] = h2f((uint16_t)lds_u16(rb[nt] + 208));
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int t = 4 * wave + k;
-                mb_h8 B[2];
-                float ds[2];
+            for (int k = 0; k < KPW; ++k) {
+                const int t = k0 + k;
+                mb_h8 B[TPW];
+                float ds[TPW];
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
+                for (int nt = 0; nt < TPW; ++nt) {
                     ds[nt] = d[nt] * (float)(int8_t)rb[nt][192 + t];
                     const uint32_t hq = lds_u16(rb[nt] + 128 + 4 * t + 2 * h);
                     const uint32_t hs = (hq & 0xFFu) | ((hq & 0xFF00u) << 8);
                     B[nt] = mb_nibbles(lds_u32(rb[nt] + 8 * t + 4 * h), hs, -32.0f);
                 }
-                mb_f16 tmp[2][MT];
+                mb_f16 tmp[TPW][MT];
                 zero(tmp);
                 mfma_step(t, B, tmp);
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
+                for (int nt = 0; nt < TPW; ++nt)
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -539,7 +556,7 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
             }
         }
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < TPW; ++nt)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -548,28 +565,41 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
         __syncthreads();  // the slot is refilled by a later issue
     }
 
-    // ---- reduce the four waves (wave order) ----
+    // ---- sum the k-parts (in order) ----
+    constexpr int NV = NT * MT * 1024;   // values per workgroup: [tile][mt][r][lane]
+    constexpr int PV = NV / THREADS;
     float* red = reinterpret_cast<float*>(mb_lds);
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < TPW; ++nt)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-                red[((wave * 2 + nt) * MT + mt) * 1024 + r * 64 + lane] = acc[nt][mt][r];
+                red[(int64_t)kpart * NV + ((tile0 + nt) * MT + mt) * 1024 + r * 64 + lane] =
+                    acc[nt][mt][r];
     __syncthreads();
-    constexpr int NV = 2 * MT * 1024;   // values per workgroup
-    constexpr int PV = NV / kMbThreads;
     float val[PV];
 #pragma unroll
     for (int i = 0; i < PV; ++i) {
-        const int idx = tid + kMbThreads * i;
-        val[i] = ((red[idx] + red[NV + idx]) + red[2 * NV + idx]) + red[3 * NV + idx];
+        const int idx = tid + THREADS * i;
+        float v = red[idx];
+#pragma unroll
+        for (int kp = 1; kp < KSW; ++kp) v += red[kp * NV + idx];
+        val[i] = v;
     }
     if (j.k_splits > 1) {
-        float* mine = j.part + ((int64_t)group * j.k_splits + split) * NV;
+        // partials in thread-contiguous order ([group][split][thread][PV]),
+        // 16-byte device-coherent (sc1) stores and loads, all loads of the
+        // merge issued together
+        const int64_t base = ((int64_t)group * j.k_splits) * NV;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            j.part + base, (short)0, j.k_splits * NV * 4, 0x00020000);
+        const int off0 = (split * NV + tid * PV) * 4;
 #pragma unroll
-        for (int i = 0; i < PV; ++i) rec_store(mine + tid + kMbThreads * i, val[i]);
+        for (int i = 0; i < PV; i += 4) {
+            const mb_f4 v = {val[i], val[i + 1], val[i + 2], val[i + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(v, rs, off0 + 4 * i, 0, kMbSc1);
+        }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         __shared__ int last;
@@ -583,14 +613,23 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
         }
         __syncthreads();
         if (!last) return;
-        const float* all = j.part + (int64_t)group * j.k_splits * NV;
+        float sum[PV];
 #pragma unroll
-        for (int i = 0; i < PV; ++i) {
-            const int idx = tid + kMbThreads * i;
-            float v = rec_load(all + idx);
-            for (int sp = 1; sp < j.k_splits; ++sp) v += rec_load(all + (int64_t)sp * NV + idx);
-            val[i] = v;
+        for (int i = 0; i < PV; ++i) sum[i] = 0.0f;
+        for (int sp = 0; sp < j.k_splits; ++sp) {
+            const int off = (sp * NV + tid * PV) * 4;
+#pragma unroll
+            for (int i = 0; i < PV; i += 4) {
+                const mb_f4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 4 * i, 0, kMbSc1);
+                sum[i] += v[0];
+                sum[i + 1] += v[1];
+                sum[i + 2] += v[2];
+                sum[i + 3] += v[3];
+            }
         }
+        // this thread's values in the epilogue order below
+#pragma unroll
+        for (int i = 0; i < PV; ++i) val[i] = sum[i];
     }
 
     // ---- epilogue ----
@@ -604,9 +643,9 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
     if constexpr (EPI == kMbEpiStore || EPI == kMbEpiAdd) {
 #pragma unroll
         for (int i = 0; i < PV; ++i) {
-            const int idx = tid + kMbThreads * i;
+            const int idx = tid + THREADS * i;
             const int b = token_of(idx);
-            const int row = group * kMbRows + local_of(idx);
+            const int row = group * ROWS + local_of(idx);
             if (b < j.n_batch && row < j.rows) {
                 float* yp = j.y + (int64_t)b * j.ld_y + row;
                 if constexpr (EPI == kMbEpiAdd)
@@ -616,13 +655,13 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
             }
         }
     } else if constexpr (EPI == kMbEpiSwiGLU) {
-        // gate values idx < MT * 1024, up values at idx + MT * 1024 (same lane / register)
+        // gate tiles first: gate value idx < NV / 2, its up value at idx + NV / 2
         static_assert(PV % 2 == 0, "pairs");
 #pragma unroll
         for (int i = 0; i < PV / 2; ++i) {
-            const int idx = tid + kMbThreads * i;
+            const int idx = tid + THREADS * i;
             const int b = token_of(idx);
-            const int row = group * 32 + (idx & 31);
+            const int row = group * (ROWS / 2) + local_of(idx);
             if (b < j.n_batch && row < j.rows)
                 j.y[(int64_t)b * j.ld_y + row] = swiglu_exact(val[i], val[i + PV / 2]);
         }
@@ -631,13 +670,13 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
         // exchanged through LDS so that each thread holds both halves
         float* pv = reinterpret_cast<float*>(mb_lds);
 #pragma unroll
-        for (int i = 0; i < PV; ++i) pv[tid + kMbThreads * i] = val[i];
+        for (int i = 0; i < PV; ++i) pv[tid + THREADS * i] = val[i];
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < PV / 2; ++i) {
-            const int idx = 2 * (tid + kMbThreads * i);  // even lane of the pair
+            const int idx = 2 * (tid + THREADS * i);  // even lane of the pair
             const int b = token_of(idx);
-            const int v0 = group * kMbRows + local_of(idx);
+            const int v0 = group * ROWS + local_of(idx);
             if (b >= j.n_batch || v0 >= j.rows) continue;
             float a = pv[idx], c = pv[idx + 1];
             const int sgi = v0 < j.seg_end[0] ? 0 : v0 < j.seg_end[1] ? 1 : 2;
@@ -670,8 +709,18 @@ __global__ __launch_bounds__(kMbThreads) void matvec_batch_kernel(MbJob j, MbThe
 
 // ---- host side ----
 
-int mb_split(int n_groups, int n_slabs, int* slabs_per_split) {
-    int k = (kMbTargetItems + n_groups - 1) / n_groups;
+// A workgroup shape (see above) and what it implies for a matrix.
+struct MbShape {
+    int nt, wv, ksw;
+    int rows_per_group(int epi) const { return epi == kMbEpiSwiGLU ? 16 * nt : 32 * nt; }
+    int target() const { return wv == 4 ? 512 : 256; }  // workgroups to split the columns for
+};
+
+constexpr MbShape kMbNarrow{2, 4, 4};
+MbShape mb_wide(int qtype) { return (qtype == kQ8_0 || qtype == kQ6_K) ? MbShape{4, 8, 2} : MbShape{8, 8, 1}; }
+
+int mb_split(int n_groups, int n_slabs, int target, int* slabs_per_split) {
+    int k = (target + n_groups - 1) / n_groups;
     if (k > n_slabs) k = n_slabs;
     if (k < 1) k = 1;
     const int per = (n_slabs + k - 1) / k;
@@ -679,27 +728,45 @@ int mb_split(int n_groups, int n_slabs, int* slabs_per_split) {
     return (n_slabs + per - 1) / per;
 }
 
+// Wide workgroups when there are enough of them to fill the GPU with few
+// column splits (each split adds its partials' traffic).
+MbShape mb_shape(int qtype, int epi, int out_rows, int n_slabs) {
+    const MbShape w = mb_wide(qtype);
+    const int groups = (out_rows + w.rows_per_group(epi) - 1) / w.rows_per_group(epi);
+    return groups >= 64 && (int64_t)groups * n_slabs >= 3 * 256 ? w : kMbNarrow;
+}
+
 size_t mb_ctr_bytes(int n_groups) { return ((size_t)n_groups * 4 + 255) / 256 * 256; }
 
 // Workspace: the groups' counters, the x records, then the split partials.
-size_t mb_ws_bytes(int n_groups, int n_slabs, int mt) {
+size_t mb_ws_bytes(const MbShape& sh, int epi, int out_rows, int n_slabs, int mt) {
+    const int groups = (out_rows + sh.rows_per_group(epi) - 1) / sh.rows_per_group(epi);
     int per;
-    const int k = mb_split(n_groups, n_slabs, &per);
-    const size_t parts = k > 1 ? (size_t)n_groups * k * 2 * mt * 1024 * 4 : 0;
-    return mb_ctr_bytes(n_groups) + (size_t)n_slabs * mb_rec(mt) + parts;
+    const int k = mb_split(groups, n_slabs, sh.target(), &per);
+    const size_t parts = k > 1 ? (size_t)groups * k * sh.nt * mt * 1024 * 4 : 0;
+    return mb_ctr_bytes(groups) + (size_t)n_slabs * mb_rec(mt) + parts;
+}
+
+template <int QT, int MT, int EPI, int NT, int WV, int KSW>
+int mb_launch_shape(MbJob& j, const MbTheta<EPI>& th, hipStream_t stream) {
+    const dim3 grid((unsigned)(j.n_groups * j.k_splits));
+    return launch(matvec_batch_kernel<QT, MT, EPI, NT, WV, KSW>, grid, dim3(64 * WV),
+                  mb_lds_bytes<QT, MT, NT, WV>(), stream, j, th);
 }
 
 template <int QT, int MT, int EPI>
-int mb_launch_t(MbJob& j, const MbTheta<EPI>& th, const void* norm_w, int norm_f16, float eps,
-                hipStream_t stream) {
+int mb_launch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void* norm_w,
+                int norm_f16, float eps, hipStream_t stream) {
     const dim3 pgrid((unsigned)((j.n_slabs + 3) / 4), (unsigned)(32 * MT));
     const int rc = launch(mb_prepare_kernel<MT>, pgrid, dim3(256), 0, stream, j.x, j.ld_x,
                           j.n_batch, j.n_slabs * kMbCols, norm_w, norm_f16, eps,
                           const_cast<uint8_t*>(j.xrec));
     if (rc != JINF_HIP_OK) return rc;
-    const dim3 grid((unsigned)(j.n_groups * j.k_splits));
-    return launch(matvec_batch_kernel<QT, MT, EPI>, grid, dim3(kMbThreads),
-                  mb_lds_bytes<QT, MT>(), stream, j, th);
+    if (sh.wv == 4) return mb_launch_shape<QT, MT, EPI, 2, 4, 4>(j, th, stream);
+    if constexpr (QT == kQ8_0 || QT == kQ6_K)
+        return mb_launch_shape<QT, MT, EPI, 4, 8, 2>(j, th, stream);
+    else
+        return mb_launch_shape<QT, MT, EPI, 8, 8, 1>(j, th, stream);
 }
 
 // Sequences 32 .. n_batch - 1 of a job as a job of their own.
@@ -718,32 +785,32 @@ MbJob mb_upper(const MbJob& j) {
     return u;
 }
 
-// More than 32 sequences run as one launch over two M-tiles when the LDS
-// holds two slots of that size, else as two launches of at most 32.
+// More than 32 sequences: one launch over two M-tiles when the shape's LDS
+// holds a slot of that size, else two launches of at most 32.
 template <int QT, int EPI>
-int mb_dispatch_t(MbJob& j, const MbTheta<EPI>& th, const void* norm_w, int norm_f16, float eps,
-                  hipStream_t stream) {
-    if (j.n_batch <= 32) return mb_launch_t<QT, 1, EPI>(j, th, norm_w, norm_f16, eps, stream);
-    if constexpr (mb_nbuf<QT, 2>() >= 2) {
-        return mb_launch_t<QT, 2, EPI>(j, th, norm_w, norm_f16, eps, stream);
-    } else {
-        MbJob lo = j;
-        lo.n_batch = 32;
-        const int rc = mb_launch_t<QT, 1, EPI>(lo, th, norm_w, norm_f16, eps, stream);
-        if (rc != JINF_HIP_OK) return rc;
-        MbJob hi = mb_upper<EPI>(j);
-        return mb_launch_t<QT, 1, EPI>(hi, th, norm_w, norm_f16, eps, stream);
-    }
+int mb_dispatch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void* norm_w,
+                  int norm_f16, float eps, hipStream_t stream) {
+    if (j.n_batch <= 32) return mb_launch_t<QT, 1, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
+    const bool fits = sh.wv == 4 ? mb_slot<QT, 2, 2>() <= kMbLdsBudget
+                                 : (QT == kQ8_0 || QT == kQ6_K) ? mb_slot<QT, 2, 4>() <= kMbLdsBudget
+                                                                : mb_slot<QT, 2, 8>() <= kMbLdsBudget;
+    if (fits) return mb_launch_t<QT, 2, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
+    MbJob lo = j;
+    lo.n_batch = 32;
+    const int rc = mb_launch_t<QT, 1, EPI>(lo, sh, th, norm_w, norm_f16, eps, stream);
+    if (rc != JINF_HIP_OK) return rc;
+    MbJob hi = mb_upper<EPI>(j);
+    return mb_launch_t<QT, 1, EPI>(hi, sh, th, norm_w, norm_f16, eps, stream);
 }
 
 template <int EPI>
-int mb_dispatch(int qtype, MbJob& j, const MbTheta<EPI>& th, const void* norm_w, int norm_f16,
-                float eps, hipStream_t stream) {
+int mb_dispatch(int qtype, MbJob& j, const MbShape& sh, const MbTheta<EPI>& th,
+                const void* norm_w, int norm_f16, float eps, hipStream_t stream) {
     switch (qtype) {
-        case kQ4_0: return mb_dispatch_t<kQ4_0, EPI>(j, th, norm_w, norm_f16, eps, stream);
-        case kQ8_0: return mb_dispatch_t<kQ8_0, EPI>(j, th, norm_w, norm_f16, eps, stream);
-        case kQ4_K: return mb_dispatch_t<kQ4_K, EPI>(j, th, norm_w, norm_f16, eps, stream);
-        case kQ6_K: return mb_dispatch_t<kQ6_K, EPI>(j, th, norm_w, norm_f16, eps, stream);
+        case kQ4_0: return mb_dispatch_t<kQ4_0, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
+        case kQ8_0: return mb_dispatch_t<kQ8_0, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
+        case kQ4_K: return mb_dispatch_t<kQ4_K, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
+        case kQ6_K: return mb_dispatch_t<kQ6_K, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
         default: return JINF_HIP_ERR_INVALID;
     }
 }
@@ -761,9 +828,10 @@ int mb_row_bytes(int qtype, int cols, int64_t* rb) {
     return JINF_HIP_OK;
 }
 
-// Shared checks and job set-up; `group_rows` output rows per workgroup.
-int mb_prepare(MbJob& j, int qtype, int rows, int cols, int n_batch, const float* x, int ld_x,
-               float* y, int ld_y, void* ws, size_t ws_bytes, int group_rows) {
+// Shared checks and job set-up for `rows` output rows of epilogue epi; the
+// workgroup shape follows the matrix.
+int mb_prepare(MbJob& j, MbShape& sh, int qtype, int epi, int rows, int cols, int n_batch,
+               const float* x, int ld_x, float* y, int ld_y, void* ws, size_t ws_bytes) {
     if (rows <= 0 || cols <= 0 || n_batch <= 0 || n_batch > kMbMaxBatch || cols % kMbCols != 0)
         return JINF_HIP_ERR_INVALID;
     if (!x || !y || !aligned(x, 16) || ld_x % 4 != 0 || ld_x < cols || ld_y <= 0)
@@ -771,14 +839,15 @@ int mb_prepare(MbJob& j, int qtype, int rows, int cols, int n_batch, const float
     if (mb_row_bytes(qtype, cols, &j.row_bytes) != JINF_HIP_OK) return JINF_HIP_ERR_INVALID;
     j.rows = rows;
     j.n_slabs = cols / kMbCols;
-    j.n_groups = (rows + group_rows - 1) / group_rows;
+    sh = mb_shape(qtype, epi, rows, j.n_slabs);
+    j.n_groups = (rows + sh.rows_per_group(epi) - 1) / sh.rows_per_group(epi);
     const int mt = n_batch > 32 ? 2 : 1;
-    if (!ws || !aligned(ws, 256) || ws_bytes < mb_ws_bytes(j.n_groups, j.n_slabs, mt)) {
+    if (!ws || !aligned(ws, 256) || ws_bytes < mb_ws_bytes(sh, epi, rows, j.n_slabs, mt)) {
         JINF_LOG("batched GEMV: workspace missing, unaligned or smaller than "
                  "jinf_matvec_batch_workspace_bytes()");
         return JINF_HIP_ERR_INVALID;
     }
-    j.k_splits = mb_split(j.n_groups, j.n_slabs, &j.slabs_per_split);
+    j.k_splits = mb_split(j.n_groups, j.n_slabs, sh.target(), &j.slabs_per_split);
     char* w = static_cast<char*>(ws);
     j.counters = reinterpret_cast<uint32_t*>(w);
     j.xrec = reinterpret_cast<uint8_t*>(w + mb_ctr_bytes(j.n_groups));
@@ -807,11 +876,18 @@ bool w_ok(const void* w) { return w && aligned(w, 16); }
 
 }  // namespace
 
-size_t matvec_batch_ws_bytes(int rows, int cols, int n_batch, int group_rows) {
+// The largest workspace any epilogue and format can need for this shape.
+size_t matvec_batch_ws_bytes(int rows, int cols, int n_batch) {
     if (rows <= 0 || cols <= 0 || cols % kMbCols != 0 || n_batch <= 0 || n_batch > kMbMaxBatch)
         return 0;
-    const int groups = (rows + group_rows - 1) / group_rows;
-    return mb_ws_bytes(groups, cols / kMbCols, n_batch > 32 ? 2 : 1);
+    const int mt = n_batch > 32 ? 2 : 1, n_slabs = cols / kMbCols;
+    size_t most = 0;
+    for (int qtype : {kQ4_0, kQ8_0})
+        for (int epi : {kMbEpiStore, kMbEpiSwiGLU}) {
+            const size_t b = mb_ws_bytes(mb_shape(qtype, epi, rows, n_slabs), epi, rows, n_slabs, mt);
+            most = b > most ? b : most;
+        }
+    return most;
 }
 
 }  // namespace jinf
@@ -819,38 +895,37 @@ size_t matvec_batch_ws_bytes(int rows, int cols, int n_batch, int group_rows) {
 using namespace jinf;
 
 extern "C" size_t jinf_matvec_batch_workspace_bytes(int rows, int cols, int n_batch) {
-    // the SwiGLU variant groups 32 output rows per workgroup
-    const size_t a = matvec_batch_ws_bytes(rows, cols, n_batch, kMbRows);
-    const size_t b = matvec_batch_ws_bytes(rows, cols, n_batch, 32);
-    return a > b ? a : b;
+    return matvec_batch_ws_bytes(rows, cols, n_batch);
 }
 
 extern "C" int jinf_matvec_batch(const void* weight, int qtype, const float* x, int ld_x, float* y,
                                  int ld_y, int rows, int cols, int n_batch, void* workspace,
                                  size_t workspace_bytes, hipStream_t stream) {
     MbJob j{};
+    MbShape sh;
     if (!w_ok(weight)) return JINF_HIP_ERR_INVALID;
-    const int rc = mb_prepare(j, qtype, rows, cols, n_batch, x, ld_x, y, ld_y, workspace,
-                              workspace_bytes, kMbRows);
+    const int rc = mb_prepare(j, sh, qtype, kMbEpiStore, rows, cols, n_batch, x, ld_x, y, ld_y,
+                              workspace, workspace_bytes);
     if (rc != JINF_HIP_OK) return rc;
     if (ld_y < rows) return JINF_HIP_ERR_INVALID;
     j.W[0] = j.W[1] = j.W[2] = static_cast<const uint8_t*>(weight);
     j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = rows;
-    return mb_dispatch<kMbEpiStore>(qtype, j, MbNoTheta{}, nullptr, 0, 0.0f, stream);
+    return mb_dispatch<kMbEpiStore>(qtype, j, sh, MbNoTheta{}, nullptr, 0, 0.0f, stream);
 }
 
 extern "C" int jinf_matvec_batch_add(const void* weight, int qtype, const float* x, int ld_x,
                                      float* y, int ld_y, int rows, int cols, int n_batch,
                                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
     MbJob j{};
+    MbShape sh;
     if (!w_ok(weight)) return JINF_HIP_ERR_INVALID;
-    const int rc = mb_prepare(j, qtype, rows, cols, n_batch, x, ld_x, y, ld_y, workspace,
-                              workspace_bytes, kMbRows);
+    const int rc = mb_prepare(j, sh, qtype, kMbEpiAdd, rows, cols, n_batch, x, ld_x, y, ld_y,
+                              workspace, workspace_bytes);
     if (rc != JINF_HIP_OK) return rc;
     if (ld_y < rows) return JINF_HIP_ERR_INVALID;
     j.W[0] = j.W[1] = j.W[2] = static_cast<const uint8_t*>(weight);
     j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = rows;
-    return mb_dispatch<kMbEpiAdd>(qtype, j, MbNoTheta{}, nullptr, 0, 0.0f, stream);
+    return mb_dispatch<kMbEpiAdd>(qtype, j, sh, MbNoTheta{}, nullptr, 0, 0.0f, stream);
 }
 
 extern "C" int jinf_rmsnorm_matvec_batch(const void* weight, int qtype, const float* h, int ld_h,
@@ -859,16 +934,17 @@ extern "C" int jinf_rmsnorm_matvec_batch(const void* weight, int qtype, const fl
                                          void* workspace, size_t workspace_bytes,
                                          hipStream_t stream) {
     MbJob j{};
+    MbShape sh;
     int f16 = 0;
     if (!w_ok(weight)) return JINF_HIP_ERR_INVALID;
-    int rc = mb_prepare(j, qtype, rows, cols, n_batch, h, ld_h, y, ld_y, workspace,
-                        workspace_bytes, kMbRows);
+    int rc = mb_prepare(j, sh, qtype, kMbEpiStore, rows, cols, n_batch, h, ld_h, y, ld_y,
+                        workspace, workspace_bytes);
     if (rc == JINF_HIP_OK) rc = mb_norm_type(norm_w, norm_type, eps, &f16);
     if (rc != JINF_HIP_OK) return rc;
     if (ld_y < rows) return JINF_HIP_ERR_INVALID;
     j.W[0] = j.W[1] = j.W[2] = static_cast<const uint8_t*>(weight);
     j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = rows;
-    return mb_dispatch<kMbEpiStore>(qtype, j, MbNoTheta{}, norm_w, f16, eps, stream);
+    return mb_dispatch<kMbEpiStore>(qtype, j, sh, MbNoTheta{}, norm_w, f16, eps, stream);
 }
 
 extern "C" int jinf_rmsnorm_swiglu_matvec_batch(const void* w_gate, const void* w_up, int qtype,
@@ -877,10 +953,11 @@ extern "C" int jinf_rmsnorm_swiglu_matvec_batch(const void* w_gate, const void* 
                                                 int n_ff, int cols, int n_batch, void* workspace,
                                                 size_t workspace_bytes, hipStream_t stream) {
     MbJob j{};
+    MbShape sh;
     int f16 = 0;
     if (!w_ok(w_gate) || !w_ok(w_up)) return JINF_HIP_ERR_INVALID;
-    int rc = mb_prepare(j, qtype, n_ff, cols, n_batch, h, ld_h, y, ld_y, workspace,
-                        workspace_bytes, 32);
+    int rc = mb_prepare(j, sh, qtype, kMbEpiSwiGLU, n_ff, cols, n_batch, h, ld_h, y, ld_y,
+                        workspace, workspace_bytes);
     if (rc == JINF_HIP_OK) rc = mb_norm_type(norm_w, norm_type, eps, &f16);
     if (rc != JINF_HIP_OK) return rc;
     if (ld_y < n_ff) return JINF_HIP_ERR_INVALID;
@@ -888,7 +965,7 @@ extern "C" int jinf_rmsnorm_swiglu_matvec_batch(const void* w_gate, const void* 
     j.W[1] = static_cast<const uint8_t*>(w_up);
     j.W[2] = j.W[0];
     j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = n_ff;
-    return mb_dispatch<kMbEpiSwiGLU>(qtype, j, MbNoTheta{}, norm_w, f16, eps, stream);
+    return mb_dispatch<kMbEpiSwiGLU>(qtype, j, sh, MbNoTheta{}, norm_w, f16, eps, stream);
 }
 
 extern "C" int jinf_rmsnorm_qkv_rope_batch(const void* wq, const void* wk, const void* wv,
@@ -913,10 +990,11 @@ extern "C" int jinf_rmsnorm_qkv_rope_batch(const void* wq, const void* wk, const
     if (kv_type != JINF_HIP_F32 && kv_type != JINF_HIP_F16) return JINF_HIP_ERR_INVALID;
     if ((wk || wv) && (max_ctx <= 0 || ld_seq < (int64_t)max_ctx * kvd)) return JINF_HIP_ERR_INVALID;
     MbJob j{};
+    MbShape sh;
     int f16 = 0;
     float* yq = q ? q : const_cast<float*>(h);
-    int rc = mb_prepare(j, qtype, rows, n_embd, n_batch, h, ld_h, yq, wq ? ld_q : 1, workspace,
-                        workspace_bytes, kMbRows);
+    int rc = mb_prepare(j, sh, qtype, kMbEpiQKV, rows, n_embd, n_batch, h, ld_h, yq,
+                        wq ? ld_q : 1, workspace, workspace_bytes);
     if (rc == JINF_HIP_OK) rc = mb_norm_type(norm_w, norm_type, eps, &f16);
     if (rc != JINF_HIP_OK) return rc;
     // segments in q, k, v order; absent matrices take no rows
@@ -939,5 +1017,5 @@ extern "C" int jinf_rmsnorm_qkv_rope_batch(const void* wq, const void* wk, const
     j.ld_seq = ld_seq;
     RopeTheta th;
     theta_table(th, head_dim, freq_base);
-    return mb_dispatch<kMbEpiQKV>(qtype, j, th, norm_w, f16, eps, stream);
+    return mb_dispatch<kMbEpiQKV>(qtype, j, sh, th, norm_w, f16, eps, stream);
 }
