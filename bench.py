@@ -780,7 +780,17 @@ _KERNEL_KEYS = [("ew_vec_kernel<unsigned short, 1", "swiglu"),
                 ("attn_mfma_kernel", "gqa_attention"),
                 ("attn_combine_kernel", "gqa_attention_combine"),
                 ("attn_decode_any_kernel", "gqa_attention_generic"),
-                ("copyBuffer", "copy_calibration")]
+                ("copyBuffer", "copy_calibration"),
+                # batched decode: matvec_batch_kernel<qtype, M-tiles, epilogue, tiles, waves, k-parts>
+                ("matvec_batch_kernel<2, 1, 3,", "batch qkv+rope (Q4_0)"),
+                ("matvec_batch_kernel<2, 1, 1,", "batch o/down+residual (Q4_0)"),
+                ("matvec_batch_kernel<2, 1, 2,", "batch gate/up+swiglu (Q4_0)"),
+                ("matvec_batch_kernel<14, 1, 0,", "batch output head (Q6_K)"),
+                ("matvec_batch_kernel", "batch gemv (other)"),
+                ("mb_prepare_kernel", "batch x preparation"),
+                ("bat_argmax", "batch argmax"),
+                ("bat_begin_kernel", "batch step begin"),
+                ("bat_embed", "batch embedding")]
 
 
 def short_kernel(name):
