@@ -12,9 +12,10 @@
 //     (Q8_0), sc * q <= 945 (Q4_K, the 6-bit sub-block scale folded in) and
 //     q - 32 (Q6_K); the block scales multiply the fp32 partial sums;
 //   - A holds x * s split into fp16 hi + lo (hi = fp16(v), lo = fp16(v - hi)),
-//     s a power of two per (token, 256-column slab) that puts the slab's
-//     largest |x| in [2^14, 2^15): about 22 significant bits, fp16's range
-//     never exceeded, and the 1/s applied exactly to the slab's fp32 sum;
+//     s a power of two per token that puts the row's largest |x| in
+//     [2^14, 2^15): about 22 significant bits for every element down to
+//     2^-18 of that largest one, fp16's range never exceeded, and the 1/s
+//     applied exactly to each slab's fp32 sum;
 //   - Q4_K's minimum term dmin * m * sum(x) uses per-(token, sub-block) sums
 //     of the scaled x.
 // The result equals the fp32 dot product up to the fp32 rounding of the sums
@@ -119,13 +120,15 @@ __device__ __forceinline__ const uint8_t* mb_row(const MbJob& j, int group, int 
         constexpr int HALF = ROWS / 2;
         int r = group * HALF + local % HALF;
         if (r >= j.rows) r = j.rows - 1;
-        return j.W[local / HALF] + (int64_t)r * j.row_bytes;
+        return (local < HALF ? j.W[0] : j.W[1]) + (int64_t)r * j.row_bytes;
     } else {
         int v = group * ROWS + local;
         if (v >= j.rows) v = j.rows - 1;
-        const int s = v < j.seg_end[0] ? 0 : v < j.seg_end[1] ? 1 : 2;
-        const int start = s == 0 ? 0 : j.seg_end[s - 1];
-        return j.W[s] + (int64_t)(v - start) * j.row_bytes;
+        // selects, not an index into the job's arrays (which would place the
+        // kernel argument in scratch memory)
+        const uint8_t* base = v < j.seg_end[0] ? j.W[0] : v < j.seg_end[1] ? j.W[1] : j.W[2];
+        const int start = v < j.seg_end[0] ? 0 : v < j.seg_end[1] ? j.seg_end[0] : j.seg_end[1];
+        return base + (int64_t)(v - start) * j.row_bytes;
     }
 }
 
@@ -181,19 +184,27 @@ __device__ __forceinline__ int mb_token(int mt, int r, int h) {
 
 // ---- x preparation ----
 //
-// One record per 256-column slab, in the order the GEMV copies it into LDS:
+// One record per 256-column slab, in the order the GEMVs read it:
 //   [MT M-tiles][16 k-steps][hi, lo][64 lanes] 16-byte fragments, lane
 //   (token % 32) + 32 h holding columns 16 t + 8 h .. + 7 in the order
 //   (0, 4, 1, 5, 2, 6, 3, 7);
-//   then the slab data: inv_s[32 MT] (1/s per token) and Q4_K's
-//   xs[8 sub-blocks][32 MT tokens] (sums of the scaled x over 32 columns).
-// Slab data after the fragments: inv_s[32 MT] floats, then xs[8][32 MT].
+//   then the slab data: inv_s[32 MT] (1/s per token, the same in every slab)
+//   and Q4_K's xs[8 sub-blocks][32 MT tokens] (sums of the scaled x over 32
+//   columns).
 __host__ __device__ constexpr int mb_meta(int mt) { return 2048 * mt; }
 __host__ __device__ constexpr int mb_rec(int mt) { return mt * 32768 + mb_meta(mt); }
 
-// grid (ceil(n_slabs / 4), 32 MT): each wave converts one slab of one token
-// (tokens >= n_batch get zeros, unit scale); with norm_w the row is first
-// RMS-normalised exactly as jinf_rmsnorm_rows does (x^ = fl32(fl32(x rs) g)).
+constexpr int kMbMaxCols = 32768;                 // columns the preparation holds
+constexpr int kMbPrepG = kMbMaxCols / 8 / 256;    // 8-column groups per thread
+
+// grid (32 MT): one workgroup per token row, the row held in registers
+// (thread i takes the 8-column groups i, i + 256, ...); tokens >= n_batch
+// get zeros and unit scale.  With norm_w the row is first RMS-normalised
+// exactly as jinf_rmsnorm_rows does (x^ = fl32(fl32(x rs) g)).  One power of
+// two s per token puts max |x^ s| in [2^14, 2^15): hi = fp16(x^ s) and
+// lo = fp16(x^ s - hi) then carry about 22 significant bits of every element
+// (lo reaches fp16's subnormals only below 2^-18 of the row's largest
+// element), and fp16's range is never exceeded.
 template <int MT>
 __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict__ x, int ld_x,
                                                           int n_batch, int cols,
@@ -201,69 +212,96 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
                                                           int norm_f16, float eps,
                                                           uint8_t* __restrict__ rec) {
     __shared__ double red[4];
-    const int b = blockIdx.y;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int n_slabs = cols / kMbCols;
+    __shared__ float redf[4];
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int ng = cols / 8;  // a multiple of 32
     const bool live = b < n_batch;
     const float* xr = x + (int64_t)(live ? b : 0) * ld_x;
-    float rs = 1.0f;
+    float v[kMbPrepG][8];
+#pragma unroll
+    for (int k = 0; k < kMbPrepG; ++k) {
+        const int g = tid + 256 * k;
+        if (live && g < ng) {
+            const float4 p = *reinterpret_cast<const float4*>(xr + 8 * g);
+            const float4 q = *reinterpret_cast<const float4*>(xr + 8 * g + 4);
+            v[k][0] = p.x; v[k][1] = p.y; v[k][2] = p.z; v[k][3] = p.w;
+            v[k][4] = q.x; v[k][5] = q.y; v[k][6] = q.z; v[k][7] = q.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[k][e] = 0.0f;
+        }
+    }
     if (norm_w && live) {
         double ss = 0.0;
-        for (int c = threadIdx.x; c < cols; c += 256) ss = fma((double)xr[c], (double)xr[c], ss);
+#pragma unroll
+        for (int k = 0; k < kMbPrepG; ++k)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fma((double)v[k][e], (double)v[k][e], ss);
         ss = block_sum(ss, red);
-        rs = rms_scale(ss, cols, eps);
-    }
-    const int slab = blockIdx.x * 4 + wave;
-    if (slab >= n_slabs) return;
-    const int c0 = slab * kMbCols + 4 * lane;
-    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (live) {
-        const float4 q = *reinterpret_cast<const float4*>(xr + c0);
-        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
-        if (norm_w) {
+        const float rs = rms_scale(ss, cols, eps);
+#pragma unroll
+        for (int k = 0; k < kMbPrepG; ++k) {
+            const int g = tid + 256 * k;
+            if (g < ng) {
 #pragma clang fp contract(off)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float g = norm_f16 ? h2f(static_cast<const uint16_t*>(norm_w)[c0 + i])
-                                         : static_cast<const float*>(norm_w)[c0 + i];
-                v[i] = (v[i] * rs) * g;
+                for (int e = 0; e < 8; ++e) {
+                    const int c = 8 * g + e;
+                    const float gw = norm_f16 ? h2f(static_cast<const uint16_t*>(norm_w)[c])
+                                              : static_cast<const float*>(norm_w)[c];
+                    v[k][e] = (v[k][e] * rs) * gw;
+                }
             }
         }
     }
-    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    m = wave_max(m);
-    int e = 15;
-    if (m > 0.0f && m <= 3.4e38f) {
-        (void)frexpf(m, &e);  // m < 2^e
-        e = e < -100 ? -100 : e;
-    }
-    const float sc = ldexpf(1.0f, 15 - e);
-    uint8_t* r = rec + (int64_t)slab * mb_rec(MT);
-    // columns cs = 4 lane .. + 3 of the slab: k-step cs / 16, half (cs % 16) / 8,
-    // fragment slot of column e8 = cs % 8 in the order (0, 4, 1, 5, 2, 6, 3, 7)
-    const int cs = 4 * lane, t = cs >> 4, h = (cs >> 3) & 1;
-    const int lf = (b & 31) + 32 * h;
-    uint16_t* fh = reinterpret_cast<uint16_t*>(r + (((b >> 5) * 16 + t) * 2) * 1024 + lf * 16);
-    uint16_t* fl = fh + 512;  // lo half: 1024 bytes further
-    const int e0 = cs & 7;    // 0 or 4
-    float sum = 0.0f;
+    float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float a = v[i] * sc;
-        const _Float16 hh = (_Float16)a;
-        const _Float16 ll = (_Float16)(a - (float)hh);
-        const int slot = 2 * (e0 + i) - (e0 ? 7 : 0);  // 0,2,4,6 / 1,3,5,7
-        fh[slot] = __builtin_bit_cast(uint16_t, hh);
-        fl[slot] = __builtin_bit_cast(uint16_t, ll);
-        sum += a;
+    for (int k = 0; k < kMbPrepG; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[k][e]));
+    m = block_max(m, redf);
+    int ex = 15;
+    if (m > 0.0f && m <= 3.4e38f) {
+        (void)frexpf(m, &ex);  // m < 2^ex
+        ex = ex < -100 ? -100 : ex;
     }
-    float* meta = reinterpret_cast<float*>(r + MT * 32768);
-    if (lane == 0) meta[b] = ldexpf(1.0f, e - 15);
-    // Q4_K sub-block sums: lanes 8 j .. 8 j + 7 hold sub-block j's 32 columns
-    sum += __shfl_xor(sum, 1, kWave);
-    sum += __shfl_xor(sum, 2, kWave);
-    sum += __shfl_xor(sum, 4, kWave);
-    if ((lane & 7) == 0) meta[32 * MT + (lane >> 3) * 32 * MT + b] = sum;
+    const float sc = ldexpf(1.0f, 15 - ex);
+#pragma unroll
+    for (int k = 0; k < kMbPrepG; ++k) {
+        const int g = tid + 256 * k;
+        const bool here = g < ng;  // uniform over aligned groups of 32 threads
+        const int slab = g >> 5, gi = g & 31, t = gi >> 1, h = gi & 1;
+        uint8_t* r = rec + (int64_t)slab * mb_rec(MT);
+        float sum = 0.0f;
+        if (here) {
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // fragment slots 2 i, 2 i + 1 hold columns i and 4 + i of the group
+                const float a0 = v[k][i] * sc, a1 = v[k][4 + i] * sc;
+                const _Float16 h0 = (_Float16)a0, h1 = (_Float16)a1;
+                const _Float16 l0 = (_Float16)(a0 - (float)h0), l1 = (_Float16)(a1 - (float)h1);
+                hw[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
+                        ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                lw[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
+                        ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += v[k][e] * sc;
+            uint8_t* f = r + (((b >> 5) * 16 + t) * 2) * 1024 + ((b & 31) + 32 * h) * 16;
+            *reinterpret_cast<uint4*>(f) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            *reinterpret_cast<uint4*>(f + 1024) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        }
+        // Q4_K sub-block sums: threads 4 q .. 4 q + 3 hold sub-block q's 32 columns
+        sum += __shfl_xor(sum, 1, kWave);
+        sum += __shfl_xor(sum, 2, kWave);
+        if (here) {
+            float* meta = reinterpret_cast<float*>(r + MT * 32768);
+            if ((gi & 3) == 0) meta[32 * MT + (gi >> 2) * 32 * MT + b] = sum;
+            if (gi == 0) meta[b] = ldexpf(1.0f, ex - 15);
+        }
+    }
 }
 
 // ---- the GEMV ----
@@ -709,18 +747,27 @@ __global__ __launch_bounds__(64 * WV) void matvec_batch_kernel(MbJob j, MbTheta<
 
 // ---- host side ----
 
+
 // A workgroup shape (see above) and what it implies for a matrix.
 struct MbShape {
     int nt, wv, ksw;
     int rows_per_group(int epi) const { return epi == kMbEpiSwiGLU ? 16 * nt : 32 * nt; }
-    int target() const { return wv == 4 ? 512 : 256; }  // workgroups to split the columns for
 };
 
 constexpr MbShape kMbNarrow{2, 4, 4};
-MbShape mb_wide(int qtype) { return (qtype == kQ8_0 || qtype == kQ6_K) ? MbShape{4, 8, 2} : MbShape{8, 8, 1}; }
+MbShape mb_wide(int qtype) {
+    return (qtype == kQ8_0 || qtype == kQ6_K) ? MbShape{4, 8, 2} : MbShape{8, 8, 1};
+}
 
-int mb_split(int n_groups, int n_slabs, int target, int* slabs_per_split) {
-    int k = (target + n_groups - 1) / n_groups;
+// Column splits: as many as keep the workgroups at most kMbSplitTarget
+// (rounded down).  Each split adds its partials' device-coherent traffic and
+// the merging workgroup's tail; measured at 32 sequences on the Llama-3-8B
+// shapes, this count beat rounding up (14336 x 4096: 26.8 against 31.7 us;
+// 28672 x 4096: 47.6 against 59.7 us) and smaller targets (4096 x 14336:
+// 26.4 us at 512 workgroups, 35.9 at 256).
+constexpr int kMbSplitTarget = 512;
+int mb_split(int n_groups, int n_slabs, int* slabs_per_split) {
+    int k = kMbSplitTarget / n_groups;
     if (k > n_slabs) k = n_slabs;
     if (k < 1) k = 1;
     const int per = (n_slabs + k - 1) / k;
@@ -742,7 +789,7 @@ size_t mb_ctr_bytes(int n_groups) { return ((size_t)n_groups * 4 + 255) / 256 * 
 size_t mb_ws_bytes(const MbShape& sh, int epi, int out_rows, int n_slabs, int mt) {
     const int groups = (out_rows + sh.rows_per_group(epi) - 1) / sh.rows_per_group(epi);
     int per;
-    const int k = mb_split(groups, n_slabs, sh.target(), &per);
+    const int k = mb_split(groups, n_slabs, &per);
     const size_t parts = k > 1 ? (size_t)groups * k * sh.nt * mt * 1024 * 4 : 0;
     return mb_ctr_bytes(groups) + (size_t)n_slabs * mb_rec(mt) + parts;
 }
@@ -757,8 +804,7 @@ int mb_launch_shape(MbJob& j, const MbTheta<EPI>& th, hipStream_t stream) {
 template <int QT, int MT, int EPI>
 int mb_launch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void* norm_w,
                 int norm_f16, float eps, hipStream_t stream) {
-    const dim3 pgrid((unsigned)((j.n_slabs + 3) / 4), (unsigned)(32 * MT));
-    const int rc = launch(mb_prepare_kernel<MT>, pgrid, dim3(256), 0, stream, j.x, j.ld_x,
+    const int rc = launch(mb_prepare_kernel<MT>, dim3(32 * MT), dim3(256), 0, stream, j.x, j.ld_x,
                           j.n_batch, j.n_slabs * kMbCols, norm_w, norm_f16, eps,
                           const_cast<uint8_t*>(j.xrec));
     if (rc != JINF_HIP_OK) return rc;
@@ -832,7 +878,8 @@ int mb_row_bytes(int qtype, int cols, int64_t* rb) {
 // workgroup shape follows the matrix.
 int mb_prepare(MbJob& j, MbShape& sh, int qtype, int epi, int rows, int cols, int n_batch,
                const float* x, int ld_x, float* y, int ld_y, void* ws, size_t ws_bytes) {
-    if (rows <= 0 || cols <= 0 || n_batch <= 0 || n_batch > kMbMaxBatch || cols % kMbCols != 0)
+    if (rows <= 0 || cols <= 0 || n_batch <= 0 || n_batch > kMbMaxBatch || cols % kMbCols != 0 ||
+        cols > kMbMaxCols)
         return JINF_HIP_ERR_INVALID;
     if (!x || !y || !aligned(x, 16) || ld_x % 4 != 0 || ld_x < cols || ld_y <= 0)
         return JINF_HIP_ERR_INVALID;
@@ -847,7 +894,7 @@ int mb_prepare(MbJob& j, MbShape& sh, int qtype, int epi, int rows, int cols, in
                  "jinf_matvec_batch_workspace_bytes()");
         return JINF_HIP_ERR_INVALID;
     }
-    j.k_splits = mb_split(j.n_groups, j.n_slabs, sh.target(), &j.slabs_per_split);
+    j.k_splits = mb_split(j.n_groups, j.n_slabs, &j.slabs_per_split);
     char* w = static_cast<char*>(ws);
     j.counters = reinterpret_cast<uint32_t*>(w);
     j.xrec = reinterpret_cast<uint8_t*>(w + mb_ctr_bytes(j.n_groups));
@@ -878,7 +925,8 @@ bool w_ok(const void* w) { return w && aligned(w, 16); }
 
 // The largest workspace any epilogue and format can need for this shape.
 size_t matvec_batch_ws_bytes(int rows, int cols, int n_batch) {
-    if (rows <= 0 || cols <= 0 || cols % kMbCols != 0 || n_batch <= 0 || n_batch > kMbMaxBatch)
+    if (rows <= 0 || cols <= 0 || cols % kMbCols != 0 || cols > kMbMaxCols || n_batch <= 0 ||
+        n_batch > kMbMaxBatch)
         return 0;
     const int mt = n_batch > 32 ? 2 : 1, n_slabs = cols / kMbCols;
     size_t most = 0;
