@@ -232,14 +232,45 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
             for (int e = 0; e < 8; ++e) v[k][e] = 0.0f;
         }
     }
+    // one workgroup reduction: the sum of squares (norm_w) and the largest
+    // |x g| (|x| without norm_w); max |x^| <= rs max |x g| up to a few
+    // roundings, so rs max |x g| fixes the scale (|x^ s| stays below
+    // 2^15 (1 + 2^-21), far inside fp16's range)
+    double ss = 0.0;
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMbPrepG; ++k) {
+        const int g = tid + 256 * k;
+        if (g < ng) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float gw = 1.0f;
+                if (norm_w) {
+                    gw = norm_f16 ? h2f(static_cast<const uint16_t*>(norm_w)[8 * g + e])
+                                  : static_cast<const float*>(norm_w)[8 * g + e];
+                    ss = fma((double)v[k][e], (double)v[k][e], ss);
+                }
+                m = fmaxf(m, fabsf(v[k][e] * gw));
+            }
+        }
+    }
+    ss = wave_sum(ss);
+    m = wave_max(m);
+    if ((tid & (kWave - 1)) == 0) {
+        red[tid / kWave] = ss;
+        redf[tid / kWave] = m;
+    }
+    __syncthreads();
+    ss = red[0];
+    m = redf[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) {
+        ss += red[i];
+        m = fmaxf(m, redf[i]);
+    }
     if (norm_w && live) {
-        double ss = 0.0;
-#pragma unroll
-        for (int k = 0; k < kMbPrepG; ++k)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ss = fma((double)v[k][e], (double)v[k][e], ss);
-        ss = block_sum(ss, red);
         const float rs = rms_scale(ss, cols, eps);
+        m = rs * m;
 #pragma unroll
         for (int k = 0; k < kMbPrepG; ++k) {
             const int g = tid + 256 * k;
@@ -255,12 +286,6 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
             }
         }
     }
-    float m = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kMbPrepG; ++k)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[k][e]));
-    m = block_max(m, redf);
     int ex = 15;
     if (m > 0.0f && m <= 3.4e38f) {
         (void)frexpf(m, &ex);  // m < 2^ex
@@ -439,11 +464,6 @@ __global__ __launch_bounds__(64 * WV) void matvec_batch_kernel(MbJob j, MbTheta<
         const uint8_t* xa = slot + WB + lane * 16;
         const float* meta = reinterpret_cast<const float*>(slot + WB + MT * 32768);
 
-        float invs[MT][16];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) invs[mt][r] = meta[mb_token(mt, r, h)];
         // the wave's tiles advance together: their matrix-core chains are
         // independent, and each x fragment is read once per k-step
         const uint8_t* rb[TPW];
@@ -453,13 +473,6 @@ __global__ __launch_bounds__(64 * WV) void matvec_batch_kernel(MbJob j, MbTheta<
             const uintptr_t a = (uintptr_t)(mb_row<EPI, ROWS>(j, group, row) + (int64_t)s * SB);
             rb[nt] = slot + row * NCH * 16 + (int)(a & 15);
         }
-        mb_f16 sacc[TPW][MT];
-#pragma unroll
-        for (int nt = 0; nt < TPW; ++nt)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[nt][mt][r] = 0.0f;
         // k-step t: tmp[nt][mt] += A(t) B[nt](t) for the hi and lo halves of A
         auto mfma_step = [&](int t, const mb_h8 (&B)[TPW], mb_f16 (&tmp)[TPW][MT]) {
 #pragma unroll
@@ -512,7 +525,7 @@ __global__ __launch_bounds__(64 * WV) void matvec_batch_kernel(MbJob j, MbTheta<
                     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                         for (int r = 0; r < 16; ++r)
-                            sacc[nt][mt][r] = fmaf(d[nt], tmp[nt][mt][r], sacc[nt][mt][r]);
+                            acc[nt][mt][r] = fmaf(d[nt], tmp[nt][mt][r], acc[nt][mt][r]);
             }
         } else if constexpr (QT == kQ4_K) {
             constexpr int NSB = KPW / 2;  // sub-blocks of this wave
@@ -561,7 +574,7 @@ __global__ __launch_bounds__(64 * WV) void matvec_batch_kernel(MbJob j, MbTheta<
                         float mins = 0.0f;
 #pragma unroll
                         for (int q = 0; q < NSB; ++q) mins = fmaf(mn[nt][q], xq[q], mins);
-                        sacc[nt][mt][r] = d[nt] * tmp[nt][mt][r] - mins;
+                        acc[nt][mt][r] += d[nt] * tmp[nt][mt][r] - mins;
                     }
                 }
         } else {
@@ -590,17 +603,23 @@ __global__ __launch_bounds__(64 * WV) void matvec_batch_kernel(MbJob j, MbTheta<
                     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                         for (int r = 0; r < 16; ++r)
-                            sacc[nt][mt][r] = fmaf(ds[nt], tmp[nt][mt][r], sacc[nt][mt][r]);
+                            acc[nt][mt][r] = fmaf(ds[nt], tmp[nt][mt][r], acc[nt][mt][r]);
             }
         }
-#pragma unroll
-        for (int nt = 0; nt < TPW; ++nt)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    acc[nt][mt][r] = fmaf(sacc[nt][mt][r], invs[mt][r], acc[nt][mt][r]);
         __syncthreads();  // the slot is refilled by a later issue
+    }
+    // the sums are in units of x * s: 1 / s per token (the same in every
+    // slab's record) scales them exactly
+    {
+        const float* inv = reinterpret_cast<const float*>(j.xrec + MT * 32768);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float is = inv[mb_token(mt, r, h)];
+#pragma unroll
+                for (int nt = 0; nt < TPW; ++nt) acc[nt][mt][r] *= is;
+            }
     }
 
     // ---- sum the k-parts (in order) ----
