@@ -197,14 +197,43 @@ __host__ __device__ constexpr int mb_rec(int mt) { return mt * 32768 + mb_meta(m
 constexpr int kMbMaxCols = 32768;                 // columns the preparation holds
 constexpr int kMbPrepG = kMbMaxCols / 8 / 256;    // 8-column groups per thread
 
-// grid (32 MT): one workgroup per token row, the row held in registers
-// (thread i takes the 8-column groups i, i + 256, ...); tokens >= n_batch
-// get zeros and unit scale.  With norm_w the row is first RMS-normalised
-// exactly as jinf_rmsnorm_rows does (x^ = fl32(fl32(x rs) g)).  One power of
-// two s per token puts max |x^ s| in [2^14, 2^15): hi = fp16(x^ s) and
-// lo = fp16(x^ s - hi) then carry about 22 significant bits of every element
-// (lo reaches fp16's subnormals only below 2^-18 of the row's largest
-// element), and fp16's range is never exceeded.
+// grid (ceil(n_slabs / 8), 32 MT): workgroup (c, b) converts slabs 8 c ..
+// 8 c + 7 of token b.  Each holds token b's whole row in registers (thread i
+// takes the 8-column groups i, i + 256, ...; every workgroup of the token
+// reads the row, mostly from L2) for the row's one reduction; tokens >=
+// n_batch get zeros and unit scale.  With norm_w the row is first
+// RMS-normalised exactly as jinf_rmsnorm_rows does (x^ = fl32(fl32(x rs) g)).
+// One power of two s per token puts max |x^ s| in [2^14, 2^15): hi =
+// fp16(x^ s) and lo = fp16(x^ s - hi) then carry about 22 significant bits
+// of every element (lo reaches fp16's subnormals only below 2^-18 of the
+// row's largest element), and fp16's range is never exceeded.
+// RMSNorm weights of 8-column group g (1 without a norm): 16-byte loads when
+// the weights are 16-byte aligned, else element loads.
+__device__ __forceinline__ void mb_norm8(const void* norm_w, int norm_f16, int g, float (&gw)[8]) {
+    if (!norm_w) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gw[e] = 1.0f;
+    } else if (((uintptr_t)norm_w & 15) != 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            gw[e] = norm_f16 ? h2f(static_cast<const uint16_t*>(norm_w)[8 * g + e])
+                             : static_cast<const float*>(norm_w)[8 * g + e];
+    } else if (norm_f16) {
+        const uint4 q = *(static_cast<const uint4*>(norm_w) + g);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            gw[2 * i] = h2f((uint16_t)(w[i] & 0xFFFFu));
+            gw[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
+        }
+    } else {
+        const float4 p = *(static_cast<const float4*>(norm_w) + 2 * g);
+        const float4 q = *(static_cast<const float4*>(norm_w) + 2 * g + 1);
+        gw[0] = p.x; gw[1] = p.y; gw[2] = p.z; gw[3] = p.w;
+        gw[4] = q.x; gw[5] = q.y; gw[6] = q.z; gw[7] = q.w;
+    }
+}
+
 template <int MT>
 __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict__ x, int ld_x,
                                                           int n_batch, int cols,
@@ -213,7 +242,7 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
                                                           uint8_t* __restrict__ rec) {
     __shared__ double red[4];
     __shared__ float redf[4];
-    const int b = blockIdx.x;
+    const int b = blockIdx.y;
     const int tid = threadIdx.x;
     const int ng = cols / 8;  // a multiple of 32
     const bool live = b < n_batch;
@@ -242,15 +271,12 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
     for (int k = 0; k < kMbPrepG; ++k) {
         const int g = tid + 256 * k;
         if (g < ng) {
+            float gw[8];
+            mb_norm8(norm_w, norm_f16, g, gw);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                float gw = 1.0f;
-                if (norm_w) {
-                    gw = norm_f16 ? h2f(static_cast<const uint16_t*>(norm_w)[8 * g + e])
-                                  : static_cast<const float*>(norm_w)[8 * g + e];
-                    ss = fma((double)v[k][e], (double)v[k][e], ss);
-                }
-                m = fmaxf(m, fabsf(v[k][e] * gw));
+                if (norm_w) ss = fma((double)v[k][e], (double)v[k][e], ss);
+                m = fmaxf(m, fabsf(v[k][e] * gw[e]));
             }
         }
     }
@@ -274,15 +300,12 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
 #pragma unroll
         for (int k = 0; k < kMbPrepG; ++k) {
             const int g = tid + 256 * k;
-            if (g < ng) {
+            if (g < ng && k == (int)blockIdx.x) {  // only this workgroup's groups
 #pragma clang fp contract(off)
+                float gw[8];
+                mb_norm8(norm_w, norm_f16, g, gw);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int c = 8 * g + e;
-                    const float gw = norm_f16 ? h2f(static_cast<const uint16_t*>(norm_w)[c])
-                                              : static_cast<const float*>(norm_w)[c];
-                    v[k][e] = (v[k][e] * rs) * gw;
-                }
+                for (int e = 0; e < 8; ++e) v[k][e] = (v[k][e] * rs) * gw[e];
             }
         }
     }
@@ -295,7 +318,8 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
 #pragma unroll
     for (int k = 0; k < kMbPrepG; ++k) {
         const int g = tid + 256 * k;
-        const bool here = g < ng;  // uniform over aligned groups of 32 threads
+        // this workgroup's 256 groups (uniform over aligned groups of 32 threads)
+        const bool here = g < ng && k == (int)blockIdx.x;
         const int slab = g >> 5, gi = g & 31, t = gi >> 1, h = gi & 1;
         uint8_t* r = rec + (int64_t)slab * mb_rec(MT);
         float sum = 0.0f;
@@ -823,7 +847,8 @@ int mb_launch_shape(MbJob& j, const MbTheta<EPI>& th, hipStream_t stream) {
 template <int QT, int MT, int EPI>
 int mb_launch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void* norm_w,
                 int norm_f16, float eps, hipStream_t stream) {
-    const int rc = launch(mb_prepare_kernel<MT>, dim3(32 * MT), dim3(256), 0, stream, j.x, j.ld_x,
+    const int rc = launch(mb_prepare_kernel<MT>, dim3((unsigned)((j.n_slabs + 7) / 8), 32 * MT),
+                          dim3(256), 0, stream, j.x, j.ld_x,
                           j.n_batch, j.n_slabs * kMbCols, norm_w, norm_f16, eps,
                           const_cast<uint8_t*>(j.xrec));
     if (rc != JINF_HIP_OK) return rc;

@@ -9,7 +9,7 @@ Bars, as for the one-token GEMVs (a = sum_j |w_j x_j| of a row, the dot
 product's own rounding scale): a GEMV output |y - y_oracle| <= 1e-5 * a;
 + residual: 1e-5 * a + one fp32 rounding of the sum; SiLU(g) * u and RoPE
 pairs carry the GEMV bars through as in test_gpu_fused.py.  The x halves
-(fp16 hi + lo under a power-of-two scale per 256 columns) keep about 22 bits,
+(fp16 hi + lo under a power-of-two scale per token) keep about 22 bits,
 far inside these bars; rows of very different magnitudes in one batch, zero
 rows and launches that split the columns exercise the scaling and the merge.
 """
@@ -137,6 +137,10 @@ def test_rmsnorm_matvec_batch(dev, qtype, g_dtype):
     ws = jinf_amd.matvec_batch_workspace(rows, cols, n_batch)
     y = host(jinf_amd.rmsnorm_matvec_batch(to_dev(W), Hd, qtype, to_dev(g), EPS, workspace=ws))
     check(y, ref, 1e-5 * a, "rmsnorm + GEMV")
+    # norm weights that are not 16-byte aligned (element loads): the same bits
+    gbuf = to_dev(np.concatenate([np.zeros(1, g_dtype), g]))
+    y1 = host(jinf_amd.rmsnorm_matvec_batch(to_dev(W), Hd, qtype, gbuf[1:], EPS, workspace=ws))
+    assert np.array_equal(y1.view(np.uint32), y.view(np.uint32))
     # no norm weight: the plain batched GEMV of h
     ref2, a2 = mv_rows(qtype, W, H)
     y2 = host(jinf_amd.rmsnorm_matvec_batch(to_dev(W), Hd, qtype, None, EPS, workspace=ws))
