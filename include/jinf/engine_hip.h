@@ -141,7 +141,7 @@ uint64_t jinf_hip_engine_step_weight_bytes(const jinf_hip_engine* e);
  * all of them at once on the matrix cores (jinf_*_batch), so each weight
  * byte is read once per step.  The reference has no counterpart: it decodes
  * one sequence (src/engine.cpp:684-805); per sequence the arithmetic is that
- * loop's.  Needs n_embd and n_ff multiples of 256. ---- */
+ * loop's.  Needs n_embd and n_ff multiples of 256, at most 32768. ---- */
 typedef struct jinf_hip_batch jinf_hip_batch;
 
 int  jinf_hip_batch_create(jinf_hip_batch** out, const jinf_hip_engine* engine, int n_seq,

@@ -188,13 +188,13 @@ int jinf_rmsnorm_qkv_rope(const void* w_q, const void* w_k, const void* w_v, int
  * src/engine.cpp:429-508 for n_batch (1..64) sequences decoded together, so
  * that each weight byte read serves all of them.  Row b of x / h / y is
  * ld_x / ld_h / ld_y elements after row b - 1.  Same weights and formats as
- * jinf_matvec with cols a multiple of 256 and every matrix 16-byte aligned
- * (the bytes up to the next 16-byte boundary past a matrix's end are read, as
- * any device allocation allows; other shapes return 5), x / h 16-byte aligned
- * with ld a multiple of 4.  Products are exact fp16 x fp16 on the matrix
- * cores with x split into two fp16 halves under a power-of-two scale per 256
- * columns (about 22 significant bits); each result equals the fp32 dot
- * product up to the fp32 rounding of the sums.
+ * jinf_matvec with cols a multiple of 256 and at most 32768 and every matrix
+ * 16-byte aligned (the bytes up to the next 16-byte boundary past a matrix's
+ * end are read, as any device allocation allows; other shapes return 5), x / h
+ * 16-byte aligned with ld a multiple of 4.  Products are exact fp16 x fp16 on
+ * the matrix cores with x split into two fp16 halves under a power-of-two
+ * scale per sequence (about 22 significant bits); each result equals the fp32
+ * dot product up to the fp32 rounding of the sums.
  *
  * RMSNorm variants: x^ = fl32(fl32(h * rs) * g) exactly as jinf_rmsnorm_rows
  * computes it (norm_w NULL: x^ = h); norm_type 0 fp32, 1 fp16.

@@ -340,8 +340,9 @@ extern "C" int jinf_hip_batch_create(jinf_hip_batch** out, const jinf_hip_engine
     if (!dp || n_seq < 1 || n_seq > 64 || max_context <= 0) return JINF_HIP_ERR_INVALID;
     if (kv_type != JINF_HIP_F32 && kv_type != JINF_HIP_F16) return JINF_HIP_ERR_INVALID;
     const jinf_hip_engine_desc& d = *dp;
-    if (d.n_embd % 256 != 0 || d.n_ff % 256 != 0) {
-        JINF_LOG("batch: n_embd %d and n_ff %d must be multiples of 256", d.n_embd, d.n_ff);
+    if (d.n_embd % 256 != 0 || d.n_ff % 256 != 0 || d.n_embd > 32768 || d.n_ff > 32768) {
+        JINF_LOG("batch: n_embd %d and n_ff %d must be multiples of 256, at most 32768", d.n_embd,
+                 d.n_ff);
         return JINF_HIP_ERR_INVALID;
     }
     jinf_hip_batch* b = new (std::nothrow) jinf_hip_batch();
