@@ -179,6 +179,33 @@ __device__ __forceinline__ float exp_neg(float a) {
     return a < -104.0f ? 0.0f : r;
 }
 
+// fp64 wave sum, same DPP pattern as wave_sum_f32 (both halves of each value
+// moved by DPP; the four row sums added in row order).  Every lane gets the
+// result.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t u = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+    return __longlong_as_double((int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v += dpp_f64<0xB1>(v);
+    v += dpp_f64<0x4E>(v);
+    v += dpp_f64<0x124>(v);
+    v += dpp_f64<0x128>(v);
+    double r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint64_t u = __double_as_longlong(v);
+        const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)u, 16 * i);
+        const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 16 * i);
+        r[i] = __longlong_as_double((int64_t)(((uint64_t)hi << 32) | lo));
+    }
+    return ((r[0] + r[1]) + r[2]) + r[3];
+}
+
 // fp32 wave max, same DPP pattern as wave_sum_f32 (every lane gets the result).
 __device__ __forceinline__ float wave_max_f32(float v) {
     v = fmaxf(v, dpp_f32<0xB1>(v));

@@ -13,16 +13,21 @@
 // registers (kSmCPT float4 chunks per thread, so up to 32 KiB per row with
 // 256 lanes), exponentiated once, and written once: one HBM read and one write
 // per element, against the reference's three reads and two exp evaluations.
-// Max and sum are wave64 butterflies plus one LDS exchange; each aligned group
-// of 4 exponentials is summed in fp32 and the group sums in fp64.  Chunks past
-// the row's live length do no arithmetic (whole waves branch over them), so
-// the VALU cost follows the live length, not the padded stride.
-// Measured alternatives at config 5 (4096 rows, stride 8192, random len), all
-// slower than this 256-lane row-per-workgroup form (30 us): longest-first row
-// order (36 us), one wave per row (57 us), length-scaled waves per row with
-// several short rows per workgroup (35 us), loading the first chunk before
-// the length is known (no change).  At uniform 8192-long rows it reaches 74% of
-// 8 TB/s (a plain copy: 75%); ragged rows lose to the per-row latency chain.
+// Every chunk's load is issued before any arithmetic, so a row's loads are in
+// flight together.  Max and sum are DPP wave reductions plus one LDS exchange
+// and one barrier each; each aligned group of 4 exponentials is summed in fp32
+// and the group sums in fp64.  Chunks past the row's live length do no
+// arithmetic (whole waves branch over them), so the VALU cost follows the live
+// length, not the padded stride.
+// Measured at config 5 (4096 rows, stride 8192, random len): this form 26 us
+// (63% of 8 TB/s); the earlier one with loads and maxima interleaved per chunk
+// and two-barrier shuffle reductions 30 us.  Also slower: two rows per
+// workgroup sharing the barriers (31 us), 2 or 16 chunks per lane instead of 8
+// (4 equal), longest-first row order, one wave per row, length-scaled waves
+// per row with several short rows per workgroup, loading the first chunk
+// before the length is known.  At uniform 8192-long rows the earlier form
+// reached 74% of 8 TB/s (a plain copy: 75%); ragged rows lose to the per-row
+// latency chain.
 // Rows longer than the register capacity (or unaligned rows) take a loop
 // kernel that reads the row three times (max, sum, write) like the reference.
 #include <math.h>
@@ -43,70 +48,116 @@ __device__ __forceinline__ int live_len(const int32_t* lens, int rows_per_len, i
     return L > n_cols ? n_cols : L;
 }
 
-template <int CPT = kSmCPT>
+// RPW rows per workgroup (rows RPW b .. RPW b + RPW - 1; the launches use 1):
+// their loads are in flight together and their reductions share the
+// workgroup's barriers.
+template <int CPT = kSmCPT, int RPW = 1>
 __global__ __launch_bounds__(1024) void softmax_vec_kernel(
-    float* out, int ld_out, const float* in, int ld_in, int n_cols, const int32_t* lens,
-    int rows_per_len, float scale) {
+    float* out, int ld_out, const float* in, int ld_in, int n_rows, int n_cols,
+    const int32_t* lens, int rows_per_len, float scale) {
 #pragma clang fp contract(off)
-    __shared__ float redf[16];
-    __shared__ double redd[16];
-    const int64_t row = blockIdx.x;
-    const int L = live_len(lens, rows_per_len, n_cols, row);
-    if (L == 0) return;  // uniform over the workgroup
-    const float* x = in + row * ld_in;
-    float* y = out + row * ld_out;
+    __shared__ float redf[16 * RPW];
+    __shared__ double redd[16 * RPW];
     const int bs = blockDim.x;
-    const int nfull = L >> 2;  // whole float4 chunks
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave, nw = bs / kWave;
     const float ninf = -INFINITY;
+    int L[RPW], nfull[RPW];
+    const float* x[RPW];
+    float* y[RPW];
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+        const int64_t row = (int64_t)blockIdx.x * RPW + q;
+        L[q] = row < n_rows ? live_len(lens, rows_per_len, n_cols, row) : 0;
+        nfull[q] = L[q] >> 2;  // whole float4 chunks
+        x[q] = in + row * ld_in;
+        y[q] = out + row * ld_out;
+    }
 
     // Chunks at or past L do no arithmetic: whole waves skip them.
-    float v[CPT][4];
-    float mx = ninf;
+    float v[RPW][CPT][4];
+    float mx[RPW];
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-        const int c = threadIdx.x + j * bs;
-        if (c < nfull) {
-            Act<float>::load(x + 4 * c, v[j]);
-        } else {
+    for (int q = 0; q < RPW; ++q) {
+        mx[q] = ninf;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[j][e] = (4 * c + e < L) ? x[4 * c + e] : ninf;
-        }
-        if (4 * c < L) {
+        for (int j = 0; j < CPT; ++j) {
+            const int c = threadIdx.x + j * bs;
+            if (c < nfull[q]) {
+                Act<float>::load(x[q] + 4 * c, v[q][j]);
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v[j][e] = v[j][e] * scale;  // -inf * scale stays -inf for scale > 0
-                mx = fmaxf(mx, v[j][e]);
+                for (int e = 0; e < 4; ++e) v[q][j][e] = (4 * c + e < L[q]) ? x[q][4 * c + e] : ninf;
             }
         }
     }
-    mx = block_max(mx, redf);
-    double sum = 0.0;
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-        const int c = threadIdx.x + j * bs;
-        if (4 * c < L) {
-            float part = 0.0f;
+    for (int q = 0; q < RPW; ++q)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float ex = 4 * c + e < L ? exp_neg(v[j][e] - mx) : 0.0f;
-                v[j][e] = ex;
-                part += ex;
+        for (int j = 0; j < CPT; ++j) {
+            const int c = threadIdx.x + j * bs;
+            if (4 * c < L[q]) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[q][j][e] = v[q][j][e] * scale;  // -inf * scale stays -inf for scale > 0
+                    mx[q] = fmaxf(mx[q], v[q][j][e]);
+                }
             }
-            sum += (double)part;
+        }
+    // one exchange for every row's maximum
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+        mx[q] = wave_max_f32(mx[q]);
+        if (lane == 0) redf[q * 16 + wid] = mx[q];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+        float m = redf[q * 16];
+        for (int i = 1; i < nw; ++i) m = fmaxf(m, redf[q * 16 + i]);
+        mx[q] = m;
+    }
+    double sum[RPW];
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+        sum[q] = 0.0;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int c = threadIdx.x + j * bs;
+            if (4 * c < L[q]) {
+                float part = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float ex = 4 * c + e < L[q] ? exp_neg(v[q][j][e] - mx[q]) : 0.0f;
+                    v[q][j][e] = ex;
+                    part += ex;
+                }
+                sum[q] += (double)part;
+            }
         }
     }
-    sum = block_sum(sum, redd);
-    const float inv = 1.0f / (float)sum;
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-        const int c = threadIdx.x + j * bs;
-        if (c < nfull) {
-            const float o[4] = {v[j][0] * inv, v[j][1] * inv, v[j][2] * inv, v[j][3] * inv};
-            Act<float>::store(y + 4 * c, o);
-        } else if (4 * c < L) {
+    for (int q = 0; q < RPW; ++q) {
+        sum[q] = wave_sum_f64(sum[q]);
+        if (lane == 0) redd[q * 16 + wid] = sum[q];
+    }
+    __syncthreads();
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (4 * c + e < L) y[4 * c + e] = v[j][e] * inv;
+    for (int q = 0; q < RPW; ++q) {
+        double t = redd[q * 16];
+        for (int i = 1; i < nw; ++i) t += redd[q * 16 + i];
+        const float inv = 1.0f / (float)t;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int c = threadIdx.x + j * bs;
+            if (c < nfull[q]) {
+                const float o[4] = {v[q][j][0] * inv, v[q][j][1] * inv, v[q][j][2] * inv,
+                                    v[q][j][3] * inv};
+                Act<float>::store(y[q] + 4 * c, o);
+            } else if (4 * c < L[q]) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (4 * c + e < L[q]) y[q][4 * c + e] = v[q][j][e] * inv;
+            }
         }
     }
 }
@@ -148,8 +199,8 @@ static int softmax_dispatch(float* out, int ld_out, const float* in, int ld_in, 
     if (bs < 256 && n_cols > 256) bs = 256;
     if (bs < kWave) bs = kWave;
     if (vec && bs <= 1024)
-        return launch(softmax_vec_kernel<kSmCPT>, dim3(n_rows), dim3(bs), 0, stream, out, ld_out,
-                      in, ld_in, n_cols, lens, rows_per_len, scale);
+        return launch(softmax_vec_kernel<kSmCPT, 1>, dim3(n_rows), dim3(bs), 0, stream, out,
+                      ld_out, in, ld_in, n_rows, n_cols, lens, rows_per_len, scale);
     const int lbs = n_cols >= 1024 ? 1024 : round_up(n_cols, kWave);
     return launch(softmax_loop_kernel, dim3(n_rows), dim3(lbs), 0, stream, out, ld_out, in,
                   ld_in, n_cols, lens, rows_per_len, scale);
