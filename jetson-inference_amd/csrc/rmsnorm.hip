@@ -121,7 +121,12 @@ __global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(
             for (int e = 0; e < E; ++e) ss = fma((double)h[e], (double)h[e], ss);
         }
     }
-    ss = block_sum(ss, red);
+    // DPP wave sums, one LDS exchange and one barrier (`red` is not reused)
+    ss = wave_sum_f64(ss);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
+    __syncthreads();
+    ss = red[0];
+    for (int i = 1; i < bs / kWave; ++i) ss += red[i];
     const float rs = rms_scale(ss, n, eps);
     TA* y = out + row * ld_out;
 #pragma unroll
