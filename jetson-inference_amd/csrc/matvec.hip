@@ -366,10 +366,12 @@ __device__ __forceinline__ void cache_store(void* c, int64_t i, float a, float b
     }
 }
 
-// Finished values v[0..R) of group g (one lane).
+// Finished values v[0..R) of group g (one lane).  rcs: the workgroup's
+// (cos, sin) table for the position (kEpiQKV; NULL: computed here).
 template <int QT, int EPI, bool WIDE = false>
 __device__ __forceinline__ void mv_epilogue(const MvJob& j, const MvTheta<EPI>& th, int g,
-                                            float (&v)[MvGroup<QT, EPI, WIDE>::R]) {
+                                            float (&v)[MvGroup<QT, EPI, WIDE>::R],
+                                            const float2* rcs = nullptr) {
     constexpr int R = MvGroup<QT, EPI, WIDE>::R;
     if constexpr (EPI == kEpiStore) {
 #pragma unroll
@@ -389,7 +391,8 @@ __device__ __forceinline__ void mv_epilogue(const MvJob& j, const MvTheta<EPI>& 
         const int pos = j.pos[0];
         float a = v[0], b = v[1];
         if (s < 2) {
-            const float2 cs = rope_cs(pos, th.t[(local % j.head_dim) / 2]);
+            const int i = (local % j.head_dim) / 2;
+            const float2 cs = rcs ? rcs[i] : rope_cs(pos, th.t[i]);
             rot(a, b, cs.x, cs.y);
         }
         if (s == 0) {
@@ -461,6 +464,14 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
     uint4 bufB[R][CPL];
     if (g0 < n_groups) fetch(g0, t0, bufA);
 
+    // RoPE: the position's (cos, sin) for every pair index, computed once per
+    // workgroup (one fp64 sincos per lane) instead of once per finished pair
+    // in the finishing lane
+    __shared__ float2 rcs[EPI == kEpiQKV ? kRopeMaxHalf : 1];
+    if constexpr (EPI == kEpiQKV) {
+        if (threadIdx.x < job.head_dim / 2) rcs[threadIdx.x] = rope_cs(job.pos[0], th.t[threadIdx.x]);
+    }
+
     // Stage x (zero past the last value) while the first weights are in flight.
     const float4* x4 = reinterpret_cast<const float4*>(job.x);
     const int nx4 = nb * (F::kElems / 4);
@@ -475,7 +486,12 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
             ss = fma((double)v.z, (double)v.z, ss);
             ss = fma((double)v.w, (double)v.w, ss);
         }
-        ss = block_sum(ss, red);
+        // DPP wave sums, one LDS exchange and one barrier (`red` is not reused)
+        ss = wave_sum_f64(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        ss = red[0];
+        for (int i = 1; i < waves; ++i) ss += red[i];
         const float rs = rms_scale(ss, nb * F::kElems, job.eps);
         // each thread rescales the slots it wrote
         for (int f = threadIdx.x; f < nx4; f += blockDim.x) {
@@ -565,7 +581,7 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
                 v[r] = wave_sum_f32(acc[r]);
                 acc[r] = 0.0f;
             }
-            if (lane == 0) mv_epilogue<QT, EPI, !ONE_TILE>(job, th, g, v);
+            if (lane == 0) mv_epilogue<QT, EPI, !ONE_TILE>(job, th, g, v, rcs);
         }
     };
 
