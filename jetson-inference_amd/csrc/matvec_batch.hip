@@ -361,12 +361,11 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
 // NBUF - 1 slabs ahead of the matrix-core work.
 // Workgroup shapes: NT 32-row tiles (ROWS = 32 NT weight rows) and WV waves;
 // the 16 k-steps of a slab are split into KSW parts, wave w taking k-part
-// w / (WV / KSW) of TPW = NT KSW / WV tiles.
-//   narrow: NT 2, WV 4, KSW 4 -- 64 rows, each wave both tiles over 4 k-steps
-//           (few rows: many workgroups, one LDS slot, three per CU);
-//   wide:   NT 8 (Q4_0, Q4_K) or 4 (Q8_0, Q6_K), WV 8 -- 256 / 128 rows that
-//           share each x record, two LDS slots so that the next slab's
-//           weights are in flight during the matrix-core work.
+// w / (WV / KSW) of TPW = NT KSW / WV tiles.  The launches use NT 2, WV 4,
+// KSW 4: 64 rows, each wave both tiles over 4 k-steps, one LDS slot, up to
+// three workgroups per CU.  (8-wave shapes over 128 or 256 rows sharing each
+// x record, with two slots so that the next slab's weights are in flight
+// during the matrix-core work, measured slower.)
 // LDS slot: the weight chunks (NWI KiB), then the x record (NXI KiB), filled
 // by 1 KiB direct-to-LDS instructions dealt round-robin to the waves.
 template <int QT, int NT> constexpr int mb_nwi() { return (32 * NT * mb_nch<QT>() * 16 + 1023) / 1024; }
@@ -798,9 +797,6 @@ struct MbShape {
 };
 
 constexpr MbShape kMbNarrow{2, 4, 4};
-MbShape mb_wide(int qtype) {
-    return (qtype == kQ8_0 || qtype == kQ6_K) ? MbShape{4, 8, 2} : MbShape{8, 8, 1};
-}
 
 // Column splits: as many as keep the workgroups at most kMbSplitTarget
 // (rounded down).  Each split adds its partials' device-coherent traffic and
@@ -818,13 +814,12 @@ int mb_split(int n_groups, int n_slabs, int* slabs_per_split) {
     return (n_slabs + per - 1) / per;
 }
 
-// Wide workgroups when there are enough of them to fill the GPU with few
-// column splits (each split adds its partials' traffic).
-MbShape mb_shape(int qtype, int epi, int out_rows, int n_slabs) {
-    const MbShape w = mb_wide(qtype);
-    const int groups = (out_rows + w.rows_per_group(epi) - 1) / w.rows_per_group(epi);
-    return groups >= 64 && (int64_t)groups * n_slabs >= 3 * 256 ? w : kMbNarrow;
-}
+// The 64-row shape for every matrix: measured at 32 sequences on the
+// Llama-3-8B step, 8-wave workgroups over 256 (Q4_0) or 128 (Q6_K) rows with
+// two LDS slots were slower on the FFN and output matrices (step 5.13 against
+// 4.71 ms; 28672 x 4096 alone 56.2 against 44.9 us), and no faster at 8 or 64
+// sequences.
+MbShape mb_shape() { return kMbNarrow; }
 
 size_t mb_ctr_bytes(int n_groups) { return ((size_t)n_groups * 4 + 255) / 256 * 256; }
 
@@ -852,11 +847,8 @@ int mb_launch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void*
                           j.n_batch, j.n_slabs * kMbCols, norm_w, norm_f16, eps,
                           const_cast<uint8_t*>(j.xrec));
     if (rc != JINF_HIP_OK) return rc;
-    if (sh.wv == 4) return mb_launch_shape<QT, MT, EPI, 2, 4, 4>(j, th, stream);
-    if constexpr (QT == kQ8_0 || QT == kQ6_K)
-        return mb_launch_shape<QT, MT, EPI, 4, 8, 2>(j, th, stream);
-    else
-        return mb_launch_shape<QT, MT, EPI, 8, 8, 1>(j, th, stream);
+    (void)sh;  // kMbNarrow
+    return mb_launch_shape<QT, MT, EPI, 2, 4, 4>(j, th, stream);
 }
 
 // Sequences 32 .. n_batch - 1 of a job as a job of their own.
@@ -881,9 +873,7 @@ template <int QT, int EPI>
 int mb_dispatch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void* norm_w,
                   int norm_f16, float eps, hipStream_t stream) {
     if (j.n_batch <= 32) return mb_launch_t<QT, 1, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
-    const bool fits = sh.wv == 4 ? mb_slot<QT, 2, 2>() <= kMbLdsBudget
-                                 : (QT == kQ8_0 || QT == kQ6_K) ? mb_slot<QT, 2, 4>() <= kMbLdsBudget
-                                                                : mb_slot<QT, 2, 8>() <= kMbLdsBudget;
+    const bool fits = mb_slot<QT, 2, 2>() <= kMbLdsBudget;
     if (fits) return mb_launch_t<QT, 2, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
     MbJob lo = j;
     lo.n_batch = 32;
@@ -930,7 +920,7 @@ int mb_prepare(MbJob& j, MbShape& sh, int qtype, int epi, int rows, int cols, in
     if (mb_row_bytes(qtype, cols, &j.row_bytes) != JINF_HIP_OK) return JINF_HIP_ERR_INVALID;
     j.rows = rows;
     j.n_slabs = cols / kMbCols;
-    sh = mb_shape(qtype, epi, rows, j.n_slabs);
+    sh = mb_shape();
     j.n_groups = (rows + sh.rows_per_group(epi) - 1) / sh.rows_per_group(epi);
     const int mt = n_batch > 32 ? 2 : 1;
     if (!ws || !aligned(ws, 256) || ws_bytes < mb_ws_bytes(sh, epi, rows, j.n_slabs, mt)) {
@@ -974,11 +964,10 @@ size_t matvec_batch_ws_bytes(int rows, int cols, int n_batch) {
         return 0;
     const int mt = n_batch > 32 ? 2 : 1, n_slabs = cols / kMbCols;
     size_t most = 0;
-    for (int qtype : {kQ4_0, kQ8_0})
-        for (int epi : {kMbEpiStore, kMbEpiSwiGLU}) {
-            const size_t b = mb_ws_bytes(mb_shape(qtype, epi, rows, n_slabs), epi, rows, n_slabs, mt);
-            most = b > most ? b : most;
-        }
+    for (int epi : {kMbEpiStore, kMbEpiSwiGLU}) {
+        const size_t b = mb_ws_bytes(mb_shape(), epi, rows, n_slabs, mt);
+        most = b > most ? b : most;
+    }
     return most;
 }
 

@@ -61,8 +61,8 @@ def batch_x(r, n_batch, cols):
     return X
 
 
-# (rows, cols): 8B q/o, k/v, a ragged row count, a many-slab shape (all
-# 64-row workgroups), and an FFN-sized matrix (256 / 128-row workgroups)
+# (rows, cols): 8B q/o, k/v, a ragged row count, a many-slab shape, an
+# FFN-sized matrix and a ragged FFN-sized one (few column splits)
 SHAPES = [(4096, 4096), (1024, 4096), (300, 2048), (64, 14336), (14336, 4096), (12300, 4096)]
 BATCHES = [1, 13, 32, 64]
 
