@@ -159,6 +159,21 @@ int  jinf_hip_batch_n_past(const jinf_hip_batch* b, int seq);
  * [-1, n_vocab) or a token for a sequence whose context is full. */
 int  jinf_hip_batch_forward(jinf_hip_batch* b, const int32_t* tokens, const float** logits);
 
+/* Prompt of sequence seq: decodes its n_tokens ids (each in [0, n_vocab))
+ * in chunks of up to n_seq tokens per step, every GEMV running on a chunk's
+ * tokens at once and token i attending to the sequence's positions up to its
+ * own, so the sequence ends where n_tokens forward steps of its own would
+ * leave it (position advanced by n_tokens, next token the last token's
+ * argmax); other sequences are untouched.  The last chunk's per-token logits
+ * occupy rows 0 .. m - 1 of the batch's logits (the last token's at row
+ * (n_tokens - 1) mod n_seq); *logits (may be NULL) receives the device
+ * pointer of that row.  Status 5 when the prompt does not fit the sequence's
+ * context or an id is outside [0, n_vocab).  The reference feeds a prompt
+ * one token at a time (src/engine.cpp:684-760); per token the arithmetic is
+ * that loop's. */
+int  jinf_hip_batch_prefill(jinf_hip_batch* b, int seq, const int32_t* tokens, int n_tokens,
+                            const float** logits);
+
 /* Greedy generation for `steps` steps (jinf_hip_engine_generate per
  * sequence): at each step every sequence emits its last argmax (the one
  * computed by the previous forward or generate step) into output[step *

@@ -238,7 +238,9 @@ int jinf_rmsnorm_swiglu_matvec_batch(const void* w_gate, const void* w_up, int q
  * q + b * ld_q, its K / V rows to k_cache / v_cache + b * ld_seq +
  * positions[b] * n_heads_kv * head_dim (elements of kv_type), RoPE at
  * positions[b]; a position outside [0, max_ctx) skips that sequence's cache
- * stores.  cols = n_embd. */
+ * stores.  ld_seq is at least max_ctx * n_heads_kv * head_dim, or 0: every
+ * row then writes into the same cache (the tokens of one prompt; their
+ * positions must differ).  cols = n_embd. */
 int jinf_rmsnorm_qkv_rope_batch(const void* w_q, const void* w_k, const void* w_v, int qtype,
                                 const float* h, int ld_h, const void* norm_w, int norm_type,
                                 float eps, int cols, float* q, int ld_q, void* k_cache,
@@ -265,7 +267,9 @@ int jinf_dequant_rows(void* out, int ld_out, const void* table, int qtype, int n
  * over t < lens[s] (clamped to [0, max_ctx]); a sequence with no position
  * gets zeros.  q and out are fp32 with row strides ld_q, ld_out (elements).
  * Cache element (s, t, kv head j, dim d) is at s*ld_seq + t*ld_pos + j*hd + d
- * in k_cache / v_cache, of kv_type JINF_HIP_F32 or JINF_HIP_F16.
+ * in k_cache / v_cache, of kv_type JINF_HIP_F32 or JINF_HIP_F16; ld_seq is at
+ * least max_ctx * ld_pos when n_seq > 1, or 0 (every row reads the same
+ * cache: the tokens of one prompt, each with its own length).
  * scale = 0 means 1/sqrt(head_dim); otherwise finite and > 0.  lens is a
  * device array of n_seq int32.  Fast path: head_dim 64 or 128, caches, q
  * and strides 16-byte aligned; an fp16 cache then runs on the matrix cores

@@ -842,7 +842,8 @@ extern "C" int jinf_attention_decode(float* out, int ld_out, const float* q, int
                                      int n_heads_kv, float scale, void* workspace,
                                      size_t workspace_bytes, hipStream_t stream) {
     if ((!lens && n_seq > 0) || max_ctx < 0) return JINF_HIP_ERR_INVALID;
-    if (n_seq > 1 && ld_seq < (int64_t)max_ctx * ld_pos) return JINF_HIP_ERR_INVALID;
+    // ld_seq 0: every sequence reads the same cache (the tokens of one prompt)
+    if (n_seq > 1 && ld_seq != 0 && ld_seq < (int64_t)max_ctx * ld_pos) return JINF_HIP_ERR_INVALID;
     if (workspace && !jinf::aligned(workspace, 4)) return JINF_HIP_ERR_INVALID;
     if (scale == 0.0f && head_dim > 0) scale = jinf::inv_sqrt_hd(head_dim);
     return jinf::attention_decode(out, ld_out, q, ld_q, k_cache, v_cache, kv_type, ld_pos, ld_seq,

@@ -120,6 +120,22 @@ __global__ __launch_bounds__(kArgThreads) void bat_argmax_end_kernel(
     if (s == gridDim.x - 1) st[kStep] = st[kStep] + 1;
 }
 
+// End of a prefill chunk (one workgroup): the argmax of the chunk's last
+// token (same rules) becomes sequence seq's next token, and its position
+// moves to new_pos.
+__global__ __launch_bounds__(kArgThreads) void bat_prefill_end_kernel(
+    const float* __restrict__ logits, int n, const float* __restrict__ pv,
+    const int* __restrict__ pi, int parts, int32_t* __restrict__ pos,
+    int32_t* __restrict__ cur, int new_pos) {
+    float bv = -INFINITY;
+    int bi = n;
+    for (int k = threadIdx.x; k < parts; k += kArgThreads) take(bv, bi, pv[k], pi[k]);
+    block_best(bv, bi);
+    if (threadIdx.x != 0) return;
+    *pos = new_pos;
+    *cur = (__builtin_isnan(logits[0]) || bi >= n) ? 0 : bi;
+}
+
 size_t up256(size_t x) { return (x + 255) / 256 * 256; }
 
 int hip_rc(hipError_t e, const char* what) {
@@ -155,7 +171,7 @@ struct jinf_hip_batch {
     size_t mws_bytes = 0;
     void* aws = nullptr;  // attention workspace
     size_t aws_bytes = 0;
-    int32_t* h_io = nullptr;  // pinned: n_seq tokens, then 16 words
+    int32_t* h_io = nullptr;  // pinned: n_seq tokens, 16 words, 3 n_seq prefill row words
     std::vector<int> h_pos;   // host copy of the positions
     hipStream_t stream = nullptr;
     // captured steps, one per attention bound (a power of two >= 64, at most
@@ -168,9 +184,9 @@ struct jinf_hip_batch {
 
 namespace {
 
-int bat_embed(jinf_hip_batch* b) {
+int bat_embed(jinf_hip_batch* b, int rows) {
     const jinf_hip_engine_desc& d = *b->d;
-    const dim3 grid((d.n_embd + 255) / 256, b->n_seq);
+    const dim3 grid((d.n_embd + 255) / 256, rows);
     if (d.token_embd_type == JINF_HIP_F32)
         return launch(bat_embed_dense_kernel<float>, grid, dim3(256), 0, b->stream, b->hidden,
                       static_cast<const float*>(d.token_embd), b->acts, d.n_vocab, d.n_embd);
@@ -178,10 +194,11 @@ int bat_embed(jinf_hip_batch* b) {
         return launch(bat_embed_dense_kernel<uint16_t>, grid, dim3(256), 0, b->stream, b->hidden,
                       static_cast<const uint16_t*>(d.token_embd), b->acts, d.n_vocab, d.n_embd);
     return jinf_dequant_rows(b->hidden, d.n_embd, d.token_embd, d.token_embd_type, d.n_vocab,
-                             d.n_embd, b->acts, b->n_seq, JINF_HIP_F32, b->stream);
+                             d.n_embd, b->acts, rows, JINF_HIP_F32, b->stream);
 }
 
-int bat_qkv(jinf_hip_batch* b, const jinf_hip_layer_weights& w, void* kc, void* vc) {
+int bat_qkv(jinf_hip_batch* b, const jinf_hip_layer_weights& w, void* kc, void* vc, int rows,
+            int64_t ld_seq) {
     const jinf_hip_engine_desc& d = *b->d;
     const void* W[3] = {w.attn_q, w.attn_k, w.attn_v};
     const int T[3] = {w.attn_q_type, w.attn_k_type, w.attn_v_type};
@@ -196,32 +213,40 @@ int bat_qkv(jinf_hip_batch* b, const jinf_hip_layer_weights& w, void* kc, void* 
             }
         BAT_TRY(jinf_rmsnorm_qkv_rope_batch(
             p[0], p[1], p[2], T[i], b->hidden, d.n_embd, w.attn_norm, w.attn_norm_type,
-            d.rms_norm_eps, d.n_embd, b->q, b->q_dim, kc, vc, b->kv_type,
-            (int64_t)b->max_ctx * b->kv_dim, b->positions, b->max_ctx, b->head_dim, d.n_heads,
-            d.n_heads_kv, d.rope_freq_base, b->n_seq, b->mws, b->mws_bytes, b->stream));
+            d.rms_norm_eps, d.n_embd, b->q, b->q_dim, kc, vc, b->kv_type, ld_seq, b->positions,
+            b->max_ctx, b->head_dim, d.n_heads, d.n_heads_kv, d.rope_freq_base, rows, b->mws,
+            b->mws_bytes, b->stream));
     }
     return JINF_HIP_OK;
 }
 
-// One step for every sequence (src/engine.cpp:692-749 per sequence).
-int bat_enqueue_step(jinf_hip_batch* b) {
+// One step (src/engine.cpp:692-749 per row) over `rows` rows.  seq < 0: a
+// decode step, row s = sequence s (every sequence; tokens and positions from
+// the begin kernel).  seq >= 0: a prefill chunk, row i = prompt token i of
+// sequence seq (tokens, positions and lengths already in the row arrays);
+// the rows share the sequence's KV region (row stride 0), each writes its
+// own position's K / V rows and attends up to them.
+int bat_enqueue_rows(jinf_hip_batch* b, int rows, int seq, int new_pos) {
     const jinf_hip_engine_desc& d = *b->d;
     hipStream_t s = b->stream;
-    const int n = d.n_embd, nff = d.n_ff, ns = b->n_seq;
+    const int n = d.n_embd, nff = d.n_ff, ns = rows;
     const float eps = d.rms_norm_eps;
-    BAT_TRY(launch(bat_begin_kernel, dim3((ns + 255) / 256), dim3(256), 0, s, b->st, b->htok,
-                   b->cur, b->pos, b->acts, b->positions, b->lens, b->hist, b->hist_rows, ns,
-                   b->max_ctx));
-    BAT_TRY(bat_embed(b));
+    const bool prefill = seq >= 0;
+    const int64_t ld_seq = prefill ? 0 : (int64_t)b->max_ctx * b->kv_dim;
+    const size_t kv_off = prefill ? (size_t)seq * b->max_ctx * b->kv_dim * b->kv_es : 0;
+    if (!prefill)
+        BAT_TRY(launch(bat_begin_kernel, dim3((ns + 255) / 256), dim3(256), 0, s, b->st, b->htok,
+                       b->cur, b->pos, b->acts, b->positions, b->lens, b->hist, b->hist_rows, ns,
+                       b->max_ctx));
+    BAT_TRY(bat_embed(b, ns));
     for (int L = 0; L < d.n_layers; ++L) {
         const jinf_hip_layer_weights& w = d.layers[L];
-        char* kc = b->kv + (size_t)L * b->kv_layer_bytes;
-        char* vc = b->kv + (size_t)(d.n_layers + L) * b->kv_layer_bytes;
-        BAT_TRY(bat_qkv(b, w, kc, vc));
+        char* kc = b->kv + (size_t)L * b->kv_layer_bytes + kv_off;
+        char* vc = b->kv + (size_t)(d.n_layers + L) * b->kv_layer_bytes + kv_off;
+        BAT_TRY(bat_qkv(b, w, kc, vc, ns, ld_seq));
         BAT_TRY(jinf_attention_decode(b->attn, b->q_dim, b->q, b->q_dim, kc, vc, b->kv_type,
-                                      b->kv_dim, (int64_t)b->max_ctx * b->kv_dim, b->lens, ns,
-                                      b->bound, b->head_dim, d.n_heads, d.n_heads_kv, 0.0f,
-                                      b->aws, b->aws_bytes, s));
+                                      b->kv_dim, ld_seq, b->lens, ns, b->bound, b->head_dim,
+                                      d.n_heads, d.n_heads_kv, 0.0f, b->aws, b->aws_bytes, s));
         BAT_TRY(jinf_matvec_batch_add(w.attn_output, w.attn_output_type, b->attn, b->q_dim,
                                       b->hidden, n, n, b->q_dim, ns, b->mws, b->mws_bytes, s));
         if (w.ffn_gate_type == w.ffn_up_type) {
@@ -244,11 +269,20 @@ int bat_enqueue_step(jinf_hip_batch* b) {
     BAT_TRY(jinf_rmsnorm_matvec_batch(d.output, d.output_type, b->hidden, n, d.output_norm,
                                       d.output_norm_type, eps, b->logits, d.n_vocab, d.n_vocab, n,
                                       ns, b->mws, b->mws_bytes, s));
+    if (prefill) {
+        const float* last = b->logits + (int64_t)(ns - 1) * d.n_vocab;
+        BAT_TRY(launch(bat_argmax_part_kernel, dim3(b->arg_parts, 1), dim3(kArgThreads), 0, s,
+                       last, d.n_vocab, b->part_v, b->part_i));
+        return launch(bat_prefill_end_kernel, dim3(1), dim3(kArgThreads), 0, s, last, d.n_vocab,
+                      b->part_v, b->part_i, b->arg_parts, b->pos + seq, b->cur + seq, new_pos);
+    }
     BAT_TRY(launch(bat_argmax_part_kernel, dim3(b->arg_parts, ns), dim3(kArgThreads), 0, s,
                    b->logits, d.n_vocab, b->part_v, b->part_i));
     return launch(bat_argmax_end_kernel, dim3(ns), dim3(kArgThreads), 0, s, b->logits, d.n_vocab,
                   b->part_v, b->part_i, b->arg_parts, b->st, b->acts, b->pos, b->cur);
 }
+
+int bat_enqueue_step(jinf_hip_batch* b) { return bat_enqueue_rows(b, b->n_seq, -1, 0); }
 
 int bat_capture(jinf_hip_batch* b, hipGraphExec_t* out) {
     BAT_TRY(hip_rc(hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal),
@@ -392,7 +426,7 @@ extern "C" int jinf_hip_batch_create(jinf_hip_batch** out, const jinf_hip_engine
     const size_t kv_total = b->kv_layer_bytes * 2 * (size_t)d.n_layers;
     if (rc == JINF_HIP_OK && kv_total) rc = hip_rc(hipMalloc((void**)&b->kv, kv_total), "hipMalloc");
     if (rc == JINF_HIP_OK)
-        rc = hip_rc(hipHostMalloc((void**)&b->h_io, (ns + 16) * 4, hipHostMallocDefault),
+        rc = hip_rc(hipHostMalloc((void**)&b->h_io, (4 * ns + 16) * 4, hipHostMallocDefault),
                     "hipHostMalloc");
     if (rc != JINF_HIP_OK) {
         bat_release(b);
@@ -474,6 +508,50 @@ extern "C" int jinf_hip_batch_forward(jinf_hip_batch* b, const int32_t* tokens,
     for (int s = 0; s < b->n_seq; ++s)
         if (tokens[s] >= 0) ++b->h_pos[s];
     *logits = b->logits;
+    return JINF_HIP_OK;
+}
+
+extern "C" int jinf_hip_batch_prefill(jinf_hip_batch* b, int seq, const int32_t* tokens,
+                                      int n_tokens, const float** logits) {
+    if (!b || seq < 0 || seq >= b->n_seq || n_tokens < 0 || (n_tokens > 0 && !tokens))
+        return JINF_HIP_ERR_INVALID;
+    const jinf_hip_engine_desc& d = *b->d;
+    for (int i = 0; i < n_tokens; ++i)
+        if (tokens[i] < 0 || tokens[i] >= d.n_vocab) {
+            JINF_LOG("batch: token id %d outside [0, %d)", tokens[i], d.n_vocab);
+            return JINF_HIP_ERR_INVALID;
+        }
+    const int p0 = b->h_pos[seq];
+    if (n_tokens > b->max_ctx - p0) {
+        JINF_LOG("batch: %d prompt tokens do not fit sequence %d's context (%d of %d used)",
+                 n_tokens, seq, p0, b->max_ctx);
+        return JINF_HIP_ERR_INVALID;
+    }
+    int32_t* rw = b->h_io + b->n_seq + 16;  // tokens, positions, lengths of a chunk
+    int last = 0;
+    for (int c = 0; c < n_tokens; c += b->n_seq) {
+        const int m = n_tokens - c < b->n_seq ? n_tokens - c : b->n_seq;
+        for (int i = 0; i < m; ++i) {
+            rw[i] = tokens[c + i];
+            rw[b->n_seq + i] = p0 + c + i;
+            rw[2 * b->n_seq + i] = p0 + c + i + 1;
+        }
+        BAT_TRY(hip_rc(hipMemcpyAsync(b->acts, rw, (size_t)m * 4, hipMemcpyHostToDevice,
+                                      b->stream), "hipMemcpyAsync"));
+        BAT_TRY(hip_rc(hipMemcpyAsync(b->positions, rw + b->n_seq, (size_t)m * 4,
+                                      hipMemcpyHostToDevice, b->stream), "hipMemcpyAsync"));
+        BAT_TRY(hip_rc(hipMemcpyAsync(b->lens, rw + 2 * b->n_seq, (size_t)m * 4,
+                                      hipMemcpyHostToDevice, b->stream), "hipMemcpyAsync"));
+        b->bound = bat_bound(b, p0 + c + m);
+        const int rc = bat_enqueue_rows(b, m, seq, p0 + c + m);
+        // the pinned rows are rewritten for the next chunk: wait for this one
+        const int sc = hip_rc(hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+        if (rc != JINF_HIP_OK) return rc;
+        if (sc != JINF_HIP_OK) return sc;
+        b->h_pos[seq] = p0 + c + m;
+        last = m - 1;
+    }
+    if (logits) *logits = b->logits + (int64_t)last * d.n_vocab;
     return JINF_HIP_OK;
 }
 

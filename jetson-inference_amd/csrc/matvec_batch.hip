@@ -1069,7 +1069,10 @@ extern "C" int jinf_rmsnorm_qkv_rope_batch(const void* wq, const void* wk, const
     if ((wk && !k_cache) || (wv && !v_cache) || (wq && (!q || ld_q < qd)))
         return JINF_HIP_ERR_INVALID;
     if (kv_type != JINF_HIP_F32 && kv_type != JINF_HIP_F16) return JINF_HIP_ERR_INVALID;
-    if ((wk || wv) && (max_ctx <= 0 || ld_seq < (int64_t)max_ctx * kvd)) return JINF_HIP_ERR_INVALID;
+    // ld_seq 0: every row writes into the same cache (the tokens of one
+    // prompt, at distinct positions)
+    if ((wk || wv) && (max_ctx <= 0 || ld_seq < 0 || (ld_seq != 0 && ld_seq < (int64_t)max_ctx * kvd)))
+        return JINF_HIP_ERR_INVALID;
     MbJob j{};
     MbShape sh;
     int f16 = 0;

@@ -125,6 +125,7 @@ SIGNATURES = {
     "jinf_hip_batch_reset": (_I, [_P, _I]),
     "jinf_hip_batch_n_past": (_I, [_P, _I]),
     "jinf_hip_batch_forward": (_I, [_P, _P, ctypes.POINTER(_P)]),
+    "jinf_hip_batch_prefill": (_I, [_P, _I, _P, _I, ctypes.POINTER(_P)]),
     "jinf_hip_batch_generate": (_I, [_P, _P, _I]),
     "jinf_hip_batch_copy_logits": (_I, [_P, _P]),
     "jinf_hip_batch_use_graph": (_I, [_P, _I]),

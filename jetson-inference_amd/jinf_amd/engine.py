@@ -228,6 +228,18 @@ class Batch:
                lib().jinf_hip_batch_forward(self._h, t.ctypes.data, ctypes.byref(p)))
         return p.value
 
+    def prefill(self, seq, tokens):
+        """Sequence seq's prompt in chunks of up to n_seq tokens per step;
+        returns the last token's logits, fp32 [n_vocab] (host copy)."""
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(-1))
+        p = ctypes.c_void_p()
+        _check("jinf_hip_batch_prefill",
+               lib().jinf_hip_batch_prefill(self._h, int(seq), t.ctypes.data, int(t.size),
+                                            ctypes.byref(p)))
+        if t.size == 0:
+            return None
+        return self.logits()[(t.size - 1) % self.n_seq].copy()
+
     def logits(self):
         """The last step's logits, fp32 [n_seq, n_vocab] (host copy)."""
         out = np.empty((self.n_seq, self.n_vocab), np.float32)

@@ -203,3 +203,54 @@ def test_batch_rejects_shapes(dev):
         assert ex.value.status == 5
         with pytest.raises(EngineError):
             Batch(e, 65, 8, mu.F16)
+
+
+@pytest.mark.parametrize("kv_type", [mu.F32, mu.F16], ids=["kv-f32", "kv-f16"])
+@pytest.mark.parametrize("name", ["mixed", "hd128-gqa4-f16embd"])
+def test_prefill_matches_oracle_and_continues(dev, name, kv_type):
+    """A prompt through prefill (chunks of n_seq tokens sharing one KV region)
+    equals the oracle's token-by-token loop, leaves the sequence where that
+    loop would, and does not touch the other sequences."""
+    n_seq, max_ctx = 4, 24
+    say(f"batch prefill {name} kv={'f16' if kv_type else 'f32'}")
+    hp, W = mu.tiny_model(seed=61, n_vocab=350, **MODELS[name])
+    tol = TOL_F16_KV if kv_type == mu.F16 else TOL
+    r = np.random.default_rng(62)
+    prompt = r.integers(0, hp["n_vocab"], size=11).astype(np.int32)  # chunks 4, 4, 3
+    ref = oeng.Decoder(hp, W, max_context=max_ctx, kv_type=kv_type)
+    for t in prompt:
+        want = ref.step(int(t))
+    other = oeng.Decoder(hp, W, max_context=max_ctx, kv_type=kv_type)
+    with Engine(hp, mu.to_device(W), 8, kv_type) as e, Batch(e, n_seq, max_ctx, kv_type) as b:
+        b.forward([5, -1, -1, -1])  # sequence 0 has one token already
+        other.step(5)
+        got = b.prefill(2, prompt)
+        compare(got, want, "prefill last token", tol)
+        assert [b.n_past(s) for s in range(n_seq)] == [1, 0, len(prompt), 0]
+        # the next steps continue both sequences from where they are
+        for k, (t0, t2) in enumerate([(7, 9), (11, 13)]):
+            b.forward([t0, -1, t2, -1])
+            lg = b.logits()
+            compare(lg[0], other.step(t0), f"step {k} seq 0", tol)
+            compare(lg[2], ref.step(t2), f"step {k} seq 2", tol)
+        # greedy generation starts from the prompt's own argmax
+        first = oeng.first_argmax(lg[2])
+        out = b.generate(1)
+        assert out[0, 2] == first
+
+
+def test_prefill_argmax_and_errors(dev):
+    hp, W = mu.tiny_model(seed=63, n_vocab=300)
+    with Engine(hp, mu.to_device(W), 8, mu.F16) as e, Batch(e, 3, 10, mu.F16) as b:
+        got = b.prefill(1, [3, 4, 5, 6, 7])
+        out = b.generate(1)
+        assert out[0, 1] == oeng.first_argmax(got)
+        assert out[0, 0] == -1 and out[0, 2] == -1  # no token yet: idle
+        with pytest.raises(EngineError) as ex:
+            b.prefill(1, [1] * 5)  # 6 of 10 used: 5 more do not fit
+        assert ex.value.status == 5
+        with pytest.raises(EngineError):
+            b.prefill(0, [300])  # id outside the vocabulary
+        with pytest.raises(EngineError):
+            b.prefill(3, [1])  # no such sequence
+        assert b.prefill(0, []) is None and b.n_past(0) == 0
