@@ -440,6 +440,27 @@ def batch_bench(args, torch, jinf_amd, spec):
     tok_s = emitted / dec_s
     log(f"{args.steps} steps x {n_seq} sequences: {ms_step:.3f} ms per step, "
         f"{tok_s:.0f} tokens/s")
+    # prompt processing: one sequence's 512-token prompt through
+    # jinf_hip_batch_prefill (chunks of n_seq tokens per step), after one
+    # untimed run
+    import ctypes
+    import numpy as np
+    n_pf = min(512, max_ctx)
+    ids = np.ascontiguousarray(
+        np.random.default_rng(args.seed).integers(0, hp["n_vocab"], n_pf).astype(np.int32))
+    lptr = ctypes.c_void_p()
+    pf_s = None
+    for _ in range(2):
+        b.reset(0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        rc = jinf_amd.lib().jinf_hip_batch_prefill(b._h, 0, ids.ctypes.data, n_pf,
+                                                  ctypes.byref(lptr))
+        pf_s = time.perf_counter() - t0
+        if rc != 0:
+            raise SystemExit(f"jinf_hip_batch_prefill failed ({rc})")
+    log(f"prefill of {n_pf} tokens in chunks of {n_seq}: {pf_s * 1e3:.2f} ms, "
+        f"{n_pf / pf_s:.0f} tokens/s")
     b.close()
     e.close()
     cpu = None
@@ -475,6 +496,9 @@ def batch_bench(args, torch, jinf_amd, spec):
                            "graph replayed per step (jinf_hip_batch_generate)",
                    "tokens_per_s": round(tok_s, 1),
                    "prefill_6_steps_ms": round(prefill_s * 1e3, 3),
+                   "prompt_tokens": n_pf,
+                   "prompt_ms": round(pf_s * 1e3, 3),
+                   "prompt_tokens_per_s": round(n_pf / pf_s, 1),
                    "weight_bytes_per_step": wbytes,
                    "kv_bytes_per_step_mean": int(kv_bytes),
                    "context": [start_pos, start_pos + args.steps],
