@@ -254,3 +254,21 @@ def test_prefill_argmax_and_errors(dev):
         with pytest.raises(EngineError):
             b.prefill(3, [1])  # no such sequence
         assert b.prefill(0, []) is None and b.n_past(0) == 0
+
+
+def test_prefill_wide_chunks(dev):
+    """Chunks of more than 32 prompt tokens (the GEMVs' second token tile)."""
+    n_seq, max_ctx = 40, 64
+    hp, W = mu.tiny_model(seed=64, n_vocab=300)
+    prompt = np.random.default_rng(65).integers(0, hp["n_vocab"], size=45).astype(np.int32)
+    ref = oeng.Decoder(hp, W, max_context=max_ctx, kv_type=mu.F16)
+    for t in prompt:
+        want = ref.step(int(t))
+    with Engine(hp, mu.to_device(W), 8, mu.F16) as e, Batch(e, n_seq, max_ctx, mu.F16) as b:
+        got = b.prefill(7, prompt)  # chunks of 40 and 5 tokens
+        compare(got, want, "prefill last token", TOL_F16_KV)
+        assert b.n_past(7) == 45
+        row = np.full(n_seq, -1, np.int32)
+        row[7] = 3
+        b.forward(row)
+        compare(b.logits()[7], ref.step(3), "after prefill", TOL_F16_KV)
