@@ -21,19 +21,21 @@
 // The result equals the fp32 dot product up to the fp32 rounding of the sums
 // (the order differs from the reference's sequential sum).
 //
-// Data movement.  A workgroup (4 waves) owns 64 weight rows (two 32-row
-// tiles) and a range of 256-column slabs.  Per slab every lane copies its
-// share of the 64 rows' bytes (the aligned 16-byte chunks covering each row's
-// slab: with a 16-byte aligned matrix they start inside it and end before the
-// next 16-byte boundary past its last byte) and of
-// x into LDS, converting x to the scaled hi / lo halves on the way; the next
-// slab's loads are issued before the current slab is multiplied, so they are
-// in flight during the matrix-core work.  Wave w multiplies columns
-// 64 w .. 64 w + 63 of the slab for both row tiles.  Within a 16-column
-// k-step, lane l supplies token / row l % 32 and columns 8 (l / 32) .. + 7 in
-// the order (0, 4, 1, 5, 2, 6, 3, 7), the order in which four bytes of
-// packed 4-bit codes unpack into fp16 pairs with two masks; A uses the same
-// order, so each fragment is one 16-byte LDS read.
+// Data movement.  A preparation launch turns x (RMSNorm applied first when
+// the GEMV reads a normed input, exactly as jinf_rmsnorm_rows computes it)
+// into per-slab records of MFMA fragments (below).  A GEMV workgroup (4
+// waves) owns 64 weight rows (two 32-row tiles) and a range of 256-column
+// slabs.  Per slab its lanes copy, with direct-to-LDS loads, the 64 rows'
+// bytes (the aligned 16-byte chunks covering each row's slab: with a 16-byte
+// aligned matrix they start inside it and end before the next 16-byte
+// boundary past its last byte) and the slab's x record into the workgroup's
+// LDS slot; up to three workgroups per CU keep one slab each in flight while
+// the others multiply.  Wave w multiplies k-steps 4 w .. 4 w + 3 of the slab
+// for both row tiles, and the four waves' sums are added in LDS at the end.
+// Within a 16-column k-step, lane l supplies token / row l % 32 and columns
+// 8 (l / 32) .. + 7 in the order (0, 4, 1, 5, 2, 6, 3, 7), the order in
+// which four bytes of packed 4-bit codes unpack into fp16 pairs with two
+// masks; A uses the same order, so each fragment is one 16-byte LDS read.
 //
 // Split over the columns.  Small row counts give few workgroups, so the
 // slabs are split over k_splits workgroups per row group; each writes its
@@ -43,11 +45,8 @@
 // resets the counter to zero.
 //
 // Epilogues (per output row r, token b): store; add into y (the residual
-// stream) and write the 64 rows' fp64 sum of squares per token, which the
-// next RMSNorm consumes; SiLU(gate) * up for a gate / up pair; RoPE at the
-// token's position and the K / V cache stores for fused q / k / v rows.
-// Prologue: RMSNorm of x from such sums of squares -- x * g is multiplied and
-// the 1 / rms factor, a per-token scalar, is applied to the final sum.
+// stream); SiLU(gate) * up for a gate / up pair; RoPE at the token's position
+// and the K / V cache stores for fused q / k / v rows.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
@@ -355,10 +354,11 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
 
 // ---- the GEMV ----
 //
-// Per 256-column slab a workgroup copies, with direct-to-LDS loads, its 64
+// Per 256-column slab a workgroup copies, with direct-to-LDS loads, its
 // weight rows' bytes (the aligned 16-byte chunks covering each row's slab)
-// and the slab's prepared x record into one of NBUF LDS slots; loads run
-// NBUF - 1 slabs ahead of the matrix-core work.
+// and the slab's prepared x record into one of NBUF LDS slots; with NBUF > 1
+// loads run NBUF - 1 slabs ahead of the matrix-core work (the launches use
+// one slot, so a slab's loads are issued after the previous slab's product).
 // Workgroup shapes: NT 32-row tiles (ROWS = 32 NT weight rows) and WV waves;
 // the 16 k-steps of a slab are split into KSW parts, wave w taking k-part
 // w / (WV / KSW) of TPW = NT KSW / WV tiles.  The launches use NT 2, WV 4,
