@@ -564,6 +564,19 @@ def engine_bench(args, torch, jinf_amd):
     out = e.generate([], n_gen)
     gen_s = time.perf_counter() - t0
     log(f"token steps decoded in this run: {e.n_past}")
+    # a 512-token prompt: batched prefill (steps of 64 tokens on the batched
+    # GEMVs) against the token-by-token forward call, each from position 0
+    n_pf = 512
+    pf_toks = [int(t) for t in torch.randint(0, hp["n_vocab"], (n_pf,), generator=g,
+                                             device="cuda").cpu()]
+    pf_ms = {}
+    for how in ("prefill", "forward", "prefill"):   # the first prefill is untimed warm-up
+        e.reset()
+        t0 = time.perf_counter()
+        getattr(e, how)(pf_toks)
+        pf_ms[how] = (time.perf_counter() - t0) * 1e3
+    log(f"{n_pf}-token prompt: prefill {pf_ms['prefill']:.1f} ms, "
+        f"forward {pf_ms['forward']:.1f} ms")
     e.close()
 
     gbs = step_bytes / (ms_tok * 1e-3) / 1e9
@@ -601,6 +614,10 @@ def engine_bench(args, torch, jinf_amd):
                    "generate_tokens_per_s": round(len(out) / gen_s, 2) if out else None,
                    "generated": len(out),
                    "prefill_6_tokens_ms": round(prefill_s * 1e3, 3),
+                   "prompt_tokens": n_pf,
+                   "prompt_prefill_ms": round(pf_ms["prefill"], 3),
+                   "prompt_forward_ms": round(pf_ms["forward"], 3),
+                   "prompt_prefill_tokens_per_s": round(n_pf / pf_ms["prefill"] * 1e3, 1),
                    "weight_bytes_per_token": wbytes,
                    "kv_bytes_per_token_mean": int(kv_bytes),
                    "context": [start_pos, start_pos + args.steps],

@@ -113,6 +113,21 @@ int jinf_hip_engine_n_past(const jinf_hip_engine* e);
 int jinf_hip_engine_forward(jinf_hip_engine* e, const int32_t* tokens, int n_tokens,
                             const float** logits);
 
+/* Decodes a prompt of n_tokens tokens in steps of up to 64 tokens, every GEMV
+ * running on a step's tokens at once on the matrix cores (the batched path
+ * of jinf_hip_batch_prefill, over this engine's own cache) and token i
+ * attending to the positions up to its own.  Leaves the engine where
+ * jinf_hip_engine_forward on the same tokens would (position advanced by
+ * n_tokens, next token the last token's argmax, *logits the last token's
+ * logits); per token the arithmetic is that loop's, with the batched GEMVs'
+ * rounding (within the same tolerances of the oracle, not bit-equal to
+ * forward).  One token, or a model whose n_embd or n_ff is not a multiple
+ * of 256 or above 32768, goes through jinf_hip_engine_forward.  Same status
+ * codes as forward.  The reference feeds a prompt one token at a time
+ * (src/engine.cpp:684-760); this entry point has no counterpart there. */
+int jinf_hip_engine_prefill(jinf_hip_engine* e, const int32_t* tokens, int n_tokens,
+                            const float** logits);
+
 /* Greedy generation (jinf_engine_generate, src/engine.cpp:762-805): the
  * prompt (if any) is decoded, then up to max_tokens argmax tokens (first
  * maximum on ties) are emitted and fed back; token 2 (end of sequence) is

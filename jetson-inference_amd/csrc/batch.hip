@@ -161,6 +161,7 @@ struct jinf_hip_batch {
     int head_dim = 0, q_dim = 0, kv_dim = 0, arg_parts = 1, hist_rows = 0;
     char* act = nullptr;  // activations, state, workspaces
     char* kv = nullptr;   // K caches, then V caches
+    bool kv_owned = true; // false: the engine's one-sequence cache, borrowed for its prefill
     size_t kv_layer_bytes = 0;
     float *hidden = nullptr, *q = nullptr, *attn = nullptr, *ff = nullptr, *up = nullptr;
     float* logits = nullptr;
@@ -329,7 +330,7 @@ void bat_release(jinf_hip_batch* b) {
     if (b->stream) (void)hipStreamSynchronize(b->stream);
     for (const auto& g : b->graphs) (void)hipGraphExecDestroy(g.second);
     if (b->h_io) (void)hipHostFree(b->h_io);
-    if (b->kv) (void)hipFree(b->kv);
+    if (b->kv && b->kv_owned) (void)hipFree(b->kv);
     if (b->act) (void)hipFree(b->act);
     if (b->stream) (void)hipStreamDestroy(b->stream);
     delete b;
@@ -339,7 +340,7 @@ void bat_release(jinf_hip_batch* b) {
 int bat_reset(jinf_hip_batch* b, int seq) {
     const jinf_hip_engine_desc& d = *b->d;
     const size_t per_seq = (size_t)b->max_ctx * b->kv_dim * b->kv_es;
-    for (int half = 0; half < 2; ++half)
+    for (int half = 0; half < 2 && b->kv_owned; ++half)
         for (int L = 0; L < d.n_layers; ++L) {
             char* base = b->kv + (size_t)(half * d.n_layers + L) * b->kv_layer_bytes;
             if (seq < 0)
@@ -366,8 +367,14 @@ int bat_set_mode(jinf_hip_batch* b, int mode) {
 
 }  // namespace
 
-extern "C" int jinf_hip_batch_create(jinf_hip_batch** out, const jinf_hip_engine* engine, int n_seq,
-                                     int max_context, int kv_type) {
+namespace {
+
+// kv_borrowed == nullptr: a batch with its own cache of n_seq regions.
+// Otherwise the cache is kv_borrowed, one region (sequence 0) laid out as the
+// engine's ([n_layers] K caches, then [n_layers] V caches, max_context *
+// kv_dim elements each), and n_seq is the number of rows of a prefill chunk.
+int bat_create(jinf_hip_batch** out, const jinf_hip_engine* engine, int n_seq, int max_context,
+               int kv_type, void* kv_borrowed) {
     if (!out) return JINF_HIP_ERR_INVALID;
     *out = nullptr;
     const jinf_hip_engine_desc* dp = engine_desc(engine);
@@ -389,7 +396,8 @@ extern "C" int jinf_hip_batch_create(jinf_hip_batch** out, const jinf_hip_engine
     b->head_dim = d.n_embd / d.n_heads;
     b->q_dim = d.n_embd;
     b->kv_dim = d.n_heads_kv * b->head_dim;
-    b->kv_layer_bytes = (size_t)n_seq * max_context * b->kv_dim * b->kv_es;
+    b->kv_owned = kv_borrowed == nullptr;
+    b->kv_layer_bytes = (size_t)(b->kv_owned ? n_seq : 1) * max_context * b->kv_dim * b->kv_es;
     b->arg_parts = (d.n_vocab + 4 * kArgThreads - 1) / (4 * kArgThreads);
     if (b->arg_parts > kBatArgParts) b->arg_parts = kBatArgParts;
     b->hist_rows = max_context < 256 ? max_context + 1 : 256;
@@ -424,7 +432,10 @@ extern "C" int jinf_hip_batch_create(jinf_hip_batch** out, const jinf_hip_engine
     int rc = hip_rc(hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking), "hipStreamCreate");
     if (rc == JINF_HIP_OK) rc = hip_rc(hipMalloc((void**)&b->act, off), "hipMalloc");
     const size_t kv_total = b->kv_layer_bytes * 2 * (size_t)d.n_layers;
-    if (rc == JINF_HIP_OK && kv_total) rc = hip_rc(hipMalloc((void**)&b->kv, kv_total), "hipMalloc");
+    if (!b->kv_owned)
+        b->kv = static_cast<char*>(kv_borrowed);
+    else if (rc == JINF_HIP_OK && kv_total)
+        rc = hip_rc(hipMalloc((void**)&b->kv, kv_total), "hipMalloc");
     if (rc == JINF_HIP_OK)
         rc = hip_rc(hipHostMalloc((void**)&b->h_io, (4 * ns + 16) * 4, hipHostMallocDefault),
                     "hipHostMalloc");
@@ -463,6 +474,27 @@ extern "C" int jinf_hip_batch_create(jinf_hip_batch** out, const jinf_hip_engine
     return JINF_HIP_OK;
 }
 
+}  // namespace
+
+namespace jinf {
+
+int batch_create_borrowed(jinf_hip_batch** out, const jinf_hip_engine* engine, int rows, void* kv,
+                          int max_context, int kv_type) {
+    if (!kv) return JINF_HIP_ERR_INVALID;
+    return bat_create(out, engine, rows, max_context, kv_type, kv);
+}
+
+void batch_set_pos(jinf_hip_batch* b, int pos) { b->h_pos[0] = pos; }
+
+const int32_t* batch_argmax(const jinf_hip_batch* b) { return b->cur; }
+
+}  // namespace jinf
+
+extern "C" int jinf_hip_batch_create(jinf_hip_batch** out, const jinf_hip_engine* engine, int n_seq,
+                                     int max_context, int kv_type) {
+    return bat_create(out, engine, n_seq, max_context, kv_type, nullptr);
+}
+
 extern "C" void jinf_hip_batch_destroy(jinf_hip_batch* b) { bat_release(b); }
 
 extern "C" int jinf_hip_batch_reset(jinf_hip_batch* b, int seq) {
@@ -483,7 +515,8 @@ extern "C" int jinf_hip_batch_use_graph(jinf_hip_batch* b, int on) {
 
 extern "C" int jinf_hip_batch_forward(jinf_hip_batch* b, const int32_t* tokens,
                                       const float** logits) {
-    if (!b || !tokens || !logits) return JINF_HIP_ERR_INVALID;
+    // a borrowed cache holds one sequence: prefill only
+    if (!b || !tokens || !logits || !b->kv_owned) return JINF_HIP_ERR_INVALID;
     const jinf_hip_engine_desc& d = *b->d;
     for (int s = 0; s < b->n_seq; ++s) {
         if (tokens[s] < -1 || tokens[s] >= d.n_vocab) {
@@ -556,7 +589,7 @@ extern "C" int jinf_hip_batch_prefill(jinf_hip_batch* b, int seq, const int32_t*
 }
 
 extern "C" int jinf_hip_batch_generate(jinf_hip_batch* b, int32_t* output, int steps) {
-    if (!b || !output || steps < 0) return JINF_HIP_ERR_INVALID;
+    if (!b || !output || steps < 0 || !b->kv_owned) return JINF_HIP_ERR_INVALID;
     int rc = JINF_HIP_OK;
     // in chunks of the device history's rows
     for (int done = 0; done < steps && rc == JINF_HIP_OK;) {

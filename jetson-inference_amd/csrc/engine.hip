@@ -37,6 +37,7 @@ namespace {
 enum { kPos = 0, kLen = 1, kTok = 2, kBest = 3, kFillEnd = 4, kStateWords = 64 };
 constexpr int kEos = 2;            // end-of-sequence id (src/engine.cpp:796-797)
 constexpr int kArgMaxParts = 256;
+constexpr int kPrefillRows = 64;   // prompt tokens per batched prefill step
 constexpr size_t kAlign = 256;
 
 // Step prologue: the token at the current position, and the attention length
@@ -107,6 +108,19 @@ __global__ __launch_bounds__(kArgThreads) void eng_argmax_end_kernel(
     st[kPos] = pos + 1;
 }
 
+// End of a prefill: the state n_tokens forward steps leave (position
+// new_pos, last argmax `best`, which is also the token at new_pos).
+__global__ void eng_prefill_end_kernel(int32_t* __restrict__ st, int32_t* __restrict__ tokens,
+                                       const int32_t* __restrict__ best, int new_pos,
+                                       int max_ctx) {
+    if (threadIdx.x != 0) return;
+    const int b = *best;
+    st[kPos] = new_pos;
+    st[kBest] = b;
+    st[kFillEnd] = new_pos;
+    if (new_pos < max_ctx) tokens[new_pos] = b;
+}
+
 bool is_matrix_type(int t) { return t == kQ4_0 || t == kQ8_0 || t == kQ4_K || t == kQ6_K; }
 bool is_dense_type(int t) { return t == JINF_HIP_F32 || t == JINF_HIP_F16; }
 
@@ -162,6 +176,11 @@ struct jinf_hip_engine {
     std::vector<std::pair<int, hipGraphExec_t>> graphs;
     int bound = 0;
     bool use_graph = true;
+    // prompt path: a batch over this engine's cache, made on the first
+    // prefill call (pre_state 1), or -1 when the model's shape is one the
+    // batched GEMVs do not take
+    jinf_hip_batch* pre = nullptr;
+    int pre_state = 0;
 };
 
 namespace {
@@ -375,6 +394,7 @@ void release(jinf_hip_engine* e) {
     if (!e) return;
     if (e->stream) (void)hipStreamSynchronize(e->stream);
     for (const auto& g : e->graphs) (void)hipGraphExecDestroy(g.second);
+    jinf_hip_batch_destroy(e->pre);  // before the cache it borrows
     if (e->h_tokens) (void)hipHostFree(e->h_tokens);
     if (e->kv) (void)hipFree(e->kv);
     if (e->act) (void)hipFree(e->act);
@@ -729,6 +749,39 @@ extern "C" int jinf_hip_engine_forward(jinf_hip_engine* e, const int32_t* tokens
     const int sc = hip_ok(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
     if (rc != JINF_HIP_OK) return rc;
     if (sc != JINF_HIP_OK) return sc;
+    *logits = e->logits;
+    return JINF_HIP_OK;
+}
+
+extern "C" int jinf_hip_engine_prefill(jinf_hip_engine* e, const int32_t* tokens, int n_tokens,
+                                       const float** logits) {
+    if (!e || !tokens || n_tokens <= 0 || !logits) return JINF_HIP_ERR_INVALID;
+    const jinf_hip_engine_desc& d = e->d;
+    if (e->pre_state == 0 && n_tokens > 1) {
+        const int rc = batch_create_borrowed(&e->pre, e, kPrefillRows, e->kv, d.max_context,
+                                             d.kv_type);
+        if (rc != JINF_HIP_OK && rc != JINF_HIP_ERR_INVALID) return rc;
+        e->pre_state = rc == JINF_HIP_OK ? 1 : -1;
+    }
+    if (n_tokens == 1 || !e->pre) return jinf_hip_engine_forward(e, tokens, n_tokens, logits);
+    // the batch validates the ids and the context against position n_past
+    batch_set_pos(e->pre, e->n_past);
+    const float* lg = nullptr;
+    ENG_TRY(jinf_hip_batch_prefill(e->pre, 0, tokens, n_tokens, &lg));
+    // the prefill has finished (the call waits): bring the engine's tokens,
+    // logits and state to where n_tokens forward steps leave them
+    const int p0 = e->n_past, p1 = p0 + n_tokens;
+    memcpy(e->h_tokens, tokens, (size_t)n_tokens * 4);
+    ENG_TRY(hip_ok(hipMemcpyAsync(e->tokens + p0, e->h_tokens, (size_t)n_tokens * 4,
+                                  hipMemcpyHostToDevice, e->stream),
+                   "hipMemcpyAsync"));
+    ENG_TRY(hip_ok(hipMemcpyAsync(e->logits, lg, (size_t)d.n_vocab * 4, hipMemcpyDeviceToDevice,
+                                  e->stream),
+                   "hipMemcpyAsync"));
+    ENG_TRY(launch(eng_prefill_end_kernel, dim3(1), dim3(64), 0, e->stream, e->state, e->tokens,
+                   batch_argmax(e->pre), p1, d.max_context));
+    ENG_TRY(hip_ok(hipStreamSynchronize(e->stream), "hipStreamSynchronize"));
+    e->n_past = p1;
     *logits = e->logits;
     return JINF_HIP_OK;
 }

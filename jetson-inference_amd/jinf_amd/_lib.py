@@ -115,6 +115,7 @@ SIGNATURES = {
     "jinf_hip_engine_reset": (_I, [_P]),
     "jinf_hip_engine_n_past": (_I, [_P]),
     "jinf_hip_engine_forward": (_I, [_P, _P, _I, ctypes.POINTER(_P)]),
+    "jinf_hip_engine_prefill": (_I, [_P, _P, _I, ctypes.POINTER(_P)]),
     "jinf_hip_engine_generate": (_I, [_P, _P, _I, _P, _I, ctypes.POINTER(_I)]),
     "jinf_hip_engine_copy_logits": (_I, [_P, _P, _I]),
     "jinf_hip_engine_use_graph": (_I, [_P, _I]),

@@ -158,6 +158,15 @@ class Engine:
                lib().jinf_hip_engine_forward(self._h, t.ctypes.data, t.size, ctypes.byref(p)))
         return p.value
 
+    def prefill(self, tokens):
+        """Decode a prompt in batched steps (jinf_hip_engine_prefill); returns
+        the device address of the last token's fp32 logits."""
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(-1))
+        p = ctypes.c_void_p()
+        _check("jinf_hip_engine_prefill",
+               lib().jinf_hip_engine_prefill(self._h, t.ctypes.data, t.size, ctypes.byref(p)))
+        return p.value
+
     def logits(self):
         """Host copy (fp32 numpy) of the last token's logits."""
         out = np.empty(self.n_vocab, np.float32)

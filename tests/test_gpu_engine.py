@@ -138,6 +138,58 @@ def test_generate_matches_host_greedy_loop(dev):
             lg = ref.step(tok)
 
 
+@pytest.mark.parametrize("kv_type", [mu.F32, mu.F16], ids=["kv-f32", "kv-f16"])
+@pytest.mark.parametrize("name", ["mixed", "hd128-gqa4", "hd96"])
+def test_prefill_matches_oracle_and_continues(dev, name, kv_type):
+    """A prompt through prefill (steps of 64 and 6 tokens on the batched GEMVs
+    over the engine's own cache; hd96's n_embd of 384 takes the token-by-token
+    path instead) equals the oracle's loop and leaves the engine where
+    forward would: later forward steps and greedy generation continue it."""
+    max_ctx = 96
+    say(f"engine prefill {name} kv={'f16' if kv_type else 'f32'}")
+    hp, W = mu.tiny_model(seed=18, **MODELS[name])
+    tol = TOL_F16_KV if kv_type == mu.F16 else TOL
+    prompt = np.random.default_rng(19).integers(0, hp["n_vocab"], size=70).astype(np.int32)
+    ref = oeng.Decoder(hp, W, max_context=max_ctx, kv_type=kv_type)
+    with make_engine(hp, W, max_ctx, kv_type) as e:
+        e.forward([5])  # the prompt starts at position 1
+        ref.step(5)
+        e.prefill(prompt)
+        for t in prompt:
+            want = ref.step(int(t))
+        assert e.n_past == 1 + len(prompt)
+        compare(e.logits(), want, f"{name} prefill last token", tol)
+        for t in (7, 11):
+            e.forward([t])
+            compare(e.logits(), ref.step(t), f"{name} step after prefill", tol)
+        first = oeng.first_argmax(e.logits())
+        assert e.generate([], 1) == [first]
+        # generation right after a prefill starts from the prompt's argmax
+        e.reset()
+        e.prefill(prompt[:9])
+        nxt = oeng.first_argmax(e.logits())
+        assert e.generate([], 1) == [nxt]
+        assert e.n_past == 9 + (nxt != oeng.EOS)  # the emitted token was decoded
+
+
+def test_prefill_errors_and_context_end(dev):
+    hp, W = mu.tiny_model(seed=20, n_vocab=64, n_layers=1)
+    with make_engine(hp, W, 8, mu.F32) as e:
+        for bad in ([64, 1], [1, -1], list(range(9))):
+            with pytest.raises(EngineError) as ex:
+                e.prefill(bad)
+            assert ex.value.status == 5
+            assert e.n_past == 0
+        e.prefill([3])             # one token: the forward path
+        e.prefill(list(range(7)))  # fills the context
+        assert e.n_past == 8
+        with pytest.raises(EngineError):
+            e.prefill([1, 2])
+        with pytest.raises(EngineError):
+            e.forward([1])
+        assert e.generate([], 3) == [oeng.first_argmax(e.logits())]
+
+
 def test_generate_stops_at_eos(dev):
     say("generation stops after emitting token 2")
     hp, W = mu.pass_through_model()
