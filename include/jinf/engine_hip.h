@@ -131,7 +131,9 @@ int jinf_hip_engine_prefill(jinf_hip_engine* e, const int32_t* tokens, int n_tok
 /* Greedy generation (jinf_engine_generate, src/engine.cpp:762-805): the
  * prompt (if any) is decoded, then up to max_tokens argmax tokens (first
  * maximum on ties) are emitted and fed back; token 2 (end of sequence) is
- * emitted and stops generation. */
+ * emitted and stops generation.  The prompt goes through
+ * jinf_hip_engine_forward (one token at a time); for a long prompt, call
+ * jinf_hip_engine_prefill first and then generate with n_prompt 0. */
 int jinf_hip_engine_generate(jinf_hip_engine* e, const int32_t* prompt, int n_prompt,
                              int32_t* output, int max_tokens, int* n_generated);
 

@@ -139,7 +139,7 @@ def test_generate_matches_host_greedy_loop(dev):
 
 
 @pytest.mark.parametrize("kv_type", [mu.F32, mu.F16], ids=["kv-f32", "kv-f16"])
-@pytest.mark.parametrize("name", ["mixed", "hd128-gqa4", "hd96"])
+@pytest.mark.parametrize("name", ["mixed", "q4_0-f16norm-tied", "hd128-gqa4", "hd96"])
 def test_prefill_matches_oracle_and_continues(dev, name, kv_type):
     """A prompt through prefill (steps of 64 and 6 tokens on the batched GEMVs
     over the engine's own cache; hd96's n_embd of 384 takes the token-by-token
