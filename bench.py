@@ -445,12 +445,12 @@ def batch_bench(args, torch, jinf_amd, spec):
     # untimed run
     import ctypes
     import numpy as np
-    n_pf = min(512, max_ctx)
+    n_pf = min(args.prompt_tokens, max_ctx)
     ids = np.ascontiguousarray(
         np.random.default_rng(args.seed).integers(0, hp["n_vocab"], n_pf).astype(np.int32))
     lptr = ctypes.c_void_p()
     pf_s = None
-    for _ in range(2):
+    for _ in range(2 if n_pf > 0 else 0):
         b.reset(0)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -459,8 +459,9 @@ def batch_bench(args, torch, jinf_amd, spec):
         pf_s = time.perf_counter() - t0
         if rc != 0:
             raise SystemExit(f"jinf_hip_batch_prefill failed ({rc})")
-    log(f"prefill of {n_pf} tokens in chunks of {n_seq}: {pf_s * 1e3:.2f} ms, "
-        f"{n_pf / pf_s:.0f} tokens/s")
+    if n_pf > 0:
+        log(f"prefill of {n_pf} tokens in chunks of {n_seq}: {pf_s * 1e3:.2f} ms, "
+            f"{n_pf / pf_s:.0f} tokens/s")
     b.close()
     e.close()
     cpu = None
@@ -497,8 +498,8 @@ def batch_bench(args, torch, jinf_amd, spec):
                    "tokens_per_s": round(tok_s, 1),
                    "prefill_6_steps_ms": round(prefill_s * 1e3, 3),
                    "prompt_tokens": n_pf,
-                   "prompt_ms": round(pf_s * 1e3, 3),
-                   "prompt_tokens_per_s": round(n_pf / pf_s, 1),
+                   "prompt_ms": round(pf_s * 1e3, 3) if n_pf else None,
+                   "prompt_tokens_per_s": round(n_pf / pf_s, 1) if n_pf else None,
                    "weight_bytes_per_step": wbytes,
                    "kv_bytes_per_step_mean": int(kv_bytes),
                    "context": [start_pos, start_pos + args.steps],
@@ -566,17 +567,19 @@ def engine_bench(args, torch, jinf_amd):
     log(f"token steps decoded in this run: {e.n_past}")
     # a 512-token prompt: batched prefill (steps of 64 tokens on the batched
     # GEMVs) against the token-by-token forward call, each from position 0
-    n_pf = 512
-    pf_toks = [int(t) for t in torch.randint(0, hp["n_vocab"], (n_pf,), generator=g,
+    n_pf = min(args.prompt_tokens, max_ctx)
+    pf_toks = [int(t) for t in torch.randint(0, hp["n_vocab"], (max(n_pf, 1),), generator=g,
                                              device="cuda").cpu()]
-    pf_ms = {}
-    for how in ("prefill", "forward", "prefill"):   # the first prefill is untimed warm-up
+    pf_ms = {"prefill": float("nan"), "forward": float("nan")}
+    for how in ("prefill", "forward", "prefill") if n_pf > 0 else ():
+        # the first prefill is untimed warm-up
         e.reset()
         t0 = time.perf_counter()
         getattr(e, how)(pf_toks)
         pf_ms[how] = (time.perf_counter() - t0) * 1e3
-    log(f"{n_pf}-token prompt: prefill {pf_ms['prefill']:.1f} ms, "
-        f"forward {pf_ms['forward']:.1f} ms")
+    if n_pf > 0:
+        log(f"{n_pf}-token prompt: prefill {pf_ms['prefill']:.1f} ms, "
+            f"forward {pf_ms['forward']:.1f} ms")
     e.close()
 
     gbs = step_bytes / (ms_tok * 1e-3) / 1e9
@@ -615,9 +618,10 @@ def engine_bench(args, torch, jinf_amd):
                    "generated": len(out),
                    "prefill_6_tokens_ms": round(prefill_s * 1e3, 3),
                    "prompt_tokens": n_pf,
-                   "prompt_prefill_ms": round(pf_ms["prefill"], 3),
-                   "prompt_forward_ms": round(pf_ms["forward"], 3),
-                   "prompt_prefill_tokens_per_s": round(n_pf / pf_ms["prefill"] * 1e3, 1),
+                   "prompt_prefill_ms": round(pf_ms["prefill"], 3) if n_pf else None,
+                   "prompt_forward_ms": round(pf_ms["forward"], 3) if n_pf else None,
+                   "prompt_prefill_tokens_per_s":
+                       round(n_pf / pf_ms["prefill"] * 1e3, 1) if n_pf else None,
                    "weight_bytes_per_token": wbytes,
                    "kv_bytes_per_token_mean": int(kv_bytes),
                    "context": [start_pos, start_pos + args.steps],
@@ -850,6 +854,8 @@ def main():
     ap.add_argument("--batch", type=int, default=0,
                     help="sequences of llama3-8b-decode-batch (default 32, at most 64)")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--prompt-tokens", type=int, default=512,
+                    help="engine workloads: tokens of the timed prompt (0 = no prompt timing)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, host cores)")

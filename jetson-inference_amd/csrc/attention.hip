@@ -441,24 +441,15 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     const uint16_t* vb = vc + (int64_t)s * ld_seq + (int64_t)j * HD;
 
     // Q' fragments of this lane's column (zero for unused head slots): the
-    // lane's DPG contiguous q values, loaded unconditionally
-    am_h4 qf[KS];
+    // lane's DPG contiguous q values, loaded unconditionally.  The loads are
+    // issued here and converted after the first tile's K / V loads have been
+    // issued (below), so the q and K / V fetches are in flight together.
+    float4 qraw[KS];
     {
-        const float qs = slot < G ? scale : 0.0f;
         const float4* qp = reinterpret_cast<const float4*>(
             q + (int64_t)s * ld_q + (int64_t)(h0 + (slot < G ? slot : 0)) * HD + DPG * lg);
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const float4 v = qp[ks];
-            const float x[4] = {v.x * qs, v.y * qs, v.z * qs, v.w * qs};
-            _Float16 hv[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const _Float16 hi = (_Float16)x[i];
-                hv[i] = lo_col ? (_Float16)(x[i] - (float)hi) : hi;
-            }
-            qf[ks] = am_h4{hv[0], hv[1], hv[2], hv[3]};
-        }
+        for (int ks = 0; ks < KS; ++ks) qraw[ks] = qp[ks];
     }
 
     float m = -INFINITY, lsum = 0.0f;
@@ -504,6 +495,24 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     if (c0 + wave * kAtTile < c1) {
         load_k(c0 + wave * kAtTile);
         load_v(c0 + wave * kAtTile);
+    }
+    // q' = q * scale as fp16 hi / lo parts (the compiler's wait for the q
+    // loads also covers the K / V loads issued after them: in-order counts)
+    am_h4 qf[KS];
+    {
+        const float qs = slot < G ? scale : 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const float4 v = qraw[ks];
+            const float x[4] = {v.x * qs, v.y * qs, v.z * qs, v.w * qs};
+            _Float16 hv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const _Float16 hi = (_Float16)x[i];
+                hv[i] = lo_col ? (_Float16)(x[i] - (float)hi) : hi;
+            }
+            qf[ks] = am_h4{hv[0], hv[1], hv[2], hv[3]};
+        }
     }
     for (int t0 = c0 + wave * kAtTile; t0 < c1; t0 += tstep) {
         const bool more = t0 + tstep < c1;  // wave-uniform
