@@ -14,13 +14,17 @@
 //     call in fp64 and rounds it to fp32 (the correctly rounded value), and
 //     passes the table by value in the kernel arguments;
 //   - grid = (units of one token / 128, tokens): a 16-byte unit is 4 (fp32)
-//     or 8 (fp16) elements of one head.  Each workgroup first issues its unit
-//     loads, then lanes 0..head_dim/2-1 evaluate the token's (cos, sin) pairs
-//     in fp64 from the fp32 angle (full-range argument reduction), round them
-//     to fp32 and share them through LDS, so the transcendental cost is paid
-//     once per token per workgroup instead of once per element, and the
-//     fp32 results are the correctly rounded cos/sin of the exact fp32 angle;
-//   - in place: each unit is read and written by the same lane.
+//     or 8 (fp16) elements of one head, one unit per lane, read and written
+//     by the same lane (in place) with nontemporal 16-byte accesses;
+//   - head_dim <= 128 (at most 64 pairs): every wave builds the token's
+//     (cos, sin) table by itself.  Lane j evaluates pair j mod head_dim/2 in
+//     fp64 from the fp32 angle (cos_sin_f32: correctly rounded in practice,
+//     about 25 fp64 operations) while its unit load is in flight, and each
+//     lane then reads the pairs of its unit from the owning lanes with
+//     cross-lane permutes.  No LDS, no barrier: a wave's stores wait only for
+//     its own loads and the permutes;
+//   - head_dim in (128, 512]: the workgroup's first head_dim/2 lanes build the
+//     table in LDS behind one barrier.
 #include <math.h>
 
 #include "jinf_device.h"
@@ -32,53 +36,62 @@ namespace jinf {
 
 constexpr int kRopeBlock = 128;
 
-// Fill cs[i] = (cos, sin) of fl32(pos * theta_i) for i < half.  Ends with a
-// barrier.
-__device__ __forceinline__ void rope_table(float2* cs, int half, int pos,
-                                           const RopeTheta& th) {
-    for (int i = threadIdx.x; i < half; i += blockDim.x) cs[i] = rope_cs(pos, th.t[i]);
-    __syncthreads();
-}
-
-// UPT units per thread, spaced one workgroup apart.
-template <typename TA, int UPT = 1>
+// One 16-byte unit per lane.  WAVE_TABLE: head_dim / 2 <= 64, the (cos, sin)
+// pairs come from lanes of the same wave; otherwise from an LDS table.  HD > 0
+// fixes head_dim at compile time (64 and 128: the index arithmetic becomes
+// shifts and masks instead of integer divisions).
+template <typename TA, bool WAVE_TABLE, int HD, typename TH>
 __global__ __launch_bounds__(kRopeBlock) void rope_vec_kernel(
-    TA* q, int ld_q, TA* k, int ld_k, const int32_t* positions, int pos0, int head_dim,
-    int units_q, int units_tok, RopeTheta th) {
+    TA* q, int ld_q, TA* k, int ld_k, const int32_t* positions, int pos0, int head_dim_arg,
+    int units_q, int units_tok, TH th) {
     using A = Act<TA>;
     constexpr int E = A::kElems;
-    __shared__ float2 cs[kRopeMaxHalf];
+    const int head_dim = HD > 0 ? HD : head_dim_arg;
+    __shared__ float2 cs[WAVE_TABLE ? 1 : kRopeMaxHalf];
     const int64_t t = blockIdx.x;
-    TA* p[UPT];
-    int i0[UPT];
-    uint4 raw[UPT];
-#pragma unroll
-    for (int j = 0; j < UPT; ++j) {
-        const int u = (blockIdx.y * UPT + j) * kRopeBlock + threadIdx.x;
-        p[j] = nullptr;
-        i0[j] = 0;
-        if (u < units_tok) {
-            const int uu = u < units_q ? u : u - units_q;
-            p[j] = u < units_q ? q + t * ld_q + (int64_t)uu * E : k + t * ld_k + (int64_t)uu * E;
-            i0[j] = (uu * E % head_dim) / 2;
-            raw[j] = ld16<true>(p[j]);
-        }
-    }
+    const int u = blockIdx.y * kRopeBlock + threadIdx.x;
+    const bool live = u < units_tok;
+    const int half = head_dim / 2;
+    const int lane = threadIdx.x & (kWave - 1);
+    // theta (a per-lane read of the kernel arguments, a vector load) is read
+    // before the unit load is issued: vector loads complete in order, so a
+    // later theta load would make the (cos, sin) evaluation wait for the
+    // unit's HBM latency instead of overlapping it.
+    float theta = 0.0f;
+    if constexpr (WAVE_TABLE) theta = th.t[lane % half];
+    // Lanes past the token's last unit load that unit too (never stored), so
+    // every lane issues exactly one unit load and the wait for theta can
+    // leave it in flight.
+    const int ul = live ? u : units_tok - 1;
+    const int uu = ul < units_q ? ul : ul - units_q;
+    TA* p = ul < units_q ? q + t * ld_q + (int64_t)uu * E : k + t * ld_k + (int64_t)uu * E;
+    const int i0 = (uu * E % head_dim) / 2;
+    const uint4 raw = ld16<true>(p);
     const int pos = positions ? positions[t] : pos0 + (int)t;
-    rope_table(cs, head_dim / 2, pos, th);
+    float c[E / 2], sn[E / 2];
+    if constexpr (WAVE_TABLE) {
+        // every lane of the wave takes part in the permutes (no lane has exited)
+        const float2 mine = rope_cs(pos, theta);
 #pragma unroll
-    for (int j = 0; j < UPT; ++j) {
-        if (p[j]) {
-            float v[E];
-            A::unpack(raw[j], v);
+        for (int e = 0; e < E / 2; ++e) {
+            c[e] = __shfl(mine.x, i0 + e, kWave);
+            sn[e] = __shfl(mine.y, i0 + e, kWave);
+        }
+    } else {
+        for (int i = threadIdx.x; i < half; i += blockDim.x) cs[i] = rope_cs(pos, th.t[i]);
+        __syncthreads();
 #pragma unroll
-            for (int e = 0; e < E / 2; ++e) {
-                const float2 c = cs[i0[j] + e];
-                rot(v[2 * e], v[2 * e + 1], c.x, c.y);
-            }
-            st16<true>(p[j], A::pack(v));
+        for (int e = 0; e < E / 2; ++e) {
+            c[e] = cs[i0 + e].x;
+            sn[e] = cs[i0 + e].y;
         }
     }
+    if (!live) return;
+    float v[E];
+    A::unpack(raw, v);
+#pragma unroll
+    for (int e = 0; e < E / 2; ++e) rot(v[2 * e], v[2 * e + 1], c[e], sn[e]);
+    st16<true>(p, A::pack(v));
 }
 
 // One pair per lane, any alignment.
@@ -103,7 +116,8 @@ __global__ __launch_bounds__(kRopeBlock) void rope_scalar_kernel(
         x1 = A::load1(p + 1);
     }
     const int pos = positions ? positions[t] : pos0 + (int)t;
-    rope_table(cs, half, pos, th);
+    for (int j = threadIdx.x; j < half; j += blockDim.x) cs[j] = rope_cs(pos, th.t[j]);
+    __syncthreads();
     if (u < pairs_tok) {
         const float2 c = cs[i];
         rot(x0, x1, c.x, c.y);
@@ -117,8 +131,6 @@ static int rope_launch(void* q, int ld_q, void* k, int ld_k, const int32_t* posi
                        int n_tokens, int head_dim, int n_heads, int n_heads_kv, float base,
                        hipStream_t stream) {
     constexpr int E = Act<TA>::kElems;
-    RopeTheta th;
-    theta_table(th, head_dim, base);
     TA* pq = static_cast<TA*>(q);
     TA* pk = static_cast<TA*>(k);
     const bool vec = head_dim % E == 0 && (n_heads == 0 || aligned(q, 16)) &&
@@ -129,9 +141,23 @@ static int rope_launch(void* q, int ld_q, void* k, int ld_k, const int32_t* posi
         const int units_q = n_heads * head_dim / E;
         const int units_tok = units_q + n_heads_kv * head_dim / E;
         const dim3 grid(n_tokens, (units_tok + kRopeBlock - 1) / kRopeBlock);
-        return launch(rope_vec_kernel<TA>, grid, dim3(kRopeBlock), 0, stream, pq, ld_q, pk,
-                      ld_k, positions, pos0, head_dim, units_q, units_tok, th);
+        auto go = [&](auto kern, const auto& th) {
+            return launch(kern, grid, dim3(kRopeBlock), 0, stream, pq, ld_q, pk, ld_k, positions,
+                          pos0, head_dim, units_q, units_tok, th);
+        };
+        if (head_dim / 2 <= kWave) {
+            RopeTheta64 th;
+            theta_table(th, head_dim, base);
+            if (head_dim == 128) return go(rope_vec_kernel<TA, true, 128, RopeTheta64>, th);
+            if (head_dim == 64) return go(rope_vec_kernel<TA, true, 64, RopeTheta64>, th);
+            return go(rope_vec_kernel<TA, true, 0, RopeTheta64>, th);
+        }
+        RopeTheta th;
+        theta_table(th, head_dim, base);
+        return go(rope_vec_kernel<TA, false, 0, RopeTheta>, th);
     }
+    RopeTheta th;
+    theta_table(th, head_dim, base);
     const int pairs_q = n_heads * head_dim / 2;
     const int pairs_tok = pairs_q + n_heads_kv * head_dim / 2;
     const dim3 grid(n_tokens, (pairs_tok + kRopeBlock - 1) / kRopeBlock);

@@ -1,10 +1,13 @@
 """GPU parity: interleaved RoPE (drop-in fp32 and fp16/fp32 rows).
 
-Bar: fp16 within 2 ulp of the oracle; fp32 within 1e-5 relative, measured
-against max(|ref|, |pair|) because a rotation output near zero is a difference
-of two products and its error scales with the pair's norm.  The GPU evaluates
-(cos, sin) in fp64 from the same fp32 angle and applies the rotation without
-contraction, like the oracle, so almost every element is bit-identical.
+Bar: fp16 within 2 ulp of the oracle; fp32 within 1e-5 of |ref| per element
+(north_star's tolerance).  The GPU evaluates (cos, sin) in fp64 from the same
+fp32 angle, rounds them once to fp32 and applies the rotation without
+contraction, like the oracle, so the outputs are expected to be bit-identical;
+each test reports the bit-identical fraction.  The relative error of an output
+near zero is also reported against max(|ref|, |pair|): such an output is a
+difference of two products, so a 1-ulp difference in cos or sin would show
+up there first.
 """
 import os
 
@@ -33,13 +36,14 @@ def check(got, ref, src, hd, what):
     if got.dtype == np.float16:
         w = tu.assert_f16_close(got, ref, 2, what)
     else:
+        w = tu.assert_f32_close(got, ref, 1e-5, 1e-30, what)
         err = np.abs(got.astype(np.float64) - ref) / np.maximum(np.abs(ref.astype(np.float64)),
                                                                  pair_floor(src, hd))
-        w = float(err.max())
-        assert w <= 1e-5, f"{what}: {w}"
+        say(f"{what}: worst error relative to the pair norm {float(err.max()):.3g}")
     exact = float(np.mean(got.view(np.uint16 if got.dtype == np.float16 else np.uint32)
                           == ref.view(np.uint16 if ref.dtype == np.float16 else np.uint32)))
     say(f"{what}: worst {w}, bit-identical fraction {exact:.6f}")
+    return exact
 
 
 def test_config2_full(dev):
@@ -51,8 +55,10 @@ def test_config2_full(dev):
     rq, rk = oracle.rope_rows(q, k, 128, pos, 0, 500000.0)
     qd, kd = to_dev(q), to_dev(k)
     jinf_amd.rope_rows(qd, kd, 128, to_dev(pos), 0, 500000.0)
-    check(host(qd), rq, q, 128, "q")
-    check(host(kd), rk, k, 128, "k")
+    # observed bit-identical: (cos, sin) are the correctly rounded values on
+    # both sides and the rotation rounds at the same points
+    assert check(host(qd), rq, q, 128, "q") == 1.0
+    assert check(host(kd), rk, k, 128, "k") == 1.0
 
 
 def test_config5_decode_shape(dev):
@@ -64,8 +70,8 @@ def test_config5_decode_shape(dev):
     rq, rk = oracle.rope_rows(q, k, 128, pos, 0, 500000.0)
     qd, kd = to_dev(q), to_dev(k)
     jinf_amd.rope_rows(qd, kd, 128, to_dev(pos), 0, 500000.0)
-    check(host(qd), rq, q, 128, "q")
-    check(host(kd), rk, k, 128, "k")
+    assert check(host(qd), rq, q, 128, "q") == 1.0
+    assert check(host(kd), rk, k, 128, "k") == 1.0
 
 
 def test_fixture(dev):
@@ -126,3 +132,24 @@ def test_full_size_norm_preservation(dev):
         na = torch.hypot(a[:, 0::2].double(), a[:, 1::2].double())
         nb = torch.hypot(b[:, 0::2].double(), b[:, 1::2].double())
         assert float(((nb - na).abs() / na.clamp_min(1e-30)).max()) < 1e-6
+
+
+@pytest.mark.parametrize("hd", [128, 64, 256])
+def test_large_positions_fp32(dev, hd):
+    """Positions up to 2^31 - 1: angles beyond 2^20 take the device library's
+    fp64 sincos, smaller ones the library's own reduction; pair 0 (theta = 1)
+    rotates by the position itself.  Every output within 1e-5 per element."""
+    say(f"fp32 rows, head_dim {hd}, positions up to 2^31 - 1")
+    r = tu.rng(hd + 7)
+    pos = np.array([0, 1, 2, 3, 4, 1000, 8191, 65535, 102943, 1 << 20, (1 << 20) - 1,
+                    (1 << 20) + 1, 1647099, 1647100, 16777215, 16777217, 123456789,
+                    (1 << 31) - 1, 1 << 30, 355, 710, 1068966896], np.int32)
+    T = pos.size
+    q = tu.normal(r, (T, 4 * hd), dtype=np.float32)
+    k = tu.normal(r, (T, 2 * hd), dtype=np.float32)
+    for base in (10000.0, 500000.0):
+        rq, rk = oracle.rope_rows(q, k, hd, pos, 0, base)
+        qd, kd = to_dev(q), to_dev(k)
+        jinf_amd.rope_rows(qd, kd, hd, to_dev(pos), 0, base)
+        check(host(qd), rq, q, hd, f"q base {base:g}")
+        check(host(kd), rk, k, hd, f"k base {base:g}")
