@@ -292,6 +292,30 @@ int jinf_attention_decode(float* out, int ld_out, const float* q, int ld_q,
  * (0 for an empty shape). */
 size_t jinf_attention_workspace_bytes(int n_seq, int n_heads, int head_dim, int max_ctx);
 
+/* jinf_attention_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  Same
+ * arguments, results and kernels as jinf_attention_decode with a workspace
+ * (bit-identical outputs); the split contexts keep their merge counters and
+ * chunk records in a library-owned scratch array in device memory instead:
+ * 16 KiB of counters plus 8 MiB of records, one copy per device, held until
+ * the process ends.  Nothing is allocated or freed by the call.
+ *   - The first call on a device looks the scratch up (hipGetSymbolAddress)
+ *     with that device current; make each call with the stream's device
+ *     current.
+ *   - A shape whose split needs more than the scratch holds (records of
+ *     n_seq * n_heads * chunks * (head_dim + 2) floats above 8 MiB, e.g.
+ *     127 sequences x 64 heads over 8192 positions) returns
+ *     JINF_HIP_ERR_INVALID with a stderr line and enqueues nothing.
+ *   - Every call on one device shares that device's scratch (each clears the
+ *     counters it uses first): calls that may run at the same time on one
+ *     device, on different streams, race and must not be issued. */
+int jinf_attention_decode_noalloc(float* out, int ld_out, const float* q, int ld_q,
+                                  const void* k_cache, const void* v_cache, int kv_type,
+                                  int64_t ld_pos, int64_t ld_seq, const int32_t* lens,
+                                  int n_seq, int max_ctx, int head_dim, int n_heads,
+                                  int n_heads_kv, float scale, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,6 +39,9 @@
 // head_dim 64 and 128 with 16-byte aligned rows take this kernel; anything
 // else takes a one-wave-per-head kernel (dims on lanes, one wave reduction
 // per position) with the same arithmetic.
+#include <atomic>
+#include <mutex>
+
 #include "jinf_device.h"
 #include "jinf_host.h"
 #include "jinf/kernels.h"
@@ -713,11 +716,42 @@ static size_t am_workspace_bytes(int n_seq, int n_heads, int head_dim, int max_c
            (size_t)n_seq * n_heads * nch * (head_dim + 2) * sizeof(float);
 }
 
+// Where a split context keeps its merge counters and chunk records.
+//   fixed == false: the caller's workspace (`base`, `bytes`), laid out as
+//     above and used only when it holds am_workspace_bytes for the call;
+//   fixed == true: this device's copy of `scratch` (below), with a fixed
+//     layout: kScratchCounterBytes of merge counters, then
+//     kScratchRecordBytes of records.  A call whose split needs more is
+//     rejected.
+struct AmScratch {
+    void* base;
+    size_t bytes;
+    bool fixed;
+};
+
+// The no-allocation entry point's scratch (jinf_attention_decode_noalloc):
+// 4096 merge counters and 8 MiB of chunk records, enough for every split of
+// up to about 1000 (sequence, head group) pairs at head_dim 128 (the 70B
+// 64-sequence decode needs 4.3 MB).  Each device that runs the library holds
+// its own copy until the process ends; host code only ever passes the
+// per-device address from hipGetSymbolAddress (scratch_base), never the
+// symbol itself.
+constexpr size_t kScratchCounterBytes = (size_t)16 << 10;
+constexpr size_t kScratchRecordBytes = (size_t)8 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchCounterBytes + kScratchRecordBytes];
+
+// Zero n merge counters (a kernel rather than a memset node, so that the
+// call stays correct when a caller captures it in a graph).
+__global__ __launch_bounds__(256) void am_clear_kernel(unsigned* __restrict__ c, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) c[i] = 0u;
+}
+
 template <int HD>
 static int am_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, const void* k,
                      const void* v, int64_t ld_pos, int64_t ld_seq, const int32_t* lens,
                      int n_past, int n_seq, int n_heads, int group, int G, float scale,
-                     void* workspace, size_t ws_bytes, hipStream_t stream) {
+                     const AmScratch& sc, hipStream_t stream) {
     const size_t shmem = (size_t)4 * 2 * kAtTile * HD * 2;  // K and V tile per wave
     // chunk: a multiple of 64 positions, at least kAmChunkMin, giving about
     // kAmTargetItems (sequence, head group, chunk) items
@@ -726,9 +760,10 @@ static int am_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, c
     ch = (ch + 63) / 64 * 64;
     if (ch < kAmChunkMin) ch = kAmChunkMin;
     // the merge keeps 16 floats per chunk (+ 8) in the tile buffers' LDS
-    const bool split = workspace && n_past > ch &&
-                       ws_bytes >= am_workspace_bytes(n_seq, n_heads, HD, n_past) &&
-                       ((n_past + ch - 1) / ch * 16 + 8) * sizeof(float) <= shmem;
+    bool split = sc.base && n_past > ch &&
+                 ((n_past + ch - 1) / ch * 16 + 8) * sizeof(float) <= shmem;
+    if (split && !sc.fixed && sc.bytes < am_workspace_bytes(n_seq, n_heads, HD, n_past))
+        split = false;
     const int chunk = split ? (int)ch : (n_past > 0 ? n_past : 1);
     const int nch = split ? (n_past + chunk - 1) / chunk : 1;
     // Few (sequence, head group) pairs: the last workgroup of each merges in
@@ -737,10 +772,31 @@ static int am_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, c
     // merge counter before retiring, so a separate wide merge launch is
     // faster (64 sequences x 8 groups: 268 us against 290).
     const bool in_kernel = (int64_t)n_seq * (n_heads / G) < kAmInKernelMerge;
-    unsigned* counters = split && in_kernel ? static_cast<unsigned*>(workspace) : nullptr;
-    float* ws = split ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                 am_counter_bytes(n_seq, n_heads))
-                      : nullptr;
+    unsigned* counters = nullptr;
+    float* ws = nullptr;
+    if (split && sc.fixed) {
+        const size_t need = (size_t)n_seq * n_heads * nch * (HD + 2) * sizeof(float);
+        const size_t slots = (size_t)n_seq * n_heads;
+        if (need > kScratchRecordBytes || (in_kernel && slots * 4 > kScratchCounterBytes)) {
+            JINF_LOG("jinf_attention_decode_noalloc: this shape splits its contexts into %d "
+                     "chunks and needs %zu bytes of records (at most %zu) and %zu merge counters "
+                     "(at most %zu); nothing was enqueued", nch, need, kScratchRecordBytes,
+                     in_kernel ? slots : (size_t)0, kScratchCounterBytes / 4);
+            return JINF_HIP_ERR_INVALID;
+        }
+        counters = in_kernel ? static_cast<unsigned*>(sc.base) : nullptr;
+        ws = reinterpret_cast<float*>(static_cast<uint8_t*>(sc.base) + kScratchCounterBytes);
+        if (counters) {
+            // the scratch keeps the previous call's contents: clear the counters
+            const int st = launch(am_clear_kernel, dim3((unsigned)((slots + 255) / 256)),
+                                  dim3(256), 0, stream, counters, (int)slots);
+            if (st != JINF_HIP_OK) return st;
+        }
+    } else if (split) {
+        counters = in_kernel ? static_cast<unsigned*>(sc.base) : nullptr;
+        ws = reinterpret_cast<float*>(static_cast<char*>(sc.base) +
+                                      am_counter_bytes(n_seq, n_heads));
+    }
     auto* kern = counters ? attn_mfma_kernel<HD, true> : attn_mfma_kernel<HD, false>;
     const int st = launch(kern, dim3(n_heads / G, nch, n_seq), dim3(256), shmem, stream, out,
                           ld_out, q, ld_q, static_cast<const uint16_t*>(k),
@@ -781,7 +837,7 @@ static int attention_decode(float* out, int64_t ld_out, const float* q, int64_t 
                             const void* k, const void* v, int kv_type, int64_t ld_pos,
                             int64_t ld_seq, const int32_t* lens, int n_past, int n_seq,
                             int head_dim, int n_heads, int n_heads_kv, float scale,
-                            void* workspace, size_t ws_bytes, hipStream_t stream) {
+                            const AmScratch& sc, hipStream_t stream) {
     if (n_seq < 0 || head_dim <= 0 || n_heads <= 0 || n_heads_kv <= 0) return JINF_HIP_ERR_INVALID;
     if (n_seq == 0) return JINF_HIP_OK;
     if (!out || !q || !k || !v || n_heads % n_heads_kv != 0) return JINF_HIP_ERR_INVALID;
@@ -814,9 +870,9 @@ static int attention_decode(float* out, int64_t ld_out, const float* q, int64_t 
         const int G = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
         if (head_dim == 64)
             return am_launch<64>(out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq,
-                                 n_heads, group, G, scale, workspace, ws_bytes, stream);
+                                 n_heads, group, G, scale, sc, stream);
         return am_launch<128>(out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq,
-                              n_heads, group, G, scale, workspace, ws_bytes, stream);
+                              n_heads, group, G, scale, sc, stream);
     }
     // fp32 cache: enough (sequence, kv head) pairs: one workgroup per pair,
     // all its query heads (up to 8) together.  Otherwise one query head per
@@ -857,7 +913,58 @@ extern "C" int jinf_attention_decode(float* out, int ld_out, const float* q, int
     if (scale == 0.0f && head_dim > 0) scale = jinf::inv_sqrt_hd(head_dim);
     return jinf::attention_decode(out, ld_out, q, ld_q, k_cache, v_cache, kv_type, ld_pos, ld_seq,
                                   lens, max_ctx, n_seq, head_dim, n_heads, n_heads_kv, scale,
-                                  workspace, workspace_bytes, stream);
+                                  jinf::AmScratch{workspace, workspace_bytes, false}, stream);
+}
+
+namespace jinf {
+
+// This device's address of `scratch`: looked up with hipGetSymbolAddress on
+// the first call made while the device is current, then cached per device.
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> g_scratch_base[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+static int scratch_base(void** base) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        JINF_LOG("jinf_attention_decode_noalloc: no usable current device (%d)", dev);
+        return JINF_HIP_ERR_DEVICE;
+    }
+    void* p = g_scratch_base[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_base[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !p) {
+                JINF_LOG("jinf_attention_decode_noalloc: hipGetSymbolAddress(scratch) on device "
+                         "%d failed: %s", dev, hipGetErrorString(e));
+                return JINF_HIP_ERR_DEVICE;
+            }
+            g_scratch_base[dev].store(p, std::memory_order_release);
+        }
+    }
+    *base = p;
+    return JINF_HIP_OK;
+}
+
+}  // namespace jinf
+
+extern "C" int jinf_attention_decode_noalloc(float* out, int ld_out, const float* q, int ld_q,
+                                             const void* k_cache, const void* v_cache,
+                                             int kv_type, int64_t ld_pos, int64_t ld_seq,
+                                             const int32_t* lens, int n_seq, int max_ctx,
+                                             int head_dim, int n_heads, int n_heads_kv,
+                                             float scale, hipStream_t stream) {
+    if ((!lens && n_seq > 0) || max_ctx < 0) return JINF_HIP_ERR_INVALID;
+    if (n_seq > 1 && ld_seq != 0 && ld_seq < (int64_t)max_ctx * ld_pos) return JINF_HIP_ERR_INVALID;
+    if (scale == 0.0f && head_dim > 0) scale = jinf::inv_sqrt_hd(head_dim);
+    void* base = nullptr;
+    const int st = jinf::scratch_base(&base);
+    if (st != JINF_HIP_OK) return st;
+    return jinf::attention_decode(out, ld_out, q, ld_q, k_cache, v_cache, kv_type, ld_pos, ld_seq,
+                                  lens, max_ctx, n_seq, head_dim, n_heads, n_heads_kv, scale,
+                                  jinf::AmScratch{base, 0, true}, stream);
 }
 
 // Drop-in for cuda/attention_kernel.cu:100-115: one sequence, fp32 cache
@@ -876,7 +983,8 @@ extern "C" void jinf_cuda_attention(float* output, const float* q, const float* 
                                           (int64_t)n_heads * head_dim, k_cache, v_cache,
                                           JINF_HIP_F32, kvw, kvw * (max_ctx > 0 ? max_ctx : n_past),
                                           nullptr, n_past, 1, head_dim, n_heads, n_heads_kv,
-                                          jinf::inv_sqrt_hd(head_dim), nullptr, 0, stream);
+                                          jinf::inv_sqrt_hd(head_dim),
+                                          jinf::AmScratch{nullptr, 0, false}, stream);
     if (st == JINF_HIP_ERR_INVALID)
         JINF_LOG("jinf_cuda_attention: invalid argument (head_dim=%d n_heads=%d n_heads_kv=%d)",
                  head_dim, n_heads, n_heads_kv);

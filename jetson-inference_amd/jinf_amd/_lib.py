@@ -56,6 +56,8 @@ SIGNATURES = {
     "jinf_attention_decode": (_I, [_P, _I, _P, _I, _P, _P, _I, ctypes.c_int64, ctypes.c_int64,
                                    _P, _I, _I, _I, _I, _I, _F, _P, ctypes.c_size_t, _P]),
     "jinf_attention_workspace_bytes": (ctypes.c_size_t, [_I, _I, _I, _I]),
+    "jinf_attention_decode_noalloc": (_I, [_P, _I, _P, _I, _P, _P, _I, ctypes.c_int64,
+                                           ctypes.c_int64, _P, _I, _I, _I, _I, _I, _F, _P]),
     "jinf_rmsnorm_matvec": (_I, [_P, _I, _P, _P, _I, _F, _P, _I, _I, _P]),
     "jinf_matvec_add": (_I, [_P, _I, _P, _P, _I, _I, _P]),
     "jinf_rmsnorm_swiglu_matvec": (_I, [_P, _P, _I, _P, _P, _I, _F, _P, _I, _I, _P]),
