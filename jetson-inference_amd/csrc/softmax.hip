@@ -10,24 +10,34 @@
 // Elements j >= L are neither read nor written.
 //
 // Design: one workgroup per row.  The live part of the row is loaded once into
-// registers (kSmCPT float4 chunks per thread, so up to 32 KiB per row with
-// 256 lanes), exponentiated once, and written once: one HBM read and one write
-// per element, against the reference's three reads and two exp evaluations.
+// registers (CPT float4 chunks per lane: 4 up to 16384 columns, 8 up to 32768),
+// exponentiated once, and written once: one HBM read and one write per
+// element, against the reference's three reads and two exp evaluations.
 // Every chunk's load is issued before any arithmetic, so a row's loads are in
 // flight together.  Max and sum are DPP wave reductions plus one LDS exchange
 // and one barrier each; each aligned group of 4 exponentials is summed in fp32
 // and the group sums in fp64.  Chunks past the row's live length do no
 // arithmetic (whole waves branch over them), so the VALU cost follows the live
 // length, not the padded stride.
-// Measured at config 5 (4096 rows, stride 8192, random len): this form 26 us
-// (63% of 8 TB/s); the earlier one with loads and maxima interleaved per chunk
-// and two-barrier shuffle reductions 30 us.  Also slower: two rows per
-// workgroup sharing the barriers (31 us), 2 or 16 chunks per lane instead of 8
-// (4 equal), longest-first row order, one wave per row, length-scaled waves
-// per row with several short rows per workgroup, loading the first chunk
-// before the length is known.  At uniform 8192-long rows the earlier form
-// reached 74% of 8 TB/s (a plain copy: 75%); ragged rows lose to the per-row
-// latency chain.
+// Grid: (rows per length entry, length entries), so a workgroup finds its
+// length entry from blockIdx.y without an integer division (the earlier
+// 64-bit division sat on every row's critical path, ahead of its loads:
+// 1.2 us of 26.6 at config 5).  Consecutive workgroups are the heads of one
+// sequence, which the round-robin dispatch spreads over all eight XCDs.
+// Measured at config 5 (4096 rows, stride 8192, random len; 130 MB):
+//   2-D grid, 512 lanes x 4 chunks   24.4 us (66% of 8 TB/s; a streaming
+//                                    probe of the same geometry, loads ->
+//                                    one cross-lane exchange -> stores,
+//                                    22.5-23.0 us: 94% of it)
+//   1-D grid with the division       26.6 us (256 x 8: 25.4 us without it)
+//   1024 lanes x 2 chunks            27.9 us
+//   waves without live data leaving before the barriers   25.5 us
+//   one barrier (per-wave max and sum combined)            26.3-30.7 us
+//   longest sequence first (host-sorted order)             24.2 us (probe:
+//                                    unchanged, so the tail is not the cause)
+//   earlier: two rows per workgroup sharing the barriers, one wave per row,
+//   length-scaled waves with several short rows per workgroup, loading the
+//   first chunk before the length is known: all slower.
 // Rows longer than the register capacity (or unaligned rows) take a loop
 // kernel that reads the row three times (max, sum, write) like the reference.
 #include <math.h>
@@ -38,126 +48,114 @@
 
 namespace jinf {
 
-constexpr int kSmCPT = 8;  // float4 chunks per lane kept in registers
+constexpr int kSmMaxGridY = 65535;
 
-__device__ __forceinline__ int live_len(const int32_t* lens, int rows_per_len, int n_cols,
-                                        int64_t row) {
-    if (!lens) return n_cols;
-    int L = lens[row / rows_per_len];
+__device__ __forceinline__ int clamp_len(int L, int n_cols) {
     L = L < 0 ? 0 : L;
     return L > n_cols ? n_cols : L;
 }
 
-// RPW rows per workgroup (rows RPW b .. RPW b + RPW - 1; the launches use 1):
-// their loads are in flight together and their reductions share the
-// workgroup's barriers.
-template <int CPT = kSmCPT, int RPW = 1>
-__global__ __launch_bounds__(1024) void softmax_vec_kernel(
+__device__ __forceinline__ int live_len(const int32_t* lens, int rows_per_len, int n_cols,
+                                        int64_t row) {
+    if (!lens) return n_cols;
+    return clamp_len(lens[(uint32_t)row / (uint32_t)rows_per_len], n_cols);
+}
+
+// One row per workgroup of BS lanes, CPT float4 chunks per lane.  GRID2D:
+// the grid is (rows_per_len, length entries) and row = blockIdx.y *
+// rows_per_len + blockIdx.x; otherwise one dimension of n_rows (length entry
+// by division).  BS is a template argument: with the block size known at
+// compile time the chunk offsets become immediates and the config-5 launch
+// takes 24.5 us instead of 26.2.
+template <int CPT, int BS, bool GRID2D>
+__global__ __launch_bounds__(BS) void softmax_vec_kernel(
     float* out, int ld_out, const float* in, int ld_in, int n_rows, int n_cols,
     const int32_t* lens, int rows_per_len, float scale) {
 #pragma clang fp contract(off)
-    __shared__ float redf[16 * RPW];
-    __shared__ double redd[16 * RPW];
-    const int bs = blockDim.x;
-    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave, nw = bs / kWave;
+    __shared__ float redf[16];
+    __shared__ double redd[16];
+    constexpr int bs = BS;
+    constexpr int nw = BS / kWave;
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     const float ninf = -INFINITY;
-    int L[RPW], nfull[RPW];
-    const float* x[RPW];
-    float* y[RPW];
-#pragma unroll
-    for (int q = 0; q < RPW; ++q) {
-        const int64_t row = (int64_t)blockIdx.x * RPW + q;
-        L[q] = row < n_rows ? live_len(lens, rows_per_len, n_cols, row) : 0;
-        nfull[q] = L[q] >> 2;  // whole float4 chunks
-        x[q] = in + row * ld_in;
-        y[q] = out + row * ld_out;
+    int64_t row;
+    int L;
+    if constexpr (GRID2D) {
+        row = (int64_t)blockIdx.y * rows_per_len + blockIdx.x;
+        L = row < n_rows ? (lens ? clamp_len(lens[blockIdx.y], n_cols) : n_cols) : 0;
+    } else {
+        row = blockIdx.x;
+        L = live_len(lens, rows_per_len, n_cols, row);
     }
+    const int nfull = L >> 2;  // whole float4 chunks
+    const float* x = in + row * ld_in;
+    float* y = out + row * ld_out;
 
     // Chunks at or past L do no arithmetic: whole waves skip them.
-    float v[RPW][CPT][4];
-    float mx[RPW];
+    float v[CPT][4];
+    float mx = ninf;
 #pragma unroll
-    for (int q = 0; q < RPW; ++q) {
-        mx[q] = ninf;
+    for (int j = 0; j < CPT; ++j) {
+        const int c = threadIdx.x + j * bs;
+        if (c < nfull) {
+            Act<float>::load(x + 4 * c, v[j]);
+        } else {
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            const int c = threadIdx.x + j * bs;
-            if (c < nfull[q]) {
-                Act<float>::load(x[q] + 4 * c, v[q][j]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[q][j][e] = (4 * c + e < L[q]) ? x[q][4 * c + e] : ninf;
-            }
+            for (int e = 0; e < 4; ++e) v[j][e] = (4 * c + e < L) ? x[4 * c + e] : ninf;
         }
     }
 #pragma unroll
-    for (int q = 0; q < RPW; ++q)
+    for (int j = 0; j < CPT; ++j) {
+        const int c = threadIdx.x + j * bs;
+        if (4 * c < L) {
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            const int c = threadIdx.x + j * bs;
-            if (4 * c < L[q]) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    v[q][j][e] = v[q][j][e] * scale;  // -inf * scale stays -inf for scale > 0
-                    mx[q] = fmaxf(mx[q], v[q][j][e]);
-                }
+            for (int e = 0; e < 4; ++e) {
+                v[j][e] = v[j][e] * scale;  // -inf * scale stays -inf for scale > 0
+                mx = fmaxf(mx, v[j][e]);
             }
         }
-    // one exchange for every row's maximum
-#pragma unroll
-    for (int q = 0; q < RPW; ++q) {
-        mx[q] = wave_max_f32(mx[q]);
-        if (lane == 0) redf[q * 16 + wid] = mx[q];
     }
+    mx = wave_max_f32(mx);
+    if (lane == 0) redf[wid] = mx;
     __syncthreads();
+    {
+        float m = redf[0];
 #pragma unroll
-    for (int q = 0; q < RPW; ++q) {
-        float m = redf[q * 16];
-        for (int i = 1; i < nw; ++i) m = fmaxf(m, redf[q * 16 + i]);
-        mx[q] = m;
+        for (int i = 1; i < nw; ++i) m = fmaxf(m, redf[i]);
+        mx = m;
     }
-    double sum[RPW];
+    double sum = 0.0;
 #pragma unroll
-    for (int q = 0; q < RPW; ++q) {
-        sum[q] = 0.0;
+    for (int j = 0; j < CPT; ++j) {
+        const int c = threadIdx.x + j * bs;
+        if (4 * c < L) {
+            float part = 0.0f;
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            const int c = threadIdx.x + j * bs;
-            if (4 * c < L[q]) {
-                float part = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float ex = 4 * c + e < L[q] ? exp_neg(v[q][j][e] - mx[q]) : 0.0f;
-                    v[q][j][e] = ex;
-                    part += ex;
-                }
-                sum[q] += (double)part;
+            for (int e = 0; e < 4; ++e) {
+                const float ex = 4 * c + e < L ? exp_neg(v[j][e] - mx) : 0.0f;
+                v[j][e] = ex;
+                part += ex;
             }
+            sum += (double)part;
         }
     }
-#pragma unroll
-    for (int q = 0; q < RPW; ++q) {
-        sum[q] = wave_sum_f64(sum[q]);
-        if (lane == 0) redd[q * 16 + wid] = sum[q];
-    }
+    sum = wave_sum_f64(sum);
+    if (lane == 0) redd[wid] = sum;
     __syncthreads();
+    double t = redd[0];
 #pragma unroll
-    for (int q = 0; q < RPW; ++q) {
-        double t = redd[q * 16];
-        for (int i = 1; i < nw; ++i) t += redd[q * 16 + i];
-        const float inv = 1.0f / (float)t;
+    for (int i = 1; i < nw; ++i) t += redd[i];
+    const float inv = 1.0f / (float)t;
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            const int c = threadIdx.x + j * bs;
-            if (c < nfull[q]) {
-                const float o[4] = {v[q][j][0] * inv, v[q][j][1] * inv, v[q][j][2] * inv,
-                                    v[q][j][3] * inv};
-                Act<float>::store(y[q] + 4 * c, o);
-            } else if (4 * c < L[q]) {
+    for (int j = 0; j < CPT; ++j) {
+        const int c = threadIdx.x + j * bs;
+        if (c < nfull) {
+            const float o[4] = {v[j][0] * inv, v[j][1] * inv, v[j][2] * inv, v[j][3] * inv};
+            Act<float>::store(y + 4 * c, o);
+        } else if (4 * c < L) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (4 * c + e < L[q]) y[q][4 * c + e] = v[q][j][e] * inv;
-            }
+            for (int e = 0; e < 4; ++e)
+                if (4 * c + e < L) y[4 * c + e] = v[j][e] * inv;
         }
     }
 }
@@ -194,13 +192,30 @@ static int softmax_dispatch(float* out, int ld_out, const float* in, int ld_in, 
     if (lens && rows_per_len <= 0) return JINF_HIP_ERR_INVALID;
     if (!(scale > 0.0f) || !isfinite(scale)) return JINF_HIP_ERR_INVALID;
     const bool vec = aligned(out, 16) && aligned(in, 16) && ld_out % 4 == 0 && ld_in % 4 == 0;
-    const int nch = (n_cols + 3) / 4;
-    int bs = round_up((nch + kSmCPT - 1) / kSmCPT, kWave);
-    if (bs < 256 && n_cols > 256) bs = 256;
-    if (bs < kWave) bs = kWave;
-    if (vec && bs <= 1024)
-        return launch(softmax_vec_kernel<kSmCPT, 1>, dim3(n_rows), dim3(bs), 0, stream, out,
-                      ld_out, in, ld_in, n_rows, n_cols, lens, rows_per_len, scale);
+    // lanes x chunks per lane: 64 x 4 up to 256 columns (1024 fit), 256 x 4
+    // up to 4096, 512 x 4 up to 8192, 1024 x 4 up to 16384, 1024 x 8 up to
+    // 32768
+    if (vec && n_cols <= 32768) {
+        const int rpl = lens ? rows_per_len : n_rows;
+        const int64_t groups = ((int64_t)n_rows + rpl - 1) / rpl;
+        const bool g2 = groups <= kSmMaxGridY;
+        const dim3 grid = g2 ? dim3((unsigned)(rpl < n_rows ? rpl : n_rows), (unsigned)groups)
+                             : dim3((unsigned)n_rows);
+        auto go = [&](auto k2d, auto k1d, int bs) {
+            return launch(g2 ? k2d : k1d, grid, dim3(bs), 0, stream, out, ld_out, in, ld_in,
+                          n_rows, n_cols, lens, rpl, scale);
+        };
+        if (n_cols <= 256)
+            return go(softmax_vec_kernel<4, 64, true>, softmax_vec_kernel<4, 64, false>, 64);
+        if (n_cols <= 4096)
+            return go(softmax_vec_kernel<4, 256, true>, softmax_vec_kernel<4, 256, false>, 256);
+        if (n_cols <= 8192)
+            return go(softmax_vec_kernel<4, 512, true>, softmax_vec_kernel<4, 512, false>, 512);
+        if (n_cols <= 16384)
+            return go(softmax_vec_kernel<4, 1024, true>, softmax_vec_kernel<4, 1024, false>,
+                      1024);
+        return go(softmax_vec_kernel<8, 1024, true>, softmax_vec_kernel<8, 1024, false>, 1024);
+    }
     const int lbs = n_cols >= 1024 ? 1024 : round_up(n_cols, kWave);
     return launch(softmax_loop_kernel, dim3(n_rows), dim3(lbs), 0, stream, out, ld_out, in,
                   ld_in, n_cols, lens, rows_per_len, scale);

@@ -89,3 +89,28 @@ def test_all_masked_rows_noop_and_length_one(dev):
     got = host(out)
     assert np.all(got[0] == 7.0) and np.all(got[3] == 7.0)
     assert got[1, 0] == 1.0 and got[2, 0] == 1.0 and np.all(got[1:3, 1:] == 7.0)
+
+
+@pytest.mark.parametrize("n_rows,rows_per_len,n_cols", [
+    (70, 8, 4096),       # last length entry covers 6 rows only
+    (5, 100, 512),       # one entry, more rows per entry than rows
+    (65537, 1, 64),      # more entries than a grid dimension holds: 1-D grid
+    (12, 3, 16384),      # 1024 lanes x 4 chunks
+    (6, 2, 256),         # 64 lanes
+    (9, 9, 20000),       # 1024 lanes x 8 chunks, length entries past 16384
+])
+def test_grid_shapes(dev, n_rows, rows_per_len, n_cols):
+    say(f"{n_rows} rows, {rows_per_len} rows per length, {n_cols} columns")
+    r = tu.rng(n_rows + n_cols)
+    x = tu.normal(r, (n_rows, n_cols), 0.0, 3.0, np.float32)
+    n_len = -(-n_rows // rows_per_len)
+    lens = r.integers(0, n_cols + 2, size=n_len).astype(np.int32)
+    lens[0] = n_cols
+    ref = oracle.softmax_rows(x, lens, rows_per_len, 1.0, out=np.full_like(x, np.nan))
+    xd = to_dev(x)
+    out = torch.full_like(xd, float("nan"))
+    jinf_amd.softmax_rows(xd, to_dev(lens), rows_per_len, 1.0, out=out)
+    got = host(out)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    live = ~np.isnan(ref)
+    tu.assert_f32_close(got[live], ref[live], 1e-5, 1e-30, "grid shapes")
