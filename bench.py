@@ -8,18 +8,26 @@ the path:
     norm     fused residual add + RMSNorm fp16 [2048, 4096], eps 1e-5
     swiglu   silu(gate) * up fp16 [2048, 14336]
     gather   Q4_0 token-embedding gather 4096 ids of 128256 x 4096 -> fp16
-`--workload llama3-70b-decode` runs config 5 (64 sequences: residual+RMSNorm,
-RoPE 64/8 heads, masked fp32 softmax over len = pos + 1, SwiGLU, residual add).
+and the same run also times config 5, the Llama-3-70B decode chain for 64
+sequences (residual+RMSNorm, RoPE 64/8 heads, masked fp32 softmax over
+len = pos + 1, SwiGLU, residual add), reported under "config5".
+`--workload llama3-70b-decode` runs config 5 alone.
 
 value = algorithmic bytes of a step / GPU time of a step (GB/s).  Algorithmic
 bytes count every input read once and every output written once.  Inputs are
 resident in HBM before timing; each kernel rotates over enough buffer sets
-(>= 512 MiB per kernel) that no launch can be served from the 256 MB
-Infinity Cache.  Times come from HIP events on the stream the kernels run on:
-the K steps are captured as one HIP graph and the replay is bracketed by two
-events (ms_per_step); each kernel's average launch duration is timed the same
-way over K back-to-back launches of that kernel alone (kernels.*.us,
-roofline.avg_launch_us).
+(>= 512 MiB of distinct memory per kernel) that no launch can be served from
+the 256 MB Infinity Cache.  Times come from HIP events on the stream the
+kernels run on: the K steps are captured as one HIP graph and the replay is
+bracketed by two events (ms_per_step); each kernel's average launch duration
+is timed the same way over max(K, --kernel-launches) back-to-back launches of
+that kernel alone in one graph (kernels.*.us, roofline.avg_launch_us), so the
+graph's own start-up cost is spread over as many launches as a decode loop
+would run.
+
+Ceilings: every kernel is timed beside a bandwidth probe (include/jinf/
+probe_hip.h) that moves the same bytes in the same launch geometry with no
+arithmetic; kernels.*.frac_of_ceiling = probe time / kernel time.
 
 Prints ONE JSON line (rank 0).  `--gpus N` with N > 1 exits: this build runs
 on one GPU.
@@ -50,24 +58,39 @@ def log(msg):
 
 class Kernel:
     """One kernel of a step: its launch closures over rotating buffer sets,
-    algorithmic bytes and rows per launch, and (for the CPU baseline) the
-    tensors of set 0 with the oracle call that computes the same thing."""
+    algorithmic bytes and rows per launch, the bandwidth probe of each set
+    (the same bytes in the same geometry, no arithmetic), and (for the CPU
+    baseline) the tensors of set 0 with the oracle call that computes the
+    same thing."""
 
-    def __init__(self, name, nbytes, rows, row_unit, launches, hip_name, set0=(), cpu=None):
+    def __init__(self, name, nbytes, rows, row_unit, launches, hip_name, set0=(), cpu=None,
+                 probes=None, probe_name=None):
         self.name, self.nbytes, self.rows, self.row_unit = name, nbytes, rows, row_unit
         self.launches, self.hip_name = launches, hip_name
         self.set0, self.cpu = set0, cpu
+        self.probes, self.probe_name = probes, probe_name
+        # probe variants tried for the ceiling: (units per lane, cross-lane exchange)
+        self.probe_upls = ((1, True), (2, True), (4, True), (1, False), (2, False), (4, False))
+        self.key = name              # unique name across the run (CPU baseline)
         self.i = 0
         self.ms = 0.0
         self.n = 0
+        self.ceil_ms = None
+        self.ceil_upl = None
 
-    def run(self):
-        self.launches[self.i % len(self.launches)]()
+    def run(self, probe=0):
+        """One launch over the next buffer set: the kernel, or (probe = a
+        (units per lane, exchange) variant) its bandwidth probe."""
+        if probe:
+            self.probes[self.i % len(self.probes)](probe)
+        else:
+            self.launches[self.i % len(self.launches)]()
         self.i += 1
 
 
-def n_sets(bytes_per_set):
-    return max(2, -(-ROTATE_BYTES // bytes_per_set))
+def n_sets(footprint_bytes):
+    """Buffer sets whose distinct memory together covers ROTATE_BYTES."""
+    return max(2, -(-ROTATE_BYTES // footprint_bytes))
 
 
 def randn16(torch, shape, mu, sigma, g):
@@ -86,54 +109,62 @@ def q4_0_table(torch, n_vocab, n_embd, g):
 
 def build_rope(torch, jinf, g, T, nh, nkv, hd, positions, keep):
     nbytes = T * (nh + nkv) * hd * 2 * 2 + T * 4
-    sets = []
-    for _ in range(n_sets(nbytes)):
+    sets, probes = [], []
+    for _ in range(n_sets(T * (nh + nkv) * hd * 2)):
         q = randn16(torch, (T, nh * hd), 0.0, 1.0, g)
         k = randn16(torch, (T, nkv * hd), 0.0, 1.0, g)
         p = positions.clone()
         keep.append((q, k, p))
         sets.append(lambda q=q, k=k, p=p: jinf.rope_rows(q, k, hd, p, 0, 500000.0))
+        probes.append(lambda u, q=q, k=k: jinf.ops.probe_rows_inplace(q, k, *u))
     return Kernel("rope", nbytes, T, "token rows", sets, "rope_vec_kernel", keep[-len(sets)],
-                  lambda o, q, k, p: o.rope_rows(q, k, hd, p, 0, 500000.0))
+                  lambda o, q, k, p: o.rope_rows(q, k, hd, p, 0, 500000.0),
+                  probes, "probe_rows_inplace_kernel")
 
 
 def build_norm(torch, jinf, g, T, H, keep):
     nbytes = 4 * T * H * 2 + H * 2
-    sets = []
-    for _ in range(n_sets(nbytes)):
+    sets, probes = [], []
+    for _ in range(n_sets(3 * T * H * 2)):
         r = randn16(torch, (T, H), 0.0, 1.0, g)
         x = randn16(torch, (T, H), 0.0, 1.0, g)
         w = randn16(torch, (H,), 1.0, 0.05, g)
         y = torch.empty_like(x)
         keep.append((r, x, w, y))
         sets.append(lambda r=r, x=x, w=w, y=y: jinf.residual_rmsnorm_rows(r, x, w, 1e-5, out=y))
+        probes.append(lambda u, r=r, x=x, y=y: jinf.ops.probe_stream(r, r, y, x, *u))
     return Kernel("residual_rmsnorm", nbytes, T, "token rows", sets, "rmsnorm_vec_kernel",
-                  keep[-len(sets)][:3], lambda o, r, x, w: o.residual_rmsnorm_rows(r, x, w, 1e-5))
+                  keep[-len(sets)][:3], lambda o, r, x, w: o.residual_rmsnorm_rows(r, x, w, 1e-5),
+                  probes, "probe_stream_kernel")
 
 
 def build_swiglu(torch, jinf, g, T, F, keep):
     nbytes = 3 * T * F * 2
-    sets = []
+    sets, probes = [], []
     for _ in range(n_sets(nbytes)):
         gt = randn16(torch, (T, F), 0.0, 2.0, g)
         up = randn16(torch, (T, F), 0.0, 2.0, g)
         o = torch.empty_like(gt)
         keep.append((gt, up, o))
         sets.append(lambda gt=gt, up=up, o=o: jinf.swiglu(gt, up, out=o))
+        probes.append(lambda u, gt=gt, up=up, o=o: jinf.ops.probe_stream(o, gt, None, up, *u))
     return Kernel("swiglu", nbytes, T, "token rows", sets, "ew_vec_kernel",
-                  keep[-len(sets)][:2], lambda o, gt, up: o.swiglu(gt, up))
+                  keep[-len(sets)][:2], lambda o, gt, up: o.swiglu(gt, up),
+                  probes, "probe_stream_kernel")
 
 
 def build_residual_add(torch, jinf, g, T, H, keep):
     nbytes = 3 * T * H * 2
-    sets = []
-    for _ in range(n_sets(nbytes)):
+    sets, probes = [], []
+    for _ in range(n_sets(2 * T * H * 2)):
         a = randn16(torch, (T, H), 0.0, 1.0, g)
         b = randn16(torch, (T, H), 0.0, 1.0, g)
         keep.append((a, b))
         sets.append(lambda a=a, b=b: jinf.residual_add(a, b))
+        probes.append(lambda u, a=a, b=b: jinf.ops.probe_stream(a, a, None, b, *u))
     return Kernel("residual_add", nbytes, T, "token rows", sets, "ew_vec_kernel",
-                  keep[-len(sets)], lambda o, a, b: o.residual_add(a, b))
+                  keep[-len(sets)], lambda o, a, b: o.residual_add(a, b),
+                  probes, "probe_stream_kernel")
 
 
 def build_gather(torch, jinf, g, n_vocab, n_embd, n_ids, keep):
@@ -141,17 +172,19 @@ def build_gather(torch, jinf, g, n_vocab, n_embd, n_ids, keep):
     nbytes = n_ids * row_bytes + n_ids * 4 + n_ids * n_embd * 2
     tables = [q4_0_table(torch, n_vocab, n_embd, g) for _ in range(2)]
     keep.append(tables)
-    sets = []
+    sets, probes = [], []
     for i in range(n_sets(n_ids * n_embd * 2)):
         ids = torch.randint(0, n_vocab, (n_ids,), generator=g, device="cuda", dtype=torch.int32)
         o = torch.empty((n_ids, n_embd), dtype=torch.float16, device="cuda")
         t = tables[i % 2]
         keep.append((ids, o))
         sets.append(lambda t=t, ids=ids, o=o: jinf.embed_q4_0(t, ids, n_embd, torch.float16, out=o))
+        probes.append(lambda u, t=t, ids=ids, o=o: jinf.ops.probe_gather(o, t, ids, row_bytes, *u))
     import numpy as np
     return Kernel("q4_0_gather", nbytes, n_ids, "token ids", sets, "embed_q4_0_kernel",
                   (tables[0], keep[-len(sets)][0]),
-                  lambda o, t, ids: o.embed_q4_0(t, ids, n_embd, np.float16))
+                  lambda o, t, ids: o.embed_q4_0(t, ids, n_embd, np.float16),
+                  probes, "probe_gather_kernel")
 
 
 def build_softmax(torch, jinf, g, n_seq, n_heads, max_len, keep):
@@ -160,16 +193,20 @@ def build_softmax(torch, jinf, g, n_seq, n_heads, max_len, keep):
     live = int(lens.sum().item())
     nbytes = 8 * n_heads * live + n_seq * 4
     foot = n_seq * n_heads * max_len * 4 * 2
-    sets = []
+    sets, probes = [], []
     for _ in range(n_sets(foot)):
         s = torch.randn((n_seq * n_heads, max_len), generator=g, device="cuda") * 3.0
         o = torch.empty_like(s)
         lc = lens.clone()
         keep.append((s, o, lc))
         sets.append(lambda s=s, o=o, lc=lc: jinf.softmax_rows(s, lc, n_heads, 1.0, out=o))
-    return Kernel("masked_softmax", nbytes, n_seq * n_heads, "score rows", sets,
-                  "softmax_vec_kernel", (keep[-len(sets)][0], lens),
-                  lambda o, s, lc: o.softmax_rows(s, lc, n_heads, 1.0))
+        probes.append(lambda u, s=s, o=o, lc=lc: jinf.ops.probe_rows_ragged(o, s, lc, n_heads))
+    k = Kernel("masked_softmax", nbytes, n_seq * n_heads, "score rows", sets,
+               "softmax_vec_kernel", (keep[-len(sets)][0], lens),
+               lambda o, s, lc: o.softmax_rows(s, lc, n_heads, 1.0),
+               probes, "probe_rows_ragged_kernel")
+    k.probe_upls = ((4, True),)  # the softmax's own 4 units per lane
+    return k
 
 
 def build_attention(torch, jinf, g, name, n_seq, max_ctx, nh, nkv, hd, lens, kv_dtype, keep):
@@ -236,6 +273,22 @@ def build_matvec(torch, jinf, g, name, rows, cols, keep, qtype=2):
                   keep[-len(sets)][:2], lambda o, W, x: o.matvec(qtype, W, x))
 
 
+def config5(torch, jinf, g, keep):
+    """the Llama-3-70B decode chain for 64 sequences."""
+    pos = torch.randint(0, 8192, (64,), generator=g, device="cuda", dtype=torch.int32)
+    ks = [build_norm(torch, jinf, g, 64, 8192, keep),
+          build_rope(torch, jinf, g, 64, 64, 8, 128, pos, keep),
+          build_softmax(torch, jinf, g, 64, 64, 8192, keep),
+          build_swiglu(torch, jinf, g, 64, 28672, keep),
+          build_residual_add(torch, jinf, g, 64, 8192, keep)]
+    for k in ks:
+        k.key = "config5_" + k.name
+    cfg = {"workload": "llama3-70b-decode", "shapes": "Llama-3-70B decode, 64 sequences: hidden "
+           "8192, 64/8 heads x 128, FFN 28672, score rows 4096 x stride 8192, len = pos + 1, "
+           "pos ~ U[0, 8192)", "storage": "f16 activations, f32 scores", "baseline_configs": [5]}
+    return ks, cfg
+
+
 def workload(name, torch, jinf, seed):
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
@@ -250,15 +303,20 @@ def workload(name, torch, jinf, seed):
                "vocab 128256; RoPE T=512, norm/SwiGLU T=2048, 4096 token ids",
                "storage": "f16 activations, Q4_0 table", "baseline_configs": [2, 3, 4]}
     elif name == "llama3-70b-decode":
-        pos = torch.randint(0, 8192, (64,), generator=g, device="cuda", dtype=torch.int32)
-        ks = [build_norm(torch, jinf, g, 64, 8192, keep),
-              build_rope(torch, jinf, g, 64, 64, 8, 128, pos, keep),
-              build_softmax(torch, jinf, g, 64, 64, 8192, keep),
-              build_swiglu(torch, jinf, g, 64, 28672, keep),
-              build_residual_add(torch, jinf, g, 64, 8192, keep)]
-        cfg = {"workload": name, "shapes": "Llama-3-70B decode, 64 sequences: hidden 8192, "
-               "64/8 heads x 128, FFN 28672, score rows 4096 x stride 8192, len = pos + 1",
-               "storage": "f16 activations, f32 scores", "baseline_configs": [5]}
+        ks, cfg = config5(torch, jinf, g, keep)
+    elif name == "calibrate":
+        # the bandwidth probes of configs 2-5 alone (for a rocprof summary)
+        k8, _ = config5(torch, jinf, g, keep)
+        ks = [build_rope(torch, jinf, g, 512, 32, 8, 128,
+                         torch.arange(512, dtype=torch.int32, device="cuda"), keep),
+              build_norm(torch, jinf, g, 2048, 4096, keep),
+              build_swiglu(torch, jinf, g, 2048, 14336, keep),
+              build_gather(torch, jinf, g, 128256, 4096, 4096, keep)] + k8
+        for k in ks:  # every probe variant, one after the other
+            k.launches = [lambda f=f, u=u: f(u) for u in k.probe_upls for f in k.probes]
+            k.hip_name = k.probe_name
+        cfg = {"workload": name, "shapes": "the bandwidth probes of BASELINE configs 2-5",
+               "baseline_configs": [2, 3, 4, 5]}
     elif name == "llama3-8b-gemv":
         H, F, KV = 4096, 14336, 1024
         ks = [build_matvec(torch, jinf, g, "gemv_q", H, H, keep),
@@ -645,12 +703,13 @@ def engine_bench(args, torch, jinf_amd):
 # --------------------------------------------------------------------------
 
 def cpu_baseline(ks, threads, budget_s):
+    """Median seconds per run of every kernel's oracle call at `threads`
+    threads, on host copies of buffer set 0, within about budget_s."""
     sys.path.insert(0, ROOT)
     import oracle
 
     oracle.set_threads(threads)
-    per = {}
-    total_s = 0.0
+    out = {}
     for k in ks:
         arrays = [t.cpu().numpy() for t in k.set0]
         fn = lambda: k.cpu(oracle, *arrays)  # noqa: E731
@@ -663,13 +722,55 @@ def cpu_baseline(ks, threads, budget_s):
             times.append(time.perf_counter() - t0)
             if time.perf_counter() > t_end and len(times) >= 3:
                 break
-        med = sorted(times)[len(times) // 2]
-        per[k.name] = {"GB/s": k.nbytes / med / 1e9, "runs": len(times)}
-        total_s += med
-    step_bytes = sum(k.nbytes for k in ks)
-    return {"value": round(step_bytes / total_s / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "per_kernel_GBs": {n: round(v["GB/s"], 3) for n, v in per.items()},
-            "runs": {n: v["runs"] for n, v in per.items()}, "s_per_step": round(total_s, 5)}
+        out[k.key] = (sorted(times)[len(times) // 2], len(times))
+    oracle.set_threads(1)
+    return out
+
+
+def host_threads(args):
+    """(threads of the all-cores run, cores this process may use)."""
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = os.cpu_count() or 1
+    return (args.cpu_threads or min(16, aff)), aff
+
+
+def cpu_baseline_both(ks, ks70, args):
+    """The oracle timed at 1 thread (the reference's CPU code is
+    single-threaded) and at every core this run may use (at most 16, the GPU
+    box's share for one GPU), for the step's kernels and config 5's."""
+    n_all, aff = host_threads(args)
+    budget = args.cpu_seconds / 2
+    runs = {1: cpu_baseline(ks + ks70, 1, budget), n_all: cpu_baseline(ks + ks70, n_all, budget)}
+
+    def rate(kl, t):
+        sec = sum(runs[t][k.key][0] for k in kl)
+        return round(sum(k.nbytes for k in kl) / sec / 1e9, 3), round(sec, 5)
+
+    def per(t):
+        return {k.key: round(k.nbytes / runs[t][k.key][0] / 1e9, 3) for k in ks + ks70}
+
+    v_all, s_all = rate(ks, n_all)
+    v_one, s_one = rate(ks, 1)
+    out = {"value": v_all, "unit": "GB/s", "cores": n_all, "kind": "port",
+           "s_per_step": s_all, "per_kernel_GBs": per(n_all),
+           "single_thread": {"value": v_one, "unit": "GB/s", "cores": 1, "s_per_step": s_one,
+                             "per_kernel_GBs": per(1)},
+           "runs": {k.key: [runs[1][k.key][1], runs[n_all][k.key][1]] for k in ks + ks70},
+           "host_cores": os.cpu_count(), "usable_cores": aff,
+           "cpu_model": cpu_model(), "cpu_info": cpu_info(),
+           "sample": (f"every kernel of the step (configs 2-4) and of config 5 at full shape on "
+                      f"a host copy of buffer set 0; median of >= 3 runs after a warm-up, about "
+                      f"{budget:.0f} s per thread count; oracle C restatement (-O3 -march="
+                      f"x86-64-v3, no FMA contraction, no fast-math), 1 thread and {n_all} "
+                      f"OpenMP threads")}
+    if ks70:
+        c1, _ = rate(ks70, 1)
+        cn, _ = rate(ks70, n_all)
+        out["config5"] = {"value": cn, "cores": n_all, "single_thread_value": c1,
+                          "unit": "GB/s"}
+    return out
 
 
 # --------------------------------------------------------------------------
@@ -756,24 +857,30 @@ def rocprof_summary(dbs, bytes_per_kernel, steps=0):
         # the copy calibration is the largest-grid blit; torch's small copies share its name
         big = c.execute("select max(grid_x * grid_y * grid_z) from kernels "
                         "where name like '%copyBuffer%'").fetchone()[0] or 0
-        for name, n, avg, mn, mx in c.execute(
-                "select name, count(*), avg(duration), min(duration), max(duration) from kernels "
-                "where name not like '%copyBuffer%' or grid_x * grid_y * grid_z = ? "
-                "group by name", (big,)):
-            key = short_kernel(name)
+        # the probes of several kernels share one kernel name: they are told
+        # apart by their grid size (work-items)
+        for name, gs, n, avg, mn, mx in c.execute(
+                "select name, grid_x * grid_y * grid_z, count(*), avg(duration), min(duration), "
+                "max(duration) from kernels where name not like '%copyBuffer%' "
+                "or grid_x * grid_y * grid_z = ? group by name, grid_x, grid_y, grid_z", (big,)):
+            key = probe_key(short_kernel(name), gs)
             if key:
-                durs.setdefault(key, (n, avg, mn, mx))
+                if key in durs:  # one key, several grids: merge (dispatch-weighted)
+                    n0, a0, m0, x0 = durs[key]
+                    durs[key] = (n0 + n, (a0 * n0 + avg * n) / (n0 + n), min(m0, mn), max(x0, mx))
+                else:
+                    durs[key] = (n, avg, mn, mx)
         try:
-            rows = c.execute("select kernel_name, counter_name, avg(value), count(*) from "
-                             "counters_collection where kernel_name not like '%copyBuffer%' "
-                             "or grid_size = ? group by kernel_name, counter_name",
+            rows = c.execute("select kernel_name, grid_size, counter_name, avg(value), count(*) "
+                             "from counters_collection where kernel_name not like '%copyBuffer%' "
+                             "or grid_size = ? group by kernel_name, grid_size, counter_name",
                              (big,)).fetchall()
         except sqlite3.OperationalError:
             rows = []
-        for name, cn, v, n in rows:
-            key = short_kernel(name)
+        for name, gs, cn, v, n in rows:
+            key = probe_key(short_kernel(name), gs)
             if key:
-                ctrs[(key, cn)] = (v, n)
+                ctrs.setdefault((key, cn), (v, n))
     if steps:
         lines += per_step_table(dbs, steps)
     lines.append("kernel durations (rocprofv3 --kernel-trace), microseconds:")
@@ -826,6 +933,11 @@ _KERNEL_KEYS = [("ew_vec_kernel<unsigned short, 1", "swiglu"),
                 ("attn_combine_kernel", "gqa_attention_combine"),
                 ("attn_decode_any_kernel", "gqa_attention_generic"),
                 ("copyBuffer", "copy_calibration"),
+                ("probe_rows_inplace_kernel", "probe_rows_inplace"),
+                ("probe_stream_kernel", "probe_stream"),
+                ("probe_gather_kernel", "probe_gather"),
+                ("probe_rows_ragged_kernel", "probe_rows_ragged"),
+                ("am_clear_kernel", "attention counter clear"),
                 # batched decode: matvec_batch_kernel<qtype, M-tiles, epilogue, tiles, waves, k-parts>
                 ("matvec_batch_kernel<2, 1, 3,", "batch qkv+rope (Q4_0)"),
                 ("matvec_batch_kernel<2, 1, 1,", "batch o/down+residual (Q4_0)"),
@@ -836,6 +948,13 @@ _KERNEL_KEYS = [("ew_vec_kernel<unsigned short, 1", "swiglu"),
                 ("bat_argmax", "batch argmax"),
                 ("bat_begin_kernel", "batch step begin"),
                 ("bat_embed", "batch embedding")]
+
+
+def probe_key(key, grid_items):
+    """Probe kernels are labelled with their grid size in work-items."""
+    if key and key.startswith("probe"):
+        return f"{key} [{grid_items} items]"
+    return key
 
 
 def short_kernel(name):
@@ -856,9 +975,16 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--prompt-tokens", type=int, default=512,
                     help="engine workloads: tokens of the timed prompt (0 = no prompt timing)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0,
-                    help="bounded CPU-baseline sample (0 = skip)")
-    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, host cores)")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0,
+                    help="bounded CPU-baseline sample, split over the 1-thread and the "
+                         "all-threads runs (0 = skip)")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="threads of the all-cores CPU run (0 = the host cores this process "
+                         "may use, at most 16: the GPU box's share for one GPU)")
+    ap.add_argument("--kernel-launches", type=int, default=200,
+                    help="back-to-back launches timed per kernel (at least --steps)")
+    ap.add_argument("--no-config5", action="store_true",
+                    help="default workload: skip the config-5 (70B decode chain) measurement")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch eagerly instead of replaying a captured HIP graph")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -900,36 +1026,46 @@ def main():
         engine_bench(args, torch, jinf_amd)
         return
     ks, cfg, keep = workload(args.workload, torch, jinf_amd, args.seed)
+    # the default run also measures config 5 (the 70B decode chain)
+    ks70 = []
+    if args.workload == "llama3-8b-layer" and not args.no_config5:
+        g70 = torch.Generator(device="cuda")
+        g70.manual_seed(args.seed + 5)
+        ks70, cfg70 = config5(torch, jinf_amd, g70, keep)
     torch.cuda.synchronize()
-    log("buffers ready: " + ", ".join(f"{k.name} x{len(k.launches)} sets" for k in ks))
+    log("buffers ready: " + ", ".join(f"{k.name} x{len(k.launches)} sets"
+                                      for k in ks + ks70))
 
     for _ in range(args.warmup):
-        for k in ks:
+        for k in ks + ks70:
             k.run()
+            if k.probes and args.workload != "calibrate":
+                for u in k.probe_upls:
+                    k.run(probe=u)
     torch.cuda.synchronize()
 
     # The K timed steps are captured into one HIP graph and replayed once: the
     # GPU then runs the kernels back to back, as an engine's captured decode
     # step would, and Python launch overhead is out of the measurement.
     # --no-graph launches them eagerly on the stream instead.
-    def record(n_steps, kernels):
+    def record(n_steps, kernels, probe):
         for _ in range(n_steps):
             for k in kernels:
-                k.run()
+                k.run(probe)
 
-    def timed(n_steps, kernels):
+    def timed(n_steps, kernels, probe=0):
         """GPU ms for n_steps passes over `kernels` (HIP events on the stream)."""
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         if args.no_graph:
             torch.cuda.synchronize()
             start.record()
-            record(n_steps, kernels)
+            record(n_steps, kernels, probe)
             end.record()
         else:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                record(n_steps, kernels)
+                record(n_steps, kernels, probe)
             g.replay()  # untimed: first replay uploads the graph
             torch.cuda.synchronize()
             start.record()
@@ -941,45 +1077,66 @@ def main():
     t0 = time.perf_counter()
     total_ms = timed(args.steps, ks)
     wall = time.perf_counter() - t0
-    # per-kernel average launch duration: each kernel alone, K launches back to
-    # back over its rotating buffer sets, same event method
-    for k in ks:
-        k.ms = timed(args.steps, [k])
-        k.n = args.steps
+    chain_ms = timed(args.steps, ks70) / args.steps if ks70 else None
+    # per-kernel average launch duration: each kernel alone, L launches back to
+    # back over its rotating buffer sets, same event method; its probe likewise
+    n_launch = max(args.steps, args.kernel_launches)
+    for k in ks + ks70:
+        k.ms = timed(n_launch, [k])
+        k.n = n_launch
+        if k.probes and args.workload != "calibrate":
+            # the ceiling: the fastest probe variant
+            for u in k.probe_upls:
+                ms = timed(n_launch, [k], probe=u)
+                if k.ceil_ms is None or ms < k.ceil_ms:
+                    k.ceil_ms, k.ceil_upl = ms, u
     ms_step = total_ms / args.steps
     step_bytes = sum(k.nbytes for k in ks)
-    kern_ms = sum(k.ms for k in ks) / args.steps
+    kern_ms = sum(k.ms / k.n for k in ks)
 
-    per = {}
-    for k in ks:
-        us = k.ms / k.n * 1e3
-        gbs = k.nbytes / (us * 1e-6) / 1e9
-        per[k.name] = {"us": round(us, 3), "GB/s": round(gbs, 1),
-                       "frac_of_8TBs": round(gbs / PEAK_GBS, 4),
-                       "rows_per_s": round(k.rows / (us * 1e-6), 1), "row_unit": k.row_unit,
-                       "bytes": k.nbytes, "sets": len(k.launches)}
+    def per_kernel(kl):
+        per = {}
+        for k in kl:
+            us = k.ms / k.n * 1e3
+            gbs = k.nbytes / (us * 1e-6) / 1e9
+            e = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac_of_8TBs": round(gbs / PEAK_GBS, 4),
+                 "rows_per_s": round(k.rows / (us * 1e-6), 1), "row_unit": k.row_unit,
+                 "bytes": k.nbytes, "sets": len(k.launches), "launches_timed": k.n}
+            if k.ceil_ms is not None:
+                cus = k.ceil_ms / k.n * 1e3
+                e.update({"ceiling_us": round(cus, 3),
+                          "ceiling_GB/s": round(k.nbytes / (cus * 1e-6) / 1e9, 1),
+                          "frac_of_ceiling": round(cus / us, 4), "ceiling_probe": k.probe_name,
+                          "ceiling_units_per_lane": k.ceil_upl[0],
+                          "ceiling_exchange": k.ceil_upl[1]})
+            per[k.name] = e
+        return per
+
+    per = per_kernel(ks)
     dom = max(ks, key=lambda k: k.ms)
     dom_us = dom.ms / dom.n * 1e3
     dom_gbs = dom.nbytes / (dom_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "kernel": dom.name, "hip_kernel": dom.hip_name,
                 "achieved": round(dom_gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom_gbs / PEAK_GBS, 4), "bytes_per_launch": dom.nbytes,
-                "avg_launch_us": round(dom_us, 3),
+                "avg_launch_us": round(dom_us, 3), "launches_timed": dom.n,
                 "traffic": traffic_from_profiles(dom.name, args.workload)}
+    c5 = None
+    if ks70:
+        b70 = sum(k.nbytes for k in ks70)
+        c5 = dict(cfg70, chain_us=round(chain_ms * 1e3, 3), chain_bytes=b70,
+                  **{"chain_GB/s": round(b70 / (chain_ms * 1e-3) / 1e9, 1),
+                     "chain_frac_of_8TBs": round(b70 / (chain_ms * 1e-3) / 1e9 / PEAK_GBS, 4)},
+                  launch="HIP graph of the K chain steps, replayed once",
+                  kernels=per_kernel(ks70))
 
     if args.calibrate_copy:
         calibrate_copy(torch)
 
     cpu = None
-    if args.cpu_seconds > 0:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    if args.cpu_seconds > 0 and args.workload != "calibrate":
         try:
-            cpu = cpu_baseline(ks, threads, args.cpu_seconds)
-            cpu["kind"] = "port"
-            cpu["sample"] = (f"every kernel of the step at full shape on a host copy of buffer "
-                             f"set 0; median of repeated runs, {args.cpu_seconds:.0f} s budget; "
-                             f"oracle C (-O3, no fast-math), {threads} OpenMP threads")
-            cpu["cpu_model"] = cpu_model()
+            cpu = cpu_baseline_both(ks, ks70, args)
         except Exception as exc:  # the baseline is reported, never required
             log(f"cpu baseline failed: {exc!r}")
             cpu = None
@@ -1000,20 +1157,48 @@ def main():
         "launch": "eager stream" if args.no_graph else "HIP graph of the K steps, replayed once",
         "wall_s_timed": round(wall, 4),
         "kernels": per,
+        "config5": c5,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
 
 
-def cpu_model():
+def _cpuinfo_fields():
+    f = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = line.split(":", 1)
+                f.setdefault(k.strip(), []).append(v.strip())
     except OSError:
         pass
-    return "unknown"
+    return f
+
+
+def cpu_model():
+    f = _cpuinfo_fields()
+    return f.get("model name", ["unknown"])[0]
+
+
+def cpu_info():
+    """Host CPU identification: /proc/cpuinfo fields and lscpu's summary."""
+    f = _cpuinfo_fields()
+    info = {k: f[k][0] for k in ("vendor_id", "model name", "cpu family", "model", "stepping",
+                                 "cpu MHz", "cache size") if k in f}
+    info["logical_cpus"] = len(f.get("processor", []))
+    info["sockets"] = len(set(f.get("physical id", []))) or None
+    try:
+        import subprocess
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in txt.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in ("Model name", "Socket(s)", "Core(s) per socket",
+                             "Thread(s) per core", "CPU max MHz", "L3 cache"):
+                info["lscpu " + k.strip()] = v.strip()
+    except Exception:  # lscpu is optional
+        pass
+    return info
 
 
 if __name__ == "__main__":

@@ -67,8 +67,10 @@ __device__ __forceinline__ void wunpack(const WRaw<uint16_t, E>& r, float (&v)[E
     }
 }
 
-template <typename TA, typename TW, bool FUSED, int CPT = kNormCPT>
-__global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(
+// BS lanes (a template argument: with the block size known at compile time
+// the chunk offsets are immediates), CPT chunks per lane.
+template <typename TA, typename TW, bool FUSED, int BS, int CPT>
+__global__ __launch_bounds__(BS) void rmsnorm_vec_kernel(
     TA* out, int ld_out, TA* res, int ld_res, const TA* in, int ld_in,
     const TW* __restrict__ w, int n, float eps) {
 #pragma clang fp contract(off)
@@ -77,7 +79,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(
     __shared__ double red[16];
     const int64_t row = blockIdx.x;
     const int nch = n / E;
-    const int bs = blockDim.x;
+    constexpr int bs = BS;
     const TA* x = in + row * ld_in;
     TA* r = FUSED ? res + row * ld_res : nullptr;
 
@@ -126,6 +128,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(
     if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
     __syncthreads();
     ss = red[0];
+#pragma unroll
     for (int i = 1; i < bs / kWave; ++i) ss += red[i];
     const float rs = rms_scale(ss, n, eps);
     TA* y = out + row * ld_out;
@@ -195,9 +198,29 @@ static int rmsnorm_launch(void* out, int ld_out, void* res, int ld_res, const vo
     TA* r = static_cast<TA*>(res);
     const TA* x = static_cast<const TA*>(in);
     const TW* wt = static_cast<const TW*>(w);
-    if (vec && bs <= 1024)
-        return launch(rmsnorm_vec_kernel<TA, TW, FUSED>, dim3(n_rows), dim3(bs), 0, stream,
-                      o, ld_out, r, ld_res, x, ld_in, wt, n, eps);
+    if (vec && bs <= 1024) {
+        // block sizes rounded up to a power of two; one chunk per lane when
+        // that covers the row, else kNormCPT
+        int bp = kWave;
+        while (bp < bs) bp *= 2;
+        const bool one = nch <= bp;
+        auto go = [&](auto kern) {
+            return launch(kern, dim3(n_rows), dim3(bp), 0, stream, o, ld_out, r, ld_res, x,
+                          ld_in, wt, n, eps);
+        };
+        switch (bp) {
+            case 64: return one ? go(rmsnorm_vec_kernel<TA, TW, FUSED, 64, 1>)
+                                : go(rmsnorm_vec_kernel<TA, TW, FUSED, 64, kNormCPT>);
+            case 128: return one ? go(rmsnorm_vec_kernel<TA, TW, FUSED, 128, 1>)
+                                 : go(rmsnorm_vec_kernel<TA, TW, FUSED, 128, kNormCPT>);
+            case 256: return one ? go(rmsnorm_vec_kernel<TA, TW, FUSED, 256, 1>)
+                                 : go(rmsnorm_vec_kernel<TA, TW, FUSED, 256, kNormCPT>);
+            case 512: return one ? go(rmsnorm_vec_kernel<TA, TW, FUSED, 512, 1>)
+                                 : go(rmsnorm_vec_kernel<TA, TW, FUSED, 512, kNormCPT>);
+            default: return one ? go(rmsnorm_vec_kernel<TA, TW, FUSED, 1024, 1>)
+                                : go(rmsnorm_vec_kernel<TA, TW, FUSED, 1024, kNormCPT>);
+        }
+    }
     const int lbs = n >= 1024 ? 1024 : round_up(n, kWave);
     return launch(rmsnorm_loop_kernel<TA, TW, FUSED>, dim3(n_rows), dim3(lbs), 0, stream,
                   o, ld_out, r, ld_res, x, ld_in, wt, n, eps);

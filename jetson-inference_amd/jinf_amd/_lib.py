@@ -75,6 +75,14 @@ SIGNATURES = {
     "jinf_rmsnorm_qkv_rope_batch": (_I, [_P, _P, _P, _I, _P, _I, _P, _I, _F, _I, _P, _I, _P,
                                          _P, _I, ctypes.c_int64, _P, _I, _I, _I, _I, _F, _I,
                                          _P, ctypes.c_size_t, _P]),
+    # bandwidth probes (include/jinf/probe_hip.h)
+    "jinf_probe_rows_inplace": (_I, [_P, ctypes.c_int64, _I, _P, ctypes.c_int64, _I, _I, _I,
+                                     _I, _P]),
+    "jinf_probe_stream": (_I, [_P, _P, _P, _P, ctypes.c_int64, _I, _I, _P]),
+    "jinf_probe_gather": (_I, [_P, ctypes.c_int64, _I, _P, ctypes.c_int64, _I, _I, _P, _I, _I,
+                               _I, _P]),
+    "jinf_probe_rows_ragged": (_I, [_P, ctypes.c_int64, _P, ctypes.c_int64, _I, _P, _I, _I,
+                                    _P]),
     # GGUF files (include/jinf/gguf_hip.h)
     "jinf_hip_gguf_load": (_I, [ctypes.POINTER(_P), ctypes.c_char_p]),
     "jinf_hip_gguf_free": (None, [_P]),

@@ -446,3 +446,46 @@ def cuda_attention(out, q, k_cache, v_cache, head_dim, n_heads, n_heads_kv, n_pa
     lib().jinf_cuda_attention(_ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), int(head_dim),
                               int(n_heads), int(n_heads_kv), int(n_past), int(max_ctx), _stream())
     return out
+
+
+# ---- bandwidth probes (include/jinf/probe_hip.h): bench.py's ceilings ----
+
+def probe_rows_inplace(a, b, units_per_lane=1, exchange=True):
+    """RoPE's traffic, in place: rows of a [T, *] and b [T, *] (same T), every
+    live byte read and rewritten (the data becomes meaningless)."""
+    ra, na, lda = _rows(a)
+    rb, nb, ldb = _rows(b)
+    es = a.element_size()
+    _check(lib().jinf_probe_rows_inplace(_ptr(a), lda * es, na * es // 16, _ptr(b),
+                                         ldb * b.element_size(), nb * b.element_size() // 16,
+                                         ra, int(units_per_lane), int(bool(exchange)),
+                                         _stream()), "jinf_probe_rows_inplace")
+
+
+def probe_stream(out0, in0, out1=None, in1=None, units_per_lane=1, exchange=True):
+    """Flat streams of out0.numel() * element_size bytes (16-byte units)."""
+    nbytes = out0.numel() * out0.element_size()
+    _check(lib().jinf_probe_stream(_ptr(out0), _ptr(out1), _ptr(in0), _ptr(in1), nbytes // 16,
+                                   int(units_per_lane), int(bool(exchange)), _stream()),
+           "jinf_probe_stream")
+
+
+def probe_gather(out, table, ids, in_row_bytes, units_per_lane=1, exchange=True):
+    """The gather's traffic: out row r from table row ids[r] (table viewed as
+    byte rows; in_row_bytes of each row read)."""
+    n_ids, n_out, ld_out = _rows(out)
+    es = out.element_size()
+    rows, _, ld_t = _rows(table)
+    _check(lib().jinf_probe_gather(_ptr(out), ld_out * es, n_out * es // 16, _ptr(table),
+                                   ld_t * table.element_size(), in_row_bytes // 16, rows,
+                                   _ptr(ids), n_ids, int(units_per_lane), int(bool(exchange)),
+                                   _stream()), "jinf_probe_gather")
+
+
+def probe_rows_ragged(out, x, lens, rows_per_len):
+    """The masked softmax's traffic over fp32 rows of x with lengths lens."""
+    rows, n, ld_in = _rows(x)
+    _, _, ld_out = _rows(out)
+    _check(lib().jinf_probe_rows_ragged(_ptr(out), ld_out * 4, _ptr(x), ld_in * 4, n, _ptr(lens),
+                                        int(rows_per_len), rows, _stream()),
+           "jinf_probe_rows_ragged")
