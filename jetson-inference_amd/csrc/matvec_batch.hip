@@ -680,11 +680,15 @@ __global__ __launch_bounds__(64 * WV) void matvec_batch_kernel(MbJob j, MbTheta<
             const mb_f4 v = {val[i], val[i + 1], val[i + 2], val[i + 3]};
             __builtin_amdgcn_raw_buffer_store_b128(v, rs, off0 + 4 * i, 0, kMbSc1);
         }
+        // every thread waits for its partial stores; the barrier orders them
+        // before thread 0's agent-scope acquire-release counter update, so the
+        // workgroup that sees the final count synchronizes with every earlier
+        // one, and its threads read the partials after the next barrier
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         __shared__ int last;
         if (tid == 0) {
-            const uint32_t prev = __hip_atomic_fetch_add(j.counters + group, 1u, __ATOMIC_RELAXED,
+            const uint32_t prev = __hip_atomic_fetch_add(j.counters + group, 1u, __ATOMIC_ACQ_REL,
                                                          __HIP_MEMORY_SCOPE_AGENT);
             last = prev == (uint32_t)(j.k_splits - 1);
             if (last)
