@@ -192,26 +192,34 @@ int parse(jinf_hip_gguf* g, FILE* f) {
         if (!r.string(g->names[i])) return JINF_HIP_ERR_PARSE;
         t.n_dims = r.get<uint32_t>();
         if (!r.ok || t.n_dims > 4) return JINF_HIP_ERR_PARSE;
+        // shape product and byte size with overflow checks: a negative
+        // dimension or a product past int64 is a malformed file
         t.n_elements = 1;
         for (uint32_t d = 0; d < t.n_dims; ++d) {
             t.shape[d] = r.get<int64_t>();
-            t.n_elements *= t.shape[d];
+            if (t.shape[d] < 0 || __builtin_mul_overflow(t.n_elements, t.shape[d], &t.n_elements))
+                return JINF_HIP_ERR_PARSE;
         }
         t.qtype = map_type(r.get<uint32_t>());
         t.offset = r.get<uint64_t>();
         if (!r.ok) return JINF_HIP_ERR_PARSE;
         int block, bytes;
         type_geometry(t.qtype, &block, &bytes);
-        t.n_bytes = block ? (uint64_t)((t.n_elements + block - 1) / block) * (uint64_t)bytes : 0;
+        t.n_bytes = 0;
+        if (block) {
+            const uint64_t blocks = ((uint64_t)t.n_elements + (uint64_t)block - 1) / (uint64_t)block;
+            if (__builtin_mul_overflow(blocks, (uint64_t)bytes, &t.n_bytes)) return JINF_HIP_ERR_PARSE;
+        }
     }
     const uint64_t pos = (uint64_t)ftello(f);
     g->data_offset = (pos + g->alignment - 1) / g->alignment * g->alignment;
+    if (g->data_offset < pos || g->data_offset > g->file_size) return JINF_HIP_ERR_PARSE;
+    const uint64_t data_bytes = g->file_size - g->data_offset;
     for (uint64_t i = 0; i < n_tensors; ++i) {
         g->tensors[i].name = g->names[i].c_str();
         const jinf_hip_gguf_tensor& t = g->tensors[i];
-        if (t.n_elements < 0 || g->data_offset + t.offset + t.n_bytes > g->file_size ||
-            g->data_offset + t.offset < g->data_offset)
-            return JINF_HIP_ERR_PARSE;
+        // data_offset + offset + n_bytes <= file_size, written so nothing wraps
+        if (t.offset > data_bytes || t.n_bytes > data_bytes - t.offset) return JINF_HIP_ERR_PARSE;
     }
     return JINF_HIP_OK;
 }

@@ -144,17 +144,21 @@ def test_hparams_defaults_and_conversions(tmp_path):
 
 
 @pytest.mark.parametrize("damage", ["magic", "version", "truncated", "string_len", "n_dims",
-                                    "alignment0", "data_past_end", "bad_type"])
+                                    "alignment0", "data_past_end", "bad_type", "negative_dim",
+                                    "dims_overflow", "bytes_past_end", "offset_wraps"])
 def test_malformed_files_are_parse_errors(tmp_path, damage):
     p = tmp_path / "bad.gguf"
     kvs = [("general.architecture", gw.STR, "llama")]
-    tensors = [("t", [32], 2, bytes(18))]
+    tensors = [("t", [32, 1], 2, bytes(18))]
     if damage == "alignment0":
         kvs.append(("general.alignment", gw.U32, 0))
     if damage == "bad_type":
         kvs.append(("x", gw.U8, 1))
-    gw.write(p, kvs, tensors)
+    data_offset = gw.write(p, kvs, tensors)
     b = bytearray(open(p, "rb").read())
+    # tensor "t": n_dims (u32) at i, dims (i64) at i + 4 and i + 12, type at
+    # i + 20, offset (u64) at i + 24
+    i = b.index(b"\x01\x00\x00\x00\x00\x00\x00\x00t") + 9
     if damage == "magic":
         b[0] = ord("X")
     elif damage == "version":
@@ -164,8 +168,16 @@ def test_malformed_files_are_parse_errors(tmp_path, damage):
     elif damage == "string_len":
         b[24:32] = (2 << 20).to_bytes(8, "little")  # first key longer than 1 MiB
     elif damage == "n_dims":
-        i = b.index(b"\x01\x00\x00\x00\x00\x00\x00\x00t") + 9  # tensor name "t", then n_dims
         b[i:i + 4] = (5).to_bytes(4, "little")
+    elif damage == "negative_dim":
+        b[i + 4:i + 12] = (-32).to_bytes(8, "little", signed=True)
+    elif damage == "dims_overflow":  # 2^62 x 4 elements: the product passes int64
+        b[i + 4:i + 12] = (1 << 62).to_bytes(8, "little")
+        b[i + 12:i + 20] = (4).to_bytes(8, "little")
+    elif damage == "bytes_past_end":  # 2^60 elements fit, their bytes do not
+        b[i + 4:i + 12] = (1 << 60).to_bytes(8, "little")
+    elif damage == "offset_wraps":  # data_offset + offset fits, + n_bytes wraps to 17
+        b[i + 24:i + 32] = ((1 << 64) - data_offset - 1).to_bytes(8, "little")
     elif damage == "data_past_end":
         b = b[:-1]
     elif damage == "bad_type":
