@@ -272,3 +272,29 @@ def test_prefill_wide_chunks(dev):
         row[7] = 3
         b.forward(row)
         compare(b.logits()[7], ref.step(3), "after prefill", TOL_F16_KV)
+
+
+@pytest.mark.parametrize("name", ["mixed", "hd128-gqa4-f16embd"])
+def test_long_prefill_splits_attention_contexts(dev, name):
+    """A 330-token prompt through the batch decoder's prefill (chunks of 64
+    tokens, one per sequence slot, sharing one KV region) at max_context 512
+    with an fp16 cache: contexts past 256 positions are split and merged by
+    the separate merge launch (64 rows x 2 head groups in "mixed") or inside
+    the attention launch (the 10-token last chunk; 64 x 1 groups in the
+    other model).  The last token's logits and the next step of that
+    sequence equal the oracle's loop."""
+    n_seq, max_ctx = 64, 512
+    say(f"batch prefill of 330 tokens, {name}, max_context {max_ctx}, kv f16")
+    hp, W = mu.tiny_model(seed=66, n_vocab=350, **MODELS[name])
+    prompt = np.random.default_rng(67).integers(0, hp["n_vocab"], size=330).astype(np.int32)
+    ref = oeng.Decoder(hp, W, max_context=max_ctx, kv_type=mu.F16)
+    for t in prompt:
+        want = ref.step(int(t))
+    with Engine(hp, mu.to_device(W), 8, mu.F16) as e, Batch(e, n_seq, max_ctx, mu.F16) as b:
+        got = b.prefill(5, prompt)
+        compare(got, want, "long prefill last token", TOL_F16_KV)
+        assert b.n_past(5) == len(prompt)
+        row = np.full(n_seq, -1, np.int32)
+        row[5] = 7
+        b.forward(row)
+        compare(b.logits()[5], ref.step(7), "step after long prefill", TOL_F16_KV)

@@ -259,3 +259,27 @@ def test_gguf_missing_tensor(dev, tmp_path):
     with pytest.raises(EngineError) as ex:
         Engine.from_gguf(str(path), 16)
     assert ex.value.status == 2
+
+
+@pytest.mark.parametrize("name", ["mixed", "hd128-gqa4"])
+def test_long_prefill_splits_attention_contexts(dev, name):
+    """A 330-token prompt through prefill at max_context 512 with an fp16 KV
+    cache: the attention of every 64-token step runs over contexts past one
+    256-position chunk, so its split contexts are merged -- by the separate
+    merge launch when the step has 128 or more (row, head group) pairs
+    ("mixed": 64 rows x 2 groups), inside the attention launch otherwise
+    (the 10-token last step; "hd128-gqa4": 64 rows x 1 group).  The last
+    token's logits and the next decode step equal the oracle's loop."""
+    max_ctx = 512
+    say(f"engine prefill of 330 tokens, {name}, max_context {max_ctx}, kv f16")
+    hp, W = mu.tiny_model(seed=24, **MODELS[name])
+    prompt = np.random.default_rng(25).integers(0, hp["n_vocab"], size=330).astype(np.int32)
+    ref = oeng.Decoder(hp, W, max_context=max_ctx, kv_type=mu.F16)
+    with make_engine(hp, W, max_ctx, mu.F16) as e:
+        e.prefill(prompt)
+        for t in prompt:
+            want = ref.step(int(t))
+        assert e.n_past == len(prompt)
+        compare(e.logits(), want, f"{name} long prefill last token", TOL_F16_KV)
+        e.forward([7])
+        compare(e.logits(), ref.step(7), f"{name} step after long prefill", TOL_F16_KV)
