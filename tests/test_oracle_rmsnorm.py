@@ -91,9 +91,53 @@ def test_fused_equals_add_then_norm():
         assert tu.bits_equal(added, expect)
 
 
-def test_reference_order_sum_within_tolerance():
-    """The reference accumulates sum(x^2) in fp32 in its own order; the fp64
-    sum the oracle uses sits within the 1e-5 budget of it."""
+def _round_f32(fr):
+    """Exact rational -> nearest float32 (ties to even)."""
+    from fractions import Fraction
+
+    f = np.float32(float(fr))
+    cands = [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+    return min(cands, key=lambda c: (abs(Fraction(float(c)) - fr),
+                                     int(np.float32(c).view(np.uint32)) & 1))
+
+
+def test_reference_order_sum_known_answers():
+    """oracle.ref_order_sumsq restates the reference kernel's fp32 order for
+    sum(x^2) (cuda/rmsnorm_kernel.cu:16-22, cuda/cuda_utils.cuh:18-64).
+    Hand-worked inputs where that order rounds differently from a sequential
+    fp32 sum and from the exact sum pin the thread count, the per-thread fma
+    and both shfl_down trees."""
+    from fractions import Fraction
+
+    # 1. n = 64, zero except x[25] = 3, x[40] = 2, x[46] = 1, x[54] = x[57] =
+    # 6144 (squares 9, 4, 1, 37748736, 37748736): 64 threads, one element
+    # each.  Warp 0 holds only 9.  Warp 1 (lanes 8, 14, 22, 25 = 4, 1, S, S
+    # with S = 37748736, whose fp32 ulp is 4): offset 16 moves S to lanes 6
+    # and 9; offset 8 gives lane 0 = 4, lane 1 = S, lane 6 = S + 1 -> S;
+    # offset 4 moves S to lane 2; offset 2 gives lane 0 = S + 4 (exact);
+    # offset 1: 2S + 4 = 75497476, a tie between 75497472 and 75497480 (ulp
+    # 8), to even: 75497472.  The tree over the two warp sums: 9 + 75497472
+    # -> 75497480.  A 32-thread split, an adjacent-pair tree, a sequential
+    # fp32 sum and the exact sum (75497486) all give 75497488.
+    x = np.zeros(64, np.float32)
+    x[[25, 40, 46, 54, 57]] = [3.0, 2.0, 1.0, 6144.0, 6144.0]
+    assert oracle.ref_order_sumsq(x) == np.float32(75497480.0)
+    # 2. n = 2048: T = 1024 threads, thread 0 accumulates x[0]^2 then
+    # x[1024]^2 as fma(v, v, acc) (nvcc contracts acc += v * v); every other
+    # element is zero, so the trees pass thread 0's partial through.  For
+    # these two values the contracted sum fl32(x1^2 + fl32(x0^2)) and the
+    # separately rounded fl32(fl32(x1^2) + fl32(x0^2)) differ by one ulp.
+    x = np.zeros(2048, np.float32)
+    x0, x1 = np.float32(float.fromhex("0x1.e5ce34p+0")), np.float32(float.fromhex("0x1.d81f86p+0"))
+    x[0], x[1024] = x0, x1
+    a0 = _round_f32(Fraction(float(x0)) ** 2)
+    fused = _round_f32(Fraction(float(x1)) ** 2 + Fraction(float(a0)))
+    separate = _round_f32(Fraction(float(_round_f32(Fraction(float(x1)) ** 2))) +
+                          Fraction(float(a0)))
+    assert fused == np.float32(float.fromhex("0x1.c026cep+2")) and separate != fused
+    assert oracle.ref_order_sumsq(x) == fused
+    # 3. the config-1 row: the reference's rounding of sum(x^2) sits within
+    # 1e-6 of the fp64 sum the oracle (and the GPU) use
     g = np.load(os.path.join(HERE, "golden", "kernels.npz"))
     x = g["rms1_x"][0]
     s32 = oracle.ref_order_sumsq(x)
