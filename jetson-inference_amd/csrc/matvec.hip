@@ -462,25 +462,71 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
     int g0 = blockIdx.x * waves + wave, t0 = 0;
     uint4 bufA[R][CPL];
     uint4 bufB[R][CPL];
-    if (g0 < n_groups) fetch(g0, t0, bufA);
 
-    // RoPE: the position's (cos, sin) for every pair index, computed once per
-    // workgroup (one fp64 sincos per lane) instead of once per finished pair
-    // in the finishing lane
-    __shared__ float2 rcs[EPI == kEpiQKV ? kRopeMaxHalf : 1];
-    if constexpr (EPI == kEpiQKV) {
-        if (threadIdx.x < job.head_dim / 2) rcs[threadIdx.x] = rope_cs(job.pos[0], th.t[threadIdx.x]);
-    }
-
-    // Stage x (zero past the last value) while the first weights are in flight.
+    // Operands of the prologue are loaded before the first weight prefetch:
+    // vector loads complete in order, so a load issued after the prefetch
+    // would make the x staging, the norm and the RoPE table wait for the
+    // weights' HBM latency instead of overlapping it.  x (zero past the last
+    // value): XPT float4 per thread cover the staged tiles (one tile: 1024
+    // float4 over 256 threads; at most 7 tiles over 256 or 512 threads).
+    constexpr int XPT = ONE_TILE ? 4 : 28;
     const float4* x4 = reinterpret_cast<const float4*>(job.x);
     const int nx4 = nb * (F::kElems / 4);
+    const int nxs = nt << 10;
+    float4 xr[XPT];
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+        const int f = threadIdx.x + k * blockDim.x;
+        xr[k] = f < nx4 ? x4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    // norm weights g of the same slots (fp32, or fp16 in the low 8 bytes),
+    // early for single-tile matrices only (held with x, the multi-tile
+    // kernel's registers would spill; it reads g after the reduction)
+    constexpr bool NW_EARLY = PRO == kProNorm && ONE_TILE;
+    uint4 nwr[NW_EARLY ? XPT : 1];
+    auto load_nw = [&](int k) {
+        const int f = threadIdx.x + k * blockDim.x;
+        uint4 r = make_uint4(0, 0, 0, 0);
+        if (f < nx4) {
+            if (job.norm_f16) {
+                const uint2 u = reinterpret_cast<const uint2*>(job.norm_w)[f];
+                r = make_uint4(u.x, u.y, 0, 0);
+            } else {
+                r = reinterpret_cast<const uint4*>(job.norm_w)[f];
+            }
+        }
+        return r;
+    };
+    if constexpr (NW_EARLY) {
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) nwr[k] = load_nw(k);
+    }
+    // RoPE: the position and this lane's theta
+    int rpos = 0;
+    float rth = 0.0f;
+    if constexpr (EPI == kEpiQKV) {
+        rpos = job.pos[0];
+        if (threadIdx.x < job.head_dim / 2) rth = th.t[threadIdx.x];
+    }
+    // first weight item (a wave past the last group fetches the last row's
+    // bytes and never uses them: the load count stays the same on every path)
+    fetch(g0, t0, bufA);
+
+    // RoPE: the position's (cos, sin) for every pair index, computed once per
+    // workgroup (one sin/cos per lane) instead of once per finished pair in
+    // the finishing lane
+    __shared__ float2 rcs[EPI == kEpiQKV ? kRopeMaxHalf : 1];
+    if constexpr (EPI == kEpiQKV) {
+        if (threadIdx.x < job.head_dim / 2) rcs[threadIdx.x] = rope_cs(rpos, rth);
+    }
+
+    // Stage x while the first weights are in flight.
     if constexpr (PRO == kProNorm) {
         __shared__ double red[8];
         double ss = 0.0;
-        for (int f = threadIdx.x; f < (nt << 10); f += blockDim.x) {
-            const float4 v = f < nx4 ? x4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
-            xl[mv_xslot(f >> 10, (f >> 4) & 63, f & 15)] = v;
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) {
+            const float4 v = xr[k];
             ss = fma((double)v.x, (double)v.x, ss);
             ss = fma((double)v.y, (double)v.y, ss);
             ss = fma((double)v.z, (double)v.z, ss);
@@ -493,34 +539,46 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
         ss = red[0];
         for (int i = 1; i < waves; ++i) ss += red[i];
         const float rs = rms_scale(ss, nb * F::kElems, job.eps);
-        // each thread rescales the slots it wrote
-        for (int f = threadIdx.x; f < nx4; f += blockDim.x) {
-            const int slot = mv_xslot(f >> 10, (f >> 4) & 63, f & 15);
-            float4 v = xl[slot];
-            float w[4];
-            if (job.norm_f16) {
-                const uint2 u = reinterpret_cast<const uint2*>(job.norm_w)[f];
-                w[0] = h2f((uint16_t)(u.x & 0xFFFFu));
-                w[1] = h2f((uint16_t)(u.x >> 16));
-                w[2] = h2f((uint16_t)(u.y & 0xFFFFu));
-                w[3] = h2f((uint16_t)(u.y >> 16));
-            } else {
-                const float4 u = reinterpret_cast<const float4*>(job.norm_w)[f];
-                w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w;
-            }
-            {
+        // x_j = fl32(fl32(h_j * rs) * g_j), written once
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) {
+            const int f = threadIdx.x + k * blockDim.x;
+            if (f < nxs) {
+                float4 v = xr[k];
+                if (f < nx4) {
+                    uint4 nw;
+                    if constexpr (NW_EARLY)
+                        nw = nwr[k];
+                    else
+                        nw = load_nw(k);
+                    float w[4];
+                    if (job.norm_f16) {
+                        w[0] = h2f((uint16_t)(nw.x & 0xFFFFu));
+                        w[1] = h2f((uint16_t)(nw.x >> 16));
+                        w[2] = h2f((uint16_t)(nw.y & 0xFFFFu));
+                        w[3] = h2f((uint16_t)(nw.y >> 16));
+                    } else {
+                        w[0] = __builtin_bit_cast(float, nw.x);
+                        w[1] = __builtin_bit_cast(float, nw.y);
+                        w[2] = __builtin_bit_cast(float, nw.z);
+                        w[3] = __builtin_bit_cast(float, nw.w);
+                    }
+                    {
 #pragma clang fp contract(off)
-                v.x = (v.x * rs) * w[0];
-                v.y = (v.y * rs) * w[1];
-                v.z = (v.z * rs) * w[2];
-                v.w = (v.w * rs) * w[3];
+                        v.x = (v.x * rs) * w[0];
+                        v.y = (v.y * rs) * w[1];
+                        v.z = (v.z * rs) * w[2];
+                        v.w = (v.w * rs) * w[3];
+                    }
+                }
+                xl[mv_xslot(f >> 10, (f >> 4) & 63, f & 15)] = v;
             }
-            xl[slot] = v;
         }
     } else {
-        for (int f = threadIdx.x; f < (nt << 10); f += blockDim.x) {
-            const float4 v = f < nx4 ? x4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
-            xl[mv_xslot(f >> 10, (f >> 4) & 63, f & 15)] = v;
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) {
+            const int f = threadIdx.x + k * blockDim.x;
+            if (f < nxs) xl[mv_xslot(f >> 10, (f >> 4) & 63, f & 15)] = xr[k];
         }
     }
     __syncthreads();
