@@ -194,7 +194,6 @@ __host__ __device__ constexpr int mb_meta(int mt) { return 2048 * mt; }
 __host__ __device__ constexpr int mb_rec(int mt) { return mt * 32768 + mb_meta(mt); }
 
 constexpr int kMbMaxCols = 32768;                 // columns the preparation holds
-constexpr int kMbPrepG = kMbMaxCols / 8 / 256;    // 8-column groups per thread
 
 // grid (ceil(n_slabs / 8), 32 MT): workgroup (c, b) converts slabs 8 c ..
 // 8 c + 7 of token b.  Each holds token b's whole row in registers (thread i
@@ -233,7 +232,11 @@ __device__ __forceinline__ void mb_norm8(const void* norm_w, int norm_f16, int g
     }
 }
 
-template <int MT>
+// KG: 8-column groups per thread (the row's groups over 256 threads: 2 at
+// 4096 columns, 7 of 8 at 14336).  Every x and norm-weight load is issued
+// before any arithmetic (weights held in registers for KG <= 8), and the two
+// row reductions are DPP wave reductions with one LDS exchange.
+template <int MT, int KG>
 __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict__ x, int ld_x,
                                                           int n_batch, int cols,
                                                           const void* __restrict__ norm_w,
@@ -246,9 +249,11 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
     const int ng = cols / 8;  // a multiple of 32
     const bool live = b < n_batch;
     const float* xr = x + (int64_t)(live ? b : 0) * ld_x;
-    float v[kMbPrepG][8];
+    constexpr bool GW_EARLY = KG <= 8;
+    float v[KG][8];
+    float gwr[GW_EARLY ? KG : 1][8];
 #pragma unroll
-    for (int k = 0; k < kMbPrepG; ++k) {
+    for (int k = 0; k < KG; ++k) {
         const int g = tid + 256 * k;
         if (live && g < ng) {
             const float4 p = *reinterpret_cast<const float4*>(xr + 8 * g);
@@ -260,6 +265,26 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
             for (int e = 0; e < 8; ++e) v[k][e] = 0.0f;
         }
     }
+    if constexpr (GW_EARLY) {
+#pragma unroll
+        for (int k = 0; k < KG; ++k) {
+            const int g = tid + 256 * k;
+            if (g < ng) {
+                mb_norm8(norm_w, norm_f16, g, gwr[k]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) gwr[k][e] = 1.0f;
+            }
+        }
+    }
+    auto gweights = [&](int k, int g, float (&gw)[8]) {
+        if constexpr (GW_EARLY) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) gw[e] = gwr[k][e];
+        } else {
+            mb_norm8(norm_w, norm_f16, g, gw);
+        }
+    };
     // one workgroup reduction: the sum of squares (norm_w) and the largest
     // |x g| (|x| without norm_w); max |x^| <= rs max |x g| up to a few
     // roundings, so rs max |x g| fixes the scale (|x^ s| stays below
@@ -267,11 +292,11 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
     double ss = 0.0;
     float m = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kMbPrepG; ++k) {
+    for (int k = 0; k < KG; ++k) {
         const int g = tid + 256 * k;
         if (g < ng) {
             float gw[8];
-            mb_norm8(norm_w, norm_f16, g, gw);
+            gweights(k, g, gw);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 if (norm_w) ss = fma((double)v[k][e], (double)v[k][e], ss);
@@ -279,8 +304,8 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
             }
         }
     }
-    ss = wave_sum(ss);
-    m = wave_max(m);
+    ss = wave_sum_f64(ss);
+    m = wave_max_f32(m);
     if ((tid & (kWave - 1)) == 0) {
         red[tid / kWave] = ss;
         redf[tid / kWave] = m;
@@ -297,12 +322,12 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
         const float rs = rms_scale(ss, cols, eps);
         m = rs * m;
 #pragma unroll
-        for (int k = 0; k < kMbPrepG; ++k) {
+        for (int k = 0; k < KG; ++k) {
             const int g = tid + 256 * k;
             if (g < ng && k == (int)blockIdx.x) {  // only this workgroup's groups
 #pragma clang fp contract(off)
                 float gw[8];
-                mb_norm8(norm_w, norm_f16, g, gw);
+                gweights(k, g, gw);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[k][e] = (v[k][e] * rs) * gw[e];
             }
@@ -315,7 +340,7 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
     }
     const float sc = ldexpf(1.0f, 15 - ex);
 #pragma unroll
-    for (int k = 0; k < kMbPrepG; ++k) {
+    for (int k = 0; k < KG; ++k) {
         const int g = tid + 256 * k;
         // this workgroup's 256 groups (uniform over aligned groups of 32 threads)
         const bool here = g < ng && k == (int)blockIdx.x;
@@ -846,10 +871,16 @@ int mb_launch_shape(MbJob& j, const MbTheta<EPI>& th, hipStream_t stream) {
 template <int QT, int MT, int EPI>
 int mb_launch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void* norm_w,
                 int norm_f16, float eps, hipStream_t stream) {
-    const int rc = launch(mb_prepare_kernel<MT>, dim3((unsigned)((j.n_slabs + 7) / 8), 32 * MT),
-                          dim3(256), 0, stream, j.x, j.ld_x,
-                          j.n_batch, j.n_slabs * kMbCols, norm_w, norm_f16, eps,
-                          const_cast<uint8_t*>(j.xrec));
+    const int kg = (j.n_slabs + 7) / 8;  // 8-column groups per thread
+    auto prep = [&](auto kern) {
+        return launch(kern, dim3((unsigned)kg, 32 * MT), dim3(256), 0, stream, j.x, j.ld_x,
+                      j.n_batch, j.n_slabs * kMbCols, norm_w, norm_f16, eps,
+                      const_cast<uint8_t*>(j.xrec));
+    };
+    const int rc = kg <= 2 ? prep(mb_prepare_kernel<MT, 2>)
+                   : kg <= 4 ? prep(mb_prepare_kernel<MT, 4>)
+                   : kg <= 8 ? prep(mb_prepare_kernel<MT, 8>)
+                             : prep(mb_prepare_kernel<MT, 16>);
     if (rc != JINF_HIP_OK) return rc;
     (void)sh;  // kMbNarrow
     return mb_launch_shape<QT, MT, EPI, 2, 4, 4>(j, th, stream);
