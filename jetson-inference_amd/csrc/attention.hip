@@ -412,7 +412,7 @@ __device__ __forceinline__ void am_merge_last(float* __restrict__ out, int64_t l
 // {O[HD], m, l} to ws, and either the last workgroup of the (sequence, head
 // group) to finish merges them (counters: one per (sequence, head group),
 // zero between calls) or, counters == nullptr, attn_combine_kernel does.
-template <int HD, bool MERGE>
+template <int HD, bool MERGE, bool RB>
 __global__ __launch_bounds__(256) void attn_mfma_kernel(
     float* __restrict__ out, int64_t ld_out, const float* __restrict__ q, int64_t ld_q,
     const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t ld_pos,
@@ -426,6 +426,11 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     constexpr int VCH = HD / 8;        // 16-byte chunks per V row
     constexpr int VRS = kWave / VCH;   // V rows per load instruction
     constexpr int VLD = kAtTile / VRS; // V loads per lane per tile
+    // RB (short contexts): every wave walks every tile but owns one 16-row
+    // block of it (block b = wave), loading only those rows: VLDW loads each
+    // for K and V.  Otherwise a wave owns whole tiles (tile = 64 w + 256 k).
+    constexpr int VLDW = RB ? 16 / VRS : VLD;
+    constexpr int NBK = RB ? 1 : 4;    // 16-row blocks of a tile this wave processes
     constexpr int PITCH = HD * 2;      // LDS bytes per staged V row
     constexpr int MS = HD + 2;         // merge record: O[HD], m, l
     extern __shared__ uint8_t am_lds[];
@@ -476,10 +481,12 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     // chunk p ^ 2 ((r >> 2) & 3) for the same reason.
     uint8_t* kst = vst + kAtTile * PITCH;  // this wave's K tile, after its V tile
     auto kswz = [](int r) { return HD == 128 ? (r & 15) : ((r >> 1) & 7); };
+    const int i0 = RB ? VLDW * wave : 0;  // first load instruction of the wave's rows
     auto load_k = [&](int t0) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only: K buffer reads are done
 #pragma unroll
-        for (int i = 0; i < VLD; ++i) {
+        for (int ii = 0; ii < VLDW; ++ii) {
+            const int i = i0 + ii;
             const int slot_i = kWave * i + lane;
             const int row = slot_i / VCH;
             const int c = (slot_i % VCH) ^ kswz(row);
@@ -490,7 +497,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     auto load_v = [&](int t0) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only: V buffer reads are done
 #pragma unroll
-        for (int i = 0; i < VLD; ++i) {
+        for (int ii = 0; ii < VLDW; ++ii) {
+            const int i = i0 + ii;
             const int slot_i = kWave * i + lane;
             const int row = slot_i / VCH;
             const int c = (slot_i % VCH) ^ (2 * ((row >> 2) & 3));
@@ -498,10 +506,13 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
             lds_load16(src, vst + 1024 * i);
         }
     };
-    const int tstep = 4 * kAtTile;
-    if (c0 + wave * kAtTile < c1) {
-        load_k(c0 + wave * kAtTile);
-        load_v(c0 + wave * kAtTile);
+    // the wave's first tile and step; wrow: the wave's first row in a tile
+    const int tstep = RB ? kAtTile : 4 * kAtTile;
+    const int tfirst = RB ? c0 : c0 + wave * kAtTile;
+    const int wrow = RB ? 16 * wave : 0;
+    if (tfirst + wrow < c1) {
+        load_k(tfirst);
+        load_v(tfirst);
     }
     // q' = q * scale as fp16 hi / lo parts (the compiler's wait for the q
     // loads also covers the K / V loads issued after them: in-order counts)
@@ -521,23 +532,27 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
             qf[ks] = am_h4{hv[0], hv[1], hv[2], hv[3]};
         }
     }
-    for (int t0 = c0 + wave * kAtTile; t0 < c1; t0 += tstep) {
-        const bool more = t0 + tstep < c1;  // wave-uniform
-        // K(t) has landed once at most the VLD V loads issued after it remain
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm<VLD>());
+    // A wave stops at the first tile holding none of its rows (with RB a
+    // wave's block can end before the tile does), so it never issues loads
+    // for a tile it does not process and never sees an all-masked tile.
+    for (int t0 = tfirst; t0 + wrow < c1; t0 += tstep) {
+        const bool more = t0 + tstep + wrow < c1;  // wave-uniform
+        // K(t) has landed once at most the VLDW V loads issued after it remain
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm<VLDW>());
         wave_lds_sync();
         // scores: A fragment = 4 halves of row 16 b + col at dims DPG lg + 4 ks
-        am_f4 S[4];
+        am_f4 S[NBK];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            S[b] = am_f4{0.f, 0.f, 0.f, 0.f};
+        for (int bi = 0; bi < NBK; ++bi) {
+            const int b = RB ? wave : bi;  // the block's rows in the tile: 16 b ..
+            S[bi] = am_f4{0.f, 0.f, 0.f, 0.f};
             const int r = 16 * b + col;
 #pragma unroll
             for (int u = 0; u < KLD; ++u) {
                 const int c = (DPG * lg) / 8 + u;  // 16-byte chunk of the row
                 const uint4 w = *reinterpret_cast<const uint4*>(kst + r * PITCH + 16 * (c ^ kswz(r)));
-                S[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(am_h4_from(w.x, w.y), qf[2 * u], S[b], 0, 0, 0);
-                S[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(am_h4_from(w.z, w.w), qf[2 * u + 1], S[b], 0, 0, 0);
+                S[bi] = __builtin_amdgcn_mfma_f32_16x16x16f16(am_h4_from(w.x, w.y), qf[2 * u], S[bi], 0, 0, 0);
+                S[bi] = __builtin_amdgcn_mfma_f32_16x16x16f16(am_h4_from(w.z, w.w), qf[2 * u + 1], S[bi], 0, 0, 0);
             }
         }
         wave_lds_sync();
@@ -545,12 +560,13 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
         // hi + lo columns, mask, tile max (lanes of one column: xor 16, 32)
         float tmax = -INFINITY;
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int bi = 0; bi < NBK; ++bi)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float v = S[b][r] + ror8(S[b][r]);
+                const int b = RB ? wave : bi;
+                const float v = S[bi][r] + ror8(S[bi][r]);
                 const float vm = t0 + 16 * b + 4 * lg + r < c1 ? v : -INFINITY;
-                S[b][r] = vm;
+                S[bi][r] = vm;
                 tmax = fmaxf(tmax, vm);
             }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
@@ -559,19 +575,19 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
         const float corr = exp_neg(m - mn);
         m = mn;
         float psum = 0.0f;
-        am_h4 P[4];
+        am_h4 P[NBK];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
+        for (int bi = 0; bi < NBK; ++bi) {
             _Float16 hv[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float pr = exp_neg(S[b][r] - mn);
+                const float pr = exp_neg(S[bi][r] - mn);
                 psum += pr;
                 const float ps = pr * kAmPScale;
                 const _Float16 hi = (_Float16)ps;
                 hv[r] = lo_col ? (_Float16)(ps - (float)hi) : hi;
             }
-            P[b] = am_h4{hv[0], hv[1], hv[2], hv[3]};
+            P[bi] = am_h4{hv[0], hv[1], hv[2], hv[3]};
         }
         lsum = fmaf(lsum, corr, psum);
         // rescale O: its rows 4 lg + r are slots (4 lg + r) & 7, whose factor
@@ -590,12 +606,13 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
         // O += P' V once the tile's V has landed in LDS (the next tile's K
         // loads, issued later, may stay in flight)
         if (more)
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm<VLD>());
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm<VLDW>());
         else
             __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
         wave_lds_sync();
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
+        for (int bi = 0; bi < NBK; ++bi) {
+            const int b = RB ? wave : bi;
             const uint8_t* vrow = vst + (16 * b + 4 * lg) * PITCH + 2 * (col & 7);
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
@@ -603,7 +620,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
                 const uint16_t* p0 = reinterpret_cast<const uint16_t*>(vrow + 16 * p);
                 const uint32_t x0 = p0[0] | ((uint32_t)p0[PITCH / 2] << 16);
                 const uint32_t x1 = p0[PITCH] | ((uint32_t)p0[3 * PITCH / 2] << 16);
-                O[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(P[b], am_h4_from(x0, x1), O[n], 0, 0, 0);
+                O[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(P[bi], am_h4_from(x0, x1), O[n], 0, 0, 0);
             }
         }
         wave_lds_sync();
@@ -801,7 +818,11 @@ static int am_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, c
         ws = reinterpret_cast<float*>(static_cast<char*>(sc.base) +
                                       am_counter_bytes(n_seq, n_heads));
     }
-    auto* kern = counters ? attn_mfma_kernel<HD, true> : attn_mfma_kernel<HD, false>;
+    // up to 128 positions per work item the four waves share each tile by
+    // 16-row blocks (otherwise at most two waves would hold a tile)
+    const bool rb = chunk <= 2 * kAtTile;
+    auto* kern = counters ? (rb ? attn_mfma_kernel<HD, true, true> : attn_mfma_kernel<HD, true, false>)
+                          : (rb ? attn_mfma_kernel<HD, false, true> : attn_mfma_kernel<HD, false, false>);
     const int st = launch(kern, dim3(n_heads / G, nch, n_seq), dim3(256), shmem, stream, out,
                           ld_out, q, ld_q, static_cast<const uint16_t*>(k),
                           static_cast<const uint16_t*>(v), ld_pos, ld_seq, lens, n_past, group,
