@@ -425,7 +425,10 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
     extern __shared__ uint4 lds[];
     float4* xl = reinterpret_cast<float4*>(lds);
     const int waves = blockDim.x / kWave;
-    const int wave = threadIdx.x / kWave;
+    // wave index in a scalar register: the walk over items below is then
+    // wave-uniform control flow (no exec-masked paths whose merged wait
+    // counts would hold the next prefetch until the current one has landed)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x & (kWave - 1);
     const int nb = job.nb;
     int nt = job.nt;
@@ -643,29 +646,36 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
         }
     };
 
-    // The last item leaves through its own branch, so on the main path the
-    // prefetch is unconditional and the compiler's wait counts stay exact
-    // (a conditional load makes it wait for every outstanding load).
-    int g1 = g0, t1 = t0;
-    while (true) {
+    // The wave's items (its groups g0, g0 + stride, ... below n_groups, each
+    // over its tiles), counted up front: the loop below has no exit but its
+    // own test, so every fetch in it is unconditional and the compiler's wait
+    // counts at the loop head see exactly the one item in flight (an exit
+    // taken from inside the loop, or a conditional fetch, merges paths on
+    // which other buffers look pending, and the next prefetch then waits for
+    // the current one).  The last one or two items follow the loop.
+    const int n_items = ((n_groups - 1 - g0) / stride + 1) * nt;
+    int g = g0, t = t0;  // the item held in bufA
+    int rem = n_items;
+    while (rem > 2) {
+        int g1 = g, t1 = t;
         advance(g1, t1);
-        if (g1 >= n_groups) {
-            process(g0, t0, bufA);
-            break;
-        }
         fetch(g1, t1, bufB);
-        process(g0, t0, bufA);
-        g0 = g1;
-        t0 = t1;
+        process(g, t, bufA);
+        g = g1;
+        t = t1;
+        advance(g, t);
+        fetch(g, t, bufA);
+        process(g1, t1, bufB);
+        rem -= 2;
+    }
+    if (rem == 2) {
+        int g1 = g, t1 = t;
         advance(g1, t1);
-        if (g1 >= n_groups) {
-            process(g0, t0, bufB);
-            break;
-        }
-        fetch(g1, t1, bufA);
-        process(g0, t0, bufB);
-        g0 = g1;
-        t0 = t1;
+        fetch(g1, t1, bufB);
+        process(g, t, bufA);
+        process(g1, t1, bufB);
+    } else {
+        process(g, t, bufA);
     }
 }
 
