@@ -23,10 +23,12 @@
 //   - x is staged once per workgroup in LDS; a lane keeps its 64 x values in
 //     registers (for the whole kernel when the matrix is one tile wide) and
 //     reuses them for all R rows;
-//   - dequantisation is folded into the dot product: the integer codes are
-//     multiplied as fp16 denormals with v_fma_mix_f32 (see mix2), and the
-//     per-block scale, offset and minimum are applied once per block or
-//     sub-block against the block's sum of x;
+//   - dequantisation is folded into the dot product: 4-bit codes (Q4_0,
+//     Q4_K) meet x as exact integers, 8 products per v_dot8_i32_i4 against
+//     x staged in fixed point as signed base-16 digit planes (plane_dot32);
+//     8-bit and 6-bit codes (Q8_0, Q6_K) are multiplied as fp16 denormals
+//     with v_fma_mix_f32 (see mix2); the per-block scale, offset and minimum
+//     are applied once per block or sub-block;
 //   - each row's lane partials meet in a DPP wave reduction.
 // Anything the tiled kernel does not serve (unaligned pointers, widths that
 // are not a multiple of the format's tile granule, more than 7 tiles) takes a
@@ -66,30 +68,8 @@ __device__ __forceinline__ float mix2(uint32_t h, float xlo, float xhi, float ac
 constexpr float kTwo24 = 16777216.0f;         // 2^24
 constexpr float kTwoM24 = 1.0f / 16777216.0f;  // 2^-24
 
-// 2^-24 * sum_j q_j x_j over 32 values whose 4-bit codes q (0..15) are packed
-// in jinf's interleaved order: word i holds values 8i..8i+7, value 8i+n in
-// bits 4n..4n+3.  xp: the 32 x values with odd positions pre-divided by 16.
-//   w & 0x000F000F        -> values 8i+0 (lo half), 8i+4 (hi half)
-//   w & 0x00F000F0        -> 8i+1, 8i+5 (codes times 16)
-//   (w >> 8) & 0x000F000F -> 8i+2, 8i+6
-//   (w >> 8) & 0x00F000F0 -> 8i+3, 8i+7 (codes times 16)
-__device__ __forceinline__ float nib_dot32(const uint32_t (&qw)[4], const float* xp) {
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t w = qw[i];
-        const uint32_t v = w >> 8;
-        const float* xi = xp + 8 * i;
-        s = mix2(w & 0x000F000Fu, xi[0], xi[4], s);
-        s = mix2(w & 0x00F000F0u, xi[1], xi[5], s);
-        s = mix2(v & 0x000F000Fu, xi[2], xi[6], s);
-        s = mix2(v & 0x00F000F0u, xi[3], xi[7], s);
-    }
-    return s;
-}
-
-// Same for 8-bit codes (0..255), four per word in value order: word i holds
-// values 4i..4i+3 as bytes.
+// 2^-24 * sum_j q_j x_j for 8-bit codes q (0..255), four per word in value
+// order: word i holds values 4i..4i+3 as bytes.
 __device__ __forceinline__ float byte_dot(const uint32_t* qw, int nw, const float* x) {
     float s = 0.0f;
 #pragma unroll
@@ -108,40 +88,154 @@ __device__ __forceinline__ uint32_t lds_dw(const uint32_t* base, int byte_off) {
     return __builtin_amdgcn_alignbit(base[k + 1], base[k], (byte_off & 3) * 8);
 }
 
+// ---- exact integer products for the 4-bit formats ----
+//
+// Q4_0 and Q4_K codes q (0..15) sit 8 to a dword (value 8i+n of a word group
+// at bits 4n).  q ^ 8 read as a signed nibble is q - 8, so one
+// v_dot8_i32_i4 gives sum_n (q_n - 8) D_n over 8 values for signed nibbles
+// D_n: one VALU op for 8 weights, against 13 for the fp16-denormal products.
+// For it each workgroup stages x once, per 32-value block:
+//   X_j = rint(x_j 2^s) with s = 22 - e, e the exponent with max |x| < 2^e
+//   (at least -100), so |X_j| <= 2^22;
+//   X_j in six balanced base-16 digits, X_j = sum_p 16^p D_p, D_p in [-8, 7]:
+//   the nibbles of (X_j + 0x888888) ^ 0x888888;
+//   plane p of a word group: digit p of its 8 values, packed like the codes.
+// Then sum_j (q_j - 8) X_j = sum_p 16^p P_p, P_p from six chains of dot8
+// (exact: |P_p| <= 32 * 64), formed as lo + 4096 hi (both exact in fp32)
+// with one rounding and scaled by 2^-s (exact).  Against fp32 x the only
+// difference is X's rounding, at most 2^-23 of the block's largest |x| per
+// value (the size of an fp32 product's own rounding for that value), and a
+// one-hot x still gives d * (q - 8) exactly.  A block holding a non-finite
+// x gives its rows NaN (the reference's fp32 products give NaN or +-inf).
+constexpr int kMvRecWords = 52;  // a lane's planes: 48 digit words, 2 scales, 2 sums
+constexpr int kMvRecTile16 = kMvRecWords * kWave / 4;  // 16-byte units per tile
+
+// A lane's x for one tile, as its format consumes it.
+struct MvXFloat {
+    float v[kMvLaneElems];  // the lane's 64 values, prepared by the format
+    float s[4];             // plain sums of values 16k .. 16k+15
+};
+struct MvXPlanes {
+    uint32_t p[48];  // word group w (values 8w .. 8w+7 of the lane): digit k at 6w + k
+    float inv[2];    // 2^-s of the lane's two 32-value blocks (NaN: non-finite x)
+    int sx[2];       // sum of X over each block
+};
+
+// sum_j (q_j - 8) X_j + add over one 32-value block (code words q, planes
+// pl[0..24)), rounded once to fp32.
+__device__ __forceinline__ float plane_dot32(const uint32_t (&q)[4], const uint32_t* pl, int add) {
+    int P[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int qs = (int)(q[i] ^ 0x88888888u);
+#pragma unroll
+        for (int k = 0; k < 6; ++k)
+            P[k] = __builtin_amdgcn_sdot8(qs, (int)pl[6 * i + k], P[k], false);
+    }
+    const int lo = P[0] + P[1] * 16 + P[2] * 256 + add;
+    const int hi = P[3] + P[4] * 16 + P[5] * 256;
+    return fmaf((float)hi, 4096.0f, (float)lo);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+// Stages word group g of the x tiles (values 8g .. 8g + 7: a, b) as planes.
+// The four groups of a 32-value block are the four lanes of one quad and call
+// this together.  Consumer lane l of tile t reads the record at
+// rec + (64 t + l) * kMvRecWords: digit words [0, 48), 2^-s [48, 50), sums
+// [50, 52).
+__device__ __forceinline__ void mv_stage_planes(uint32_t* rec, int g, float4 a, float4 b) {
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    // block maximum of |x| as bit patterns (NaN and infinities compare above
+    // every finite value)
+    uint32_t mb = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mb = max(mb, __float_as_uint(v[i]) & 0x7FFFFFFFu);
+    mb = max(mb, dpp_u32<0xB1>(mb));  // quad_perm [1,0,3,2]
+    mb = max(mb, dpp_u32<0x4E>(mb));  // quad_perm [2,3,0,1]
+    const bool finite = mb < 0x7F800000u;
+    const int e = max(__builtin_amdgcn_frexp_expf(__uint_as_float(mb)), -100);
+    const float scale = ldexpf(1.0f, 22 - e);
+    // X + 0x888888: x 2^s + 1.5 2^23 rounds x 2^s to an integer (|x 2^s| <=
+    // 2^22), whose bits are 0x4B400000 + X.  (In a non-finite block these
+    // are meaningless; the block's 2^-s is NaN.)
+    uint32_t V[8];
+    uint32_t us = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t u = __float_as_uint(fmaf(v[i], scale, 12582912.0f)) - (0x4B400000u - 0x888888u);
+        us += u;
+        V[i] = u ^ 0x888888u;
+    }
+    // digit pairs: byte c of t[k] = digits 2c of values 2k, 2k + 1 (low, high
+    // nibble), byte c of u[k] = digits 2c + 1; then plane p = byte p / 2 of
+    // t or u over k = 0..3
+    uint32_t t[4], u[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        t[k] = (V[2 * k] & 0x0F0F0F0Fu) | ((V[2 * k + 1] << 4) & 0xF0F0F0F0u);
+        u[k] = ((V[2 * k] >> 4) & 0x0F0F0F0Fu) | (V[2 * k + 1] & 0xF0F0F0F0u);
+    }
+    uint32_t pl[6];
+#pragma unroll
+    for (int o = 0; o < 2; ++o) {
+        const uint32_t* src = o ? u : t;
+        const uint32_t a01 = __builtin_amdgcn_perm(src[1], src[0], 0x05010400u);
+        const uint32_t a23 = __builtin_amdgcn_perm(src[3], src[2], 0x05010400u);
+        const uint32_t b01 = __builtin_amdgcn_perm(src[1], src[0], 0x07030602u);
+        const uint32_t b23 = __builtin_amdgcn_perm(src[3], src[2], 0x07030602u);
+        pl[o] = __builtin_amdgcn_perm(a23, a01, 0x05040100u);
+        pl[2 + o] = __builtin_amdgcn_perm(a23, a01, 0x07060302u);
+        pl[4 + o] = __builtin_amdgcn_perm(b23, b01, 0x05040100u);
+    }
+    uint32_t* r = rec + (g >> 3) * kMvRecWords;  // consumer lane: 8 groups each
+    uint2* d = reinterpret_cast<uint2*>(r + 6 * (g & 7));
+    d[0] = make_uint2(pl[0], pl[1]);
+    d[1] = make_uint2(pl[2], pl[3]);
+    d[2] = make_uint2(pl[4], pl[5]);
+    us += dpp_u32<0xB1>(us);
+    us += dpp_u32<0x4E>(us);
+    if ((g & 3) == 0) {
+        const int blk = (g >> 2) & 1;
+        r[48 + blk] = __float_as_uint(finite ? ldexpf(1.0f, e - 22) : __builtin_nanf(""));
+        r[50 + blk] = us - 32u * 0x888888u;
+    }
+}
+
 // ---- format policies for the tiled kernel ----
 //
 // Each gives the block geometry, the width granule of the fast path (a
 // multiple that makes row and tile byte counts multiples of 16), the rows per
-// item, how a lane's x registers are prepared, and the lane's dot product over
-// its 64 values of one staged row tile (`row`: the tile's bytes in LDS as
-// dwords; xs[k]: plain sum of the lane's x values 16k .. 16k+15).
+// item, the lane's x representation (kPlanes: MvXPlanes, else MvXFloat with
+// its values prepared by prep) and the lane's dot product over its 64 values
+// of one staged row tile (`row`: the tile's bytes in LDS as dwords).
 
 template <int QT> struct MvFmt;
 
 // Q4_0: lane = 2 consecutive blocks (36 B, 9 dwords at 9 * lane: conflict
-// free).  y += d * (2^24 * nib_dot - 8 * sum x) per block, with the 2^24 in d.
+// free).  y += (d 2^-s) sum (q - 8) X per block (plane_dot32).
 template <> struct MvFmt<kQ4_0> {
     static constexpr int kElems = 32, kBytes = 18, kColGranule = 256, kRows = 2;
-    static __device__ void prep(float (&xv)[64]) {
-#pragma unroll
-        for (int i = 1; i < 64; i += 2) xv[i] *= 0.0625f;
-    }
-    static __device__ float dot(const uint32_t* row, int lane, const float (&xv)[64],
-                                const float (&xs)[4]) {
+    static constexpr bool kPlanes = true;
+    using XReg = MvXPlanes;
+    static __device__ float dot(const uint32_t* row, int lane, const XReg& x) {
         const uint32_t* l = row + 9 * lane;
         uint32_t D[9];
 #pragma unroll
         for (int i = 0; i < 9; ++i) D[i] = l[i];
-        const float d0 = h2f((uint16_t)(D[0] & 0xFFFFu)) * kTwo24;
-        const float d1 = h2f((uint16_t)(D[4] >> 16)) * kTwo24;
+        const float d0 = h2f((uint16_t)(D[0] & 0xFFFFu));
+        const float d1 = h2f((uint16_t)(D[4] >> 16));
         const uint32_t q0[4] = {__builtin_amdgcn_alignbit(D[1], D[0], 16),
                                 __builtin_amdgcn_alignbit(D[2], D[1], 16),
                                 __builtin_amdgcn_alignbit(D[3], D[2], 16),
                                 __builtin_amdgcn_alignbit(D[4], D[3], 16)};
         const uint32_t q1[4] = {D[5], D[6], D[7], D[8]};
-        const float s0 = fmaf(-8.0f * kTwoM24, xs[0] + xs[1], nib_dot32(q0, xv));
-        const float s1 = fmaf(-8.0f * kTwoM24, xs[2] + xs[3], nib_dot32(q1, xv + 32));
-        return fmaf(d1, s1, d0 * s0);
+        const float t0 = plane_dot32(q0, x.p, 0);
+        const float t1 = plane_dot32(q1, x.p + 24, 0);
+        return fmaf(d1 * x.inv[1], t1, (d0 * x.inv[0]) * t0);
     }
 };
 
@@ -150,9 +244,12 @@ template <> struct MvFmt<kQ4_0> {
 // fp16-denormal product, and the bias comes back as -128 * sum x per block.
 template <> struct MvFmt<kQ8_0> {
     static constexpr int kElems = 32, kBytes = 34, kColGranule = 256, kRows = 1;
+    static constexpr bool kPlanes = false;
+    using XReg = MvXFloat;
     static __device__ void prep(float (&)[64]) {}
-    static __device__ float dot(const uint32_t* row, int lane, const float (&xv)[64],
-                                const float (&xs)[4]) {
+    static __device__ float dot(const uint32_t* row, int lane, const XReg& x) {
+        const float (&xv)[64] = x.v;
+        const float (&xs)[4] = x.s;
         const uint32_t* l = row + 17 * lane;
         uint32_t D[17];
 #pragma unroll
@@ -173,16 +270,14 @@ template <> struct MvFmt<kQ8_0> {
 
 // Q4_K: lane = one quarter of a super-block (sub-blocks 2k, 2k+1 of block
 // lane / 4, k = lane % 4): header dwords 0-3 of the block (shared by its four
-// lanes) and 8 dwords of nibbles.  Per sub-block:
-//   sum_j (sub_d q_j - sub_min) x_j = sub_d * sum q x - sub_min * sum x.
+// lanes) and 8 dwords of nibbles.  Per sub-block (one 32-value x block):
+//   sum_j (sub_d q_j - sub_min) x_j
+//     = 2^-s (sub_d sum q X - sub_min sum X),  sum q X = sum (q - 8) X + 8 sum X.
 template <> struct MvFmt<kQ4_K> {
     static constexpr int kElems = 256, kBytes = 144, kColGranule = 256, kRows = 2;
-    static __device__ void prep(float (&xv)[64]) {
-#pragma unroll
-        for (int i = 1; i < 64; i += 2) xv[i] *= 0.0625f;
-    }
-    static __device__ float dot(const uint32_t* row, int lane, const float (&xv)[64],
-                                const float (&xs)[4]) {
+    static constexpr bool kPlanes = true;
+    using XReg = MvXPlanes;
+    static __device__ float dot(const uint32_t* row, int lane, const XReg& x) {
         const int k = lane & 3;
         const uint32_t* b = row + 36 * (lane >> 2);
         const uint32_t h = b[0];
@@ -193,13 +288,15 @@ template <> struct MvFmt<kQ4_K> {
             q0[i] = b[4 + 8 * k + i];
             q1[i] = b[8 + 8 * k + i];
         }
-        const float d = h2f((uint16_t)(h & 0xFFFFu)) * kTwo24;
+        const float d = h2f((uint16_t)(h & 0xFFFFu));
         const float dmin = h2f((uint16_t)(h >> 16));
         int sc0, mn0, sc1, mn1;
         q4_K_scale_min(s, 2 * k, sc0, mn0);
         q4_K_scale_min(s, 2 * k + 1, sc1, mn1);
-        const float t0 = fmaf(d * (float)sc0, nib_dot32(q0, xv), -(dmin * (float)mn0) * (xs[0] + xs[1]));
-        const float t1 = fmaf(d * (float)sc1, nib_dot32(q1, xv + 32), -(dmin * (float)mn1) * (xs[2] + xs[3]));
+        const float u0 = plane_dot32(q0, x.p, 8 * x.sx[0]);
+        const float u1 = plane_dot32(q1, x.p + 24, 8 * x.sx[1]);
+        const float t0 = fmaf(d * (float)sc0, u0, -(dmin * (float)mn0) * (float)x.sx[0]) * x.inv[0];
+        const float t1 = fmaf(d * (float)sc1, u1, -(dmin * (float)mn1) * (float)x.sx[1]) * x.inv[1];
         return t0 + t1;
     }
 };
@@ -217,9 +314,12 @@ template <> struct MvFmt<kQ4_K> {
 // Per 16-value sub-block: (d * scale) * (sum q6 x - 32 sum x).
 template <> struct MvFmt<kQ6_K> {
     static constexpr int kElems = 256, kBytes = 210, kColGranule = 2048, kRows = 1;
+    static constexpr bool kPlanes = false;
+    using XReg = MvXFloat;
     static __device__ void prep(float (&)[64]) {}
-    static __device__ float dot(const uint32_t* row, int lane, const float (&xv)[64],
-                                const float (&xs)[4]) {
+    static __device__ float dot(const uint32_t* row, int lane, const XReg& x) {
+        const float (&xv)[64] = x.v;
+        const float (&xs)[4] = x.s;
         const int k = lane & 3;
         const int base = 210 * (lane >> 2);
         uint32_t ql[8], qh[4];
@@ -414,9 +514,11 @@ __device__ __forceinline__ void mv_epilogue(const MvJob& j, const MvTheta<EPI>& 
 // its last tile.  The wave's LDS accesses execute in order; the fences keep
 // the compiler from moving the read-back above the stores.  Workgroup
 // barriers only follow the x staging.
-template <int QT, bool ONE_TILE, int PRO, int EPI>
-__global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
-                                                                      MvTheta<EPI> th) {
+// WV1: waves of a one-tile workgroup (4, or 8 where the kernel fits four
+// waves per SIMD: one x staging for twice the waves).
+template <int QT, bool ONE_TILE, int PRO, int EPI, int WV1>
+__global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob job,
+                                                                           MvTheta<EPI> th) {
     using F = MvFmt<QT>;
     using G = MvGroup<QT, EPI, !ONE_TILE>;
     constexpr int R = G::R;
@@ -432,7 +534,10 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
     const int lane = threadIdx.x & (kWave - 1);
     const int nb = job.nb;
     int nt = job.nt;
-    uint4* stage = lds + (nt << 10) + wave * T::kStageChunks;
+    // x region: per tile 1024 float4 (MvXFloat formats) or 64 plane records
+    constexpr int XT16 = F::kPlanes ? kMvRecTile16 : 1024;
+    uint32_t* xrec = reinterpret_cast<uint32_t*>(lds);
+    uint4* stage = lds + nt * XT16 + wave * T::kStageChunks;
     const int n_groups = G::groups(job);
     const int stride = gridDim.x * waves;
     if (ONE_TILE) nt = 1;
@@ -472,14 +577,20 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
     // weights' HBM latency instead of overlapping it.  x (zero past the last
     // value): XPT float4 per thread cover the staged tiles (one tile: 1024
     // float4 over 256 threads; at most 7 tiles over 256 or 512 threads).
-    constexpr int XPT = ONE_TILE ? 4 : 28;
+    constexpr int XPT = ONE_TILE ? 16 / WV1 : 28;
+    // float4 number of slot k: plane formats take word groups of two
+    // consecutive float4 (group threadIdx.x + (k / 2) blockDim.x)
+    auto fi = [&](int k) {
+        return F::kPlanes ? 2 * ((int)threadIdx.x + (k >> 1) * (int)blockDim.x) + (k & 1)
+                          : (int)threadIdx.x + k * (int)blockDim.x;
+    };
     const float4* x4 = reinterpret_cast<const float4*>(job.x);
     const int nx4 = nb * (F::kElems / 4);
     const int nxs = nt << 10;
     float4 xr[XPT];
 #pragma unroll
     for (int k = 0; k < XPT; ++k) {
-        const int f = threadIdx.x + k * blockDim.x;
+        const int f = fi(k);
         xr[k] = f < nx4 ? x4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     // norm weights g of the same slots (fp32, or fp16 in the low 8 bytes),
@@ -488,7 +599,7 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
     constexpr bool NW_EARLY = PRO == kProNorm && ONE_TILE;
     uint4 nwr[NW_EARLY ? XPT : 1];
     auto load_nw = [&](int k) {
-        const int f = threadIdx.x + k * blockDim.x;
+        const int f = fi(k);
         uint4 r = make_uint4(0, 0, 0, 0);
         if (f < nx4) {
             if (job.norm_f16) {
@@ -545,7 +656,7 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
         // x_j = fl32(fl32(h_j * rs) * g_j), written once
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {
-            const int f = threadIdx.x + k * blockDim.x;
+            const int f = fi(k);
             if (f < nxs) {
                 float4 v = xr[k];
                 if (f < nx4) {
@@ -574,35 +685,60 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
                         v.w = (v.w * rs) * w[3];
                     }
                 }
-                xl[mv_xslot(f >> 10, (f >> 4) & 63, f & 15)] = v;
+                if constexpr (F::kPlanes)
+                    xr[k] = v;
+                else
+                    xl[mv_xslot(f >> 10, (f >> 4) & 63, f & 15)] = v;
             }
         }
-    } else {
+    }
+    if constexpr (F::kPlanes) {
+        // 2 g < nxs holds for whole waves (nxs is a multiple of 1024), so the
+        // four lanes of a block stage it together
+#pragma unroll
+        for (int k = 0; k < XPT; k += 2) {
+            const int g = threadIdx.x + (k >> 1) * blockDim.x;
+            if (2 * g < nxs) mv_stage_planes(xrec, g, xr[k], xr[k + 1]);
+        }
+    } else if constexpr (PRO != kProNorm) {
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {
-            const int f = threadIdx.x + k * blockDim.x;
+            const int f = fi(k);
             if (f < nxs) xl[mv_xslot(f >> 10, (f >> 4) & 63, f & 15)] = xr[k];
         }
     }
     __syncthreads();
     if (g0 >= n_groups) return;
 
-    float xv[kMvLaneElems];
-    float xs[4];
+    typename F::XReg xw;
     auto load_x = [&](int t) {
+        if constexpr (F::kPlanes) {
+            const uint4* rp = reinterpret_cast<const uint4*>(xrec + (t * kWave + lane) * kMvRecWords);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const float4 v = xl[mv_xslot(t, lane, j)];
-            xv[4 * j] = v.x; xv[4 * j + 1] = v.y; xv[4 * j + 2] = v.z; xv[4 * j + 3] = v.w;
+            for (int i = 0; i < 12; ++i) {
+                const uint4 u = rp[i];
+                xw.p[4 * i] = u.x; xw.p[4 * i + 1] = u.y; xw.p[4 * i + 2] = u.z; xw.p[4 * i + 3] = u.w;
+            }
+            const uint4 u = rp[12];
+            xw.inv[0] = __uint_as_float(u.x);
+            xw.inv[1] = __uint_as_float(u.y);
+            xw.sx[0] = (int)u.z;
+            xw.sx[1] = (int)u.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float4 v = xl[mv_xslot(t, lane, j)];
+                xw.v[4 * j] = v.x; xw.v[4 * j + 1] = v.y; xw.v[4 * j + 2] = v.z; xw.v[4 * j + 3] = v.w;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float s = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s += xw.v[16 * k + i];
+                xw.s[k] = s;
+            }
+            F::prep(xw.v);
         }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s += xv[16 * k + i];
-            xs[k] = s;
-        }
-        F::prep(xv);
     };
     if (ONE_TILE) load_x(0);
 
@@ -630,7 +766,7 @@ __global__ __launch_bounds__(ONE_TILE ? 256 : 512) void matvec_kernel(MvJob job,
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t* rowp = reinterpret_cast<const uint32_t*>(stage + r * T::kChunks);
-            if (live) acc[r] += F::dot(rowp, lane, xv, xs);
+            if (live) acc[r] += F::dot(rowp, lane, xw);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -739,6 +875,9 @@ __global__ __launch_bounds__(256) void matvec_any_kernel(MvJob job, MvTheta<EPI>
 template <int QT, int PRO, int EPI>
 static int mv_run(MvJob job, int cols, const MvTheta<EPI>& th, hipStream_t stream) {
     using F = MvFmt<QT>;
+    // 8-wave one-tile workgroups where the kernel fits four waves per SIMD:
+    // Q4_0 except the fused q / k / v launch (its RoPE table costs registers)
+    constexpr int WV1 = QT == kQ4_0 && EPI != kEpiQKV ? 8 : 4;
     using G = MvGroup<QT, EPI>;
     using GW = MvGroup<QT, EPI, true>;
     job.nb = cols / F::kElems;
@@ -751,20 +890,22 @@ static int mv_run(MvJob job, int cols, const MvTheta<EPI>& th, hipStream_t strea
     if (tiled) {
         const int stage_chunks = job.nt == 1 ? MvTile<QT, G::R>::kStageChunks
                                              : MvTile<QT, GW::R>::kStageChunks;
-        // wide matrices: 8 waves share one copy of x, 4 where 8 staging
-        // regions and x would not fit in the 160 KiB of LDS (7-tile Q8_0 / Q6_K)
-        int waves = job.nt == 1 ? 4 : 8;
-        if ((size_t)(job.nt * 1024 + waves * stage_chunks) * 16 > kMvLdsBytes) waves = 4;
+        // one-tile matrices: WV1 waves; wide ones: 8 waves share one copy of
+        // x, 4 where 8 staging regions and x would not fit in the 160 KiB of
+        // LDS (7-tile Q8_0 / Q6_K)
+        constexpr int xt16 = F::kPlanes ? kMvRecTile16 : 1024;  // x per tile, 16-byte units
+        int waves = job.nt == 1 ? WV1 : 8;
+        if ((size_t)(job.nt * xt16 + waves * stage_chunks) * 16 > kMvLdsBytes) waves = 4;
         int grid = (n_groups + waves - 1) / waves;
         // 512 workgroups (two per CU on 256 CUs) measured best for Q4_0 at
         // 4096-14336 rows; each wave then streams several items.
         if (grid > 512) grid = 512;
-        const size_t shmem = ((size_t)job.nt * 1024 + (size_t)waves * stage_chunks) * 16;
+        const size_t shmem = ((size_t)job.nt * xt16 + (size_t)waves * stage_chunks) * 16;
         if (job.nt == 1)
-            return launch(matvec_kernel<QT, true, PRO, EPI>, dim3(grid), dim3(waves * kWave),
+            return launch(matvec_kernel<QT, true, PRO, EPI, WV1>, dim3(grid), dim3(waves * kWave),
                           shmem, stream, job, th);
-        return launch(matvec_kernel<QT, false, PRO, EPI>, dim3(grid), dim3(waves * kWave), shmem,
-                      stream, job, th);
+        return launch(matvec_kernel<QT, false, PRO, EPI, 4>, dim3(grid), dim3(waves * kWave),
+                      shmem, stream, job, th);
     }
     const int any_groups = G::groups(job);
     if ((any_groups + 3) / 4 > 0x7FFFFFFF / 4) return JINF_HIP_ERR_INVALID;
