@@ -121,6 +121,46 @@ def test_one_hot_columns_exact(dev, qtype, cols):
         assert tu.bits_equal(y, Wf[:, j] + np.float32(0.0)), (NAMES[qtype], j)
 
 
+Q4 = [oracle.Q4_0, oracle.Q4_K]
+
+
+# The tiled kernel multiplies 4-bit codes with x rounded per 32-value block to
+# 22-bit fixed point (exponent from the block's largest |x|): the bar must
+# hold at both ends of the exponent range, and for a block whose values span
+# many binades.
+@pytest.mark.parametrize("qtype", Q4, ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("rows,cols", [(512, 4096), (256, 14336)])
+@pytest.mark.parametrize("scale", [2.0 ** -80, 2.0 ** 60, "spread"])
+def test_q4_x_scales(dev, qtype, rows, cols, scale):
+    say(f"{NAMES[qtype]} matvec {rows}x{cols}, x scale {scale}")
+    r = tu.rng(rows + qtype)
+    W = tu.quant_table(r, qtype, rows, cols)
+    if scale == "spread":  # |x| from 2^-40 to 2^10 within every block
+        x = (tu.normal(r, (cols,), 0.0, 1.0, np.float32) *
+             np.exp2(r.uniform(-40, 10, cols))).astype(np.float32)
+    else:
+        x = (tu.normal(r, (cols,), 0.0, 1.0, np.float64) * scale).astype(np.float32)
+    ref, a = _oracle(qtype, W, x)
+    y = host(jinf_amd.matvec(to_dev(W), to_dev(x), qtype))
+    check(y, ref, a, f"{NAMES[qtype]} scale {scale}")
+
+
+# A non-finite x value makes every row NaN in the tiled 4-bit kernel (its
+# block's scale is NaN); the reference's fp32 products give NaN (a zero
+# weight times inf, or any NaN) or +-inf there.
+@pytest.mark.parametrize("qtype", Q4, ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
+def test_q4_nonfinite_x_gives_nan_rows(dev, qtype, bad):
+    rows, cols = 256, 8192
+    say(f"{NAMES[qtype]} matvec with x[4100] = {bad}")
+    r = tu.rng(11 + qtype)
+    W = tu.quant_table(r, qtype, rows, cols)
+    x = tu.normal(r, (cols,), 0.0, 1.0, np.float32)
+    x[4100] = bad
+    y = host(jinf_amd.matvec(to_dev(W), to_dev(x), qtype))
+    assert np.all(np.isnan(y))
+
+
 def test_unsupported_qtype_leaves_output(dev):
     y = torch.full((16,), 3.0, dtype=torch.float32, device=dev)
     w = torch.zeros(16 * 20, dtype=torch.uint8, device=dev)
