@@ -466,11 +466,13 @@ __device__ __forceinline__ void cache_store(void* c, int64_t i, float a, float b
     }
 }
 
-// Finished values v[0..R) of group g (one lane).  rcs: the workgroup's
-// (cos, sin) table for the position (kEpiQKV; NULL: computed here).
+// Finished values v[0..R) of group g (one lane).  yo: kEpiAdd's y values of
+// the group's rows, loaded ahead (NULL: read here); pos: kEpiQKV's position;
+// rcs: its (cos, sin) table for the position (NULL: computed here).
 template <int QT, int EPI, bool WIDE = false>
 __device__ __forceinline__ void mv_epilogue(const MvJob& j, const MvTheta<EPI>& th, int g,
                                             float (&v)[MvGroup<QT, EPI, WIDE>::R],
+                                            const float* yo, int pos,
                                             const float2* rcs = nullptr) {
     constexpr int R = MvGroup<QT, EPI, WIDE>::R;
     if constexpr (EPI == kEpiStore) {
@@ -480,7 +482,7 @@ __device__ __forceinline__ void mv_epilogue(const MvJob& j, const MvTheta<EPI>& 
     } else if constexpr (EPI == kEpiAdd) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            if (g * R + r < j.rows) j.y[g * R + r] = j.y[g * R + r] + v[r];
+            if (g * R + r < j.rows) j.y[g * R + r] = (yo ? yo[r] : j.y[g * R + r]) + v[r];
     } else if constexpr (EPI == kEpiSwiGLU) {
         if (g < j.rows) j.y[g] = swiglu_exact(v[0], v[1]);
     } else {
@@ -488,7 +490,6 @@ __device__ __forceinline__ void mv_epilogue(const MvJob& j, const MvTheta<EPI>& 
         if (v0 >= j.rows) return;
         const int s = v0 < j.seg_end[0] ? 0 : v0 < j.seg_end[1] ? 1 : 2;
         const int local = v0 - (s == 0 ? 0 : j.seg_end[s - 1]);
-        const int pos = j.pos[0];
         float a = v[0], b = v[1];
         if (s < 2) {
             const int i = (local % j.head_dim) / 2;
@@ -543,7 +544,20 @@ __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob
     if (ONE_TILE) nt = 1;
 
     using Buf = uint4[R][CPL];
-    auto fetch = [&](int g, int t, Buf& buf) {
+    // kEpiAdd: the group's y values ride with each item's weights (loaded
+    // ahead, so the residual add does not wait for a load after the dot
+    // product; only the owning wave reads or writes a row of y)
+    using YBuf = float[R];
+    auto fetch = [&](int g, int t, Buf& buf, YBuf& yb) {
+        if constexpr (EPI == kEpiAdd) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int row = g * R + r < job.rows ? g * R + r : job.rows - 1;
+                yb[r] = job.y[row];
+            }
+        } else {
+            (void)yb;
+        }
         const int tb = t * T::kTileBlocks;
         const int nbt = nb - tb < T::kTileBlocks ? nb - tb : T::kTileBlocks;
         const int nchunk = nbt * F::kBytes / 16;  // whole by the width granule
@@ -570,6 +584,7 @@ __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob
     int g0 = blockIdx.x * waves + wave, t0 = 0;
     uint4 bufA[R][CPL];
     uint4 bufB[R][CPL];
+    float yA[R], yB[R];
 
     // Operands of the prologue are loaded before the first weight prefetch:
     // vector loads complete in order, so a load issued after the prefetch
@@ -624,7 +639,7 @@ __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob
     }
     // first weight item (a wave past the last group fetches the last row's
     // bytes and never uses them: the load count stays the same on every path)
-    fetch(g0, t0, bufA);
+    fetch(g0, t0, bufA, yA);
 
     // RoPE: the position's (cos, sin) for every pair index, computed once per
     // workgroup (one sin/cos per lane) instead of once per finished pair in
@@ -746,7 +761,18 @@ __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 
-    auto process = [&](int g, int t, const Buf& buf) {
+    // kEpiSwiGLU: lane k keeps the k-th finished group's gate and up sums
+    // (every lane holds the wave sums), and the lanes evaluate silu(gate) * up
+    // and store together, every 64 groups and at the end, instead of one
+    // lane per group while the wave waits
+    int sw_g = -1, sw_n = 0;
+    float sw_gate = 0.0f, sw_up = 0.0f;
+    auto sw_flush = [&]() {
+        if (sw_g >= 0) job.y[sw_g] = swiglu_exact(sw_gate, sw_up);
+        sw_g = -1;
+    };
+
+    auto process = [&](int g, int t, const Buf& buf, const YBuf& yb) {
         if (!ONE_TILE) load_x(t);
         const bool live = t * kMvTileElems + lane * kMvLaneElems < nb * F::kElems;
         // Every lane writes every chunk (no branch, so no load is left pending
@@ -778,7 +804,19 @@ __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob
                 v[r] = wave_sum_f32(acc[r]);
                 acc[r] = 0.0f;
             }
-            if (lane == 0) mv_epilogue<QT, EPI, !ONE_TILE>(job, th, g, v, rcs);
+            if constexpr (EPI == kEpiSwiGLU) {
+                if (lane == sw_n) {
+                    sw_g = g;  // below n_groups = rows
+                    sw_gate = v[0];
+                    sw_up = v[1];
+                }
+                if (++sw_n == kWave) {
+                    sw_flush();
+                    sw_n = 0;
+                }
+            } else if (lane == 0) {
+                mv_epilogue<QT, EPI, !ONE_TILE>(job, th, g, v, yb, rpos, rcs);
+            }
         }
     };
 
@@ -795,24 +833,25 @@ __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob
     while (rem > 2) {
         int g1 = g, t1 = t;
         advance(g1, t1);
-        fetch(g1, t1, bufB);
-        process(g, t, bufA);
+        fetch(g1, t1, bufB, yB);
+        process(g, t, bufA, yA);
         g = g1;
         t = t1;
         advance(g, t);
-        fetch(g, t, bufA);
-        process(g1, t1, bufB);
+        fetch(g, t, bufA, yA);
+        process(g1, t1, bufB, yB);
         rem -= 2;
     }
     if (rem == 2) {
         int g1 = g, t1 = t;
         advance(g1, t1);
-        fetch(g1, t1, bufB);
-        process(g, t, bufA);
-        process(g1, t1, bufB);
+        fetch(g1, t1, bufB, yB);
+        process(g, t, bufA, yA);
+        process(g1, t1, bufB, yB);
     } else {
-        process(g, t, bufA);
+        process(g, t, bufA, yA);
     }
+    if constexpr (EPI == kEpiSwiGLU) sw_flush();
 }
 
 // Any width / alignment: one wave per group of R rows; each lane takes
@@ -865,7 +904,7 @@ __global__ __launch_bounds__(256) void matvec_any_kernel(MvJob job, MvTheta<EPI>
     float v[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) v[r] = wave_sum_f32(acc[r]);
-    if (lane == 0) mv_epilogue<QT, EPI>(job, th, g, v);
+    if (lane == 0) mv_epilogue<QT, EPI>(job, th, g, v, nullptr, EPI == kEpiQKV ? job.pos[0] : 0);
 }
 
 // Launch a job: the tiled kernel with at most 512 workgroups when the shape
