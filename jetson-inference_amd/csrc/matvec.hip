@@ -510,6 +510,11 @@ __device__ __forceinline__ void mv_epilogue(const MvJob& j, const MvTheta<EPI>& 
     }
 }
 
+// Whether the kernel defers its epilogue to the end (at most 64 groups per
+// wave).  (Deferring the q / k / v epilogue as well measured 6.5 against 6.3
+// us: its groups are few per wave.)
+constexpr bool mv_defers(int epi) { return epi == kEpiSwiGLU; }
+
 // Each wave takes whole groups of R rows (groups g, g + stride, ...) and
 // walks their tiles in order, so a row's partial sums stay in registers until
 // its last tile.  The wave's LDS accesses execute in order; the fences keep
@@ -763,13 +768,17 @@ __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob
 
     // kEpiSwiGLU: lane k keeps the k-th finished group's gate and up sums
     // (every lane holds the wave sums), and the lanes evaluate silu(gate) * up
-    // and store together, every 64 groups and at the end, instead of one
-    // lane per group while the wave waits
-    int sw_g = -1, sw_n = 0;
-    float sw_gate = 0.0f, sw_up = 0.0f;
-    auto sw_flush = [&]() {
-        if (sw_g >= 0) job.y[sw_g] = swiglu_exact(sw_gate, sw_up);
-        sw_g = -1;
+    // and store together at the end, instead of one lane per group while the
+    // wave waits; the epilogue's registers are then not live in the loop.  A
+    // wave finishes at most 64 groups (mv_run sizes the grid so).
+    constexpr bool DEFER = mv_defers(EPI);
+    int dk_g = -1, dk_n = 0;
+    float dk_v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) dk_v[r] = 0.0f;
+    auto dk_flush = [&]() {
+        if (dk_g >= 0) mv_epilogue<QT, EPI, !ONE_TILE>(job, th, dk_g, dk_v, nullptr, rpos, rcs);
+        dk_g = -1;
     };
 
     auto process = [&](int g, int t, const Buf& buf, const YBuf& yb) {
@@ -804,16 +813,13 @@ __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob
                 v[r] = wave_sum_f32(acc[r]);
                 acc[r] = 0.0f;
             }
-            if constexpr (EPI == kEpiSwiGLU) {
-                if (lane == sw_n) {
-                    sw_g = g;  // below n_groups = rows
-                    sw_gate = v[0];
-                    sw_up = v[1];
+            if constexpr (DEFER) {
+                if (lane == dk_n) {
+                    dk_g = g;  // below n_groups
+#pragma unroll
+                    for (int r = 0; r < R; ++r) dk_v[r] = v[r];
                 }
-                if (++sw_n == kWave) {
-                    sw_flush();
-                    sw_n = 0;
-                }
+                ++dk_n;
             } else if (lane == 0) {
                 mv_epilogue<QT, EPI, !ONE_TILE>(job, th, g, v, yb, rpos, rcs);
             }
@@ -851,7 +857,7 @@ __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob
     } else {
         process(g, t, bufA, yA);
     }
-    if constexpr (EPI == kEpiSwiGLU) sw_flush();
+    if constexpr (DEFER) dk_flush();
 }
 
 // Any width / alignment: one wave per group of R rows; each lane takes
@@ -915,7 +921,8 @@ template <int QT, int PRO, int EPI>
 static int mv_run(MvJob job, int cols, const MvTheta<EPI>& th, hipStream_t stream) {
     using F = MvFmt<QT>;
     // 8-wave one-tile workgroups where the kernel fits four waves per SIMD:
-    // Q4_0 except the fused q / k / v launch (its RoPE table costs registers)
+    // Q4_0, except the fused q / k / v launch (154 VGPRs; with its epilogue
+    // deferred it fits, but its 1.5 groups per wave then ran 7.9 against 6.5 us)
     constexpr int WV1 = QT == kQ4_0 && EPI != kEpiQKV ? 8 : 4;
     using G = MvGroup<QT, EPI>;
     using GW = MvGroup<QT, EPI, true>;
@@ -937,8 +944,11 @@ static int mv_run(MvJob job, int cols, const MvTheta<EPI>& th, hipStream_t strea
         if ((size_t)(job.nt * xt16 + waves * stage_chunks) * 16 > kMvLdsBytes) waves = 4;
         int grid = (n_groups + waves - 1) / waves;
         // 512 workgroups (two per CU on 256 CUs) measured best for Q4_0 at
-        // 4096-14336 rows; each wave then streams several items.
+        // 4096-14336 rows; each wave then streams several items.  Deferred
+        // epilogues hold one finished group per lane: at most 64 per wave.
         if (grid > 512) grid = 512;
+        if (mv_defers(EPI) && (int64_t)grid * waves * kWave < n_groups)
+            grid = (int)(((int64_t)n_groups + waves * kWave - 1) / (waves * kWave));
         const size_t shmem = ((size_t)job.nt * xt16 + (size_t)waves * stage_chunks) * 16;
         if (job.nt == 1)
             return launch(matvec_kernel<QT, true, PRO, EPI, WV1>, dim3(grid), dim3(waves * kWave),
