@@ -572,7 +572,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
                 tmax = fmaxf(tmax, vm);
             }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+        tmax = xor32_max(tmax);
         const float mn = fmaxf(m, tmax);
         const float corr = exp_neg(m - mn);
         m = mn;
@@ -634,9 +634,9 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 #pragma unroll
     for (int n = 0; n < NB; ++n)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) O[n][r] += __shfl_xor(O[n][r], 32, kWave);
+        for (int r = 0; r < 4; ++r) O[n][r] = xor32_sum(O[n][r]);
     lsum += __shfl_xor(lsum, 16, kWave);
-    lsum += __shfl_xor(lsum, 32, kWave);
+    lsum = xor32_sum(lsum);
 
     // merge the four waves (wave order) through LDS
     __syncthreads();
