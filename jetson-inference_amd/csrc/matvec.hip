@@ -521,12 +521,15 @@ constexpr bool mv_defers(int epi) { return epi == kEpiSwiGLU; }
 // the compiler from moving the read-back above the stores.  Workgroup
 // barriers only follow the x staging.
 // WV1: waves of a one-tile workgroup (4, or 8 where the kernel fits four
-// waves per SIMD: one x staging for twice the waves).
-template <int QT, bool ONE_TILE, int PRO, int EPI, int WV1>
+// waves per SIMD: one x staging for twice the waves).  TALL: a one-tile
+// matrix with the wide row grouping (two rows per item for the one-row
+// formats), for very tall matrices.
+template <int QT, bool ONE_TILE, int PRO, int EPI, int WV1, bool TALL = false>
 __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob job,
                                                                            MvTheta<EPI> th) {
     using F = MvFmt<QT>;
-    using G = MvGroup<QT, EPI, !ONE_TILE>;
+    constexpr bool WIDE = !ONE_TILE || TALL;
+    using G = MvGroup<QT, EPI, WIDE>;
     constexpr int R = G::R;
     using T = MvTile<QT, R>;
     constexpr int CPL = T::kCPL;
@@ -568,7 +571,7 @@ __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob
         const int nchunk = nbt * F::kBytes / 16;  // whole by the width granule
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint8_t* src = mv_row<QT, EPI, !ONE_TILE>(job, g, r) + (int64_t)tb * F::kBytes;
+            const uint8_t* src = mv_row<QT, EPI, WIDE>(job, g, r) + (int64_t)tb * F::kBytes;
 #pragma unroll
             for (int k = 0; k < CPL; ++k) {
                 // Lanes past the tile's end re-read its last chunk (never used).
@@ -777,7 +780,7 @@ __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob
 #pragma unroll
     for (int r = 0; r < R; ++r) dk_v[r] = 0.0f;
     auto dk_flush = [&]() {
-        if (dk_g >= 0) mv_epilogue<QT, EPI, !ONE_TILE>(job, th, dk_g, dk_v, nullptr, rpos, rcs);
+        if (dk_g >= 0) mv_epilogue<QT, EPI, WIDE>(job, th, dk_g, dk_v, nullptr, rpos, rcs);
         dk_g = -1;
     };
 
@@ -821,7 +824,7 @@ __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob
                 }
                 ++dk_n;
             } else if (lane == 0) {
-                mv_epilogue<QT, EPI, !ONE_TILE>(job, th, g, v, yb, rpos, rcs);
+                mv_epilogue<QT, EPI, WIDE>(job, th, g, v, yb, rpos, rcs);
             }
         }
     };
@@ -929,13 +932,17 @@ static int mv_run(MvJob job, int cols, const MvTheta<EPI>& th, hipStream_t strea
     job.nb = cols / F::kElems;
     job.row_bytes = (int64_t)job.nb * F::kBytes;
     job.nt = (cols + kMvTileElems - 1) / kMvTileElems;
-    const int n_groups = job.nt == 1 ? G::groups(job) : GW::groups(job);
+    // Very tall one-tile matrices of the one-row formats (the output head,
+    // 128256 x 4096 Q6_K: 100 against 106 us) take two rows per item.
+    constexpr bool kTallable = F::kRows == 1 && EPI == kEpiStore;
+    const bool tall = kTallable && job.nt == 1 && job.rows >= 32768;
+    const int n_groups = job.nt == 1 && !tall ? G::groups(job) : GW::groups(job);
     bool tiled = cols % F::kColGranule == 0 && job.nt <= kMvMaxTiles && aligned(job.x, 16);
     for (int s = 0; s < 3; ++s) tiled = tiled && aligned(job.W[s], 16);
     if (PRO == kProNorm) tiled = tiled && aligned(job.norm_w, job.norm_f16 ? 8 : 16);
     if (tiled) {
-        const int stage_chunks = job.nt == 1 ? MvTile<QT, G::R>::kStageChunks
-                                             : MvTile<QT, GW::R>::kStageChunks;
+        const int stage_chunks = job.nt == 1 && !tall ? MvTile<QT, G::R>::kStageChunks
+                                                      : MvTile<QT, GW::R>::kStageChunks;
         // one-tile matrices: WV1 waves; wide ones: 8 waves share one copy of
         // x, 4 where 8 staging regions and x would not fit in the 160 KiB of
         // LDS (7-tile Q8_0 / Q6_K)
@@ -950,6 +957,11 @@ static int mv_run(MvJob job, int cols, const MvTheta<EPI>& th, hipStream_t strea
         if (mv_defers(EPI) && (int64_t)grid * waves * kWave < n_groups)
             grid = (int)(((int64_t)n_groups + waves * kWave - 1) / (waves * kWave));
         const size_t shmem = ((size_t)job.nt * xt16 + (size_t)waves * stage_chunks) * 16;
+        if constexpr (kTallable) {
+            if (tall)
+                return launch(matvec_kernel<QT, true, PRO, EPI, WV1, true>, dim3(grid),
+                              dim3(waves * kWave), shmem, stream, job, th);
+        }
         if (job.nt == 1)
             return launch(matvec_kernel<QT, true, PRO, EPI, WV1>, dim3(grid), dim3(waves * kWave),
                           shmem, stream, job, th);

@@ -121,6 +121,27 @@ def test_one_hot_columns_exact(dev, qtype, cols):
         assert tu.bits_equal(y, Wf[:, j] + np.float32(0.0)), (NAMES[qtype], j)
 
 
+# Very tall one-tile matrices of the one-row formats (an output head) take two
+# rows per item; an odd row count leaves the last item half empty.
+@pytest.mark.parametrize("qtype", [oracle.Q6_K, oracle.Q8_0], ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("norm", [False, True], ids=["plain", "rmsnorm"])
+def test_tall_one_tile(dev, qtype, norm):
+    rows, cols = 32769, 4096
+    say(f"{NAMES[qtype]} tall matvec {rows}x{cols} norm={norm}")
+    r = tu.rng(17 + qtype)
+    W = tu.quant_table(r, qtype, rows, cols)
+    h = tu.normal(r, (cols,), 0.0, 1.0, np.float32)
+    if norm:
+        g = (r.uniform(0.5, 1.5, cols)).astype(np.float32)
+        x = oracle.rmsnorm_rows(h.reshape(1, -1), g, 1e-5).reshape(-1)
+        ref, a = _oracle(qtype, W, x)
+        y = host(jinf_amd.rmsnorm_matvec(to_dev(W), to_dev(h), qtype, norm_w=to_dev(g)))
+    else:
+        ref, a = _oracle(qtype, W, h)
+        y = host(jinf_amd.matvec(to_dev(W), to_dev(h), qtype))
+    check(y, ref, a, f"{NAMES[qtype]} tall norm={norm}")
+
+
 Q4 = [oracle.Q4_0, oracle.Q4_K]
 
 
