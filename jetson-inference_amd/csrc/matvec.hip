@@ -121,19 +121,33 @@ struct MvXPlanes {
     int sx[2];       // sum of X over each block
 };
 
+// v_dot8_i32_i4 with a zero accumulator, in its three-operand form (the
+// compiler picks the two-operand accumulate-in-place form and first moves a
+// zero into the destination: six moves per block)
+__device__ __forceinline__ int sdot8_first(int a, int b) {
+    int r;
+    asm("v_dot8_i32_i4 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 // sum_j (q_j - 8) X_j + add over one 32-value block (code words q, planes
 // pl[0..24)), rounded once to fp32.
 __device__ __forceinline__ float plane_dot32(const uint32_t (&q)[4], const uint32_t* pl, int add) {
-    int P[6] = {0, 0, 0, 0, 0, 0};
+    int P[6];
+    {
+        const int qs = (int)(q[0] ^ 0x88888888u);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+        for (int k = 0; k < 6; ++k) P[k] = sdot8_first(qs, (int)pl[k]);
+    }
+#pragma unroll
+    for (int i = 1; i < 4; ++i) {
         const int qs = (int)(q[i] ^ 0x88888888u);
 #pragma unroll
         for (int k = 0; k < 6; ++k)
             P[k] = __builtin_amdgcn_sdot8(qs, (int)pl[6 * i + k], P[k], false);
     }
-    const int lo = P[0] + P[1] * 16 + P[2] * 256 + add;
-    const int hi = P[3] + P[4] * 16 + P[5] * 256;
+    const int lo = (P[2] * 16 + P[1]) * 16 + P[0] + add;
+    const int hi = (P[5] * 16 + P[4]) * 16 + P[3];
     return fmaf((float)hi, 4096.0f, (float)lo);
 }
 
