@@ -537,8 +537,9 @@ constexpr bool mv_defers(int epi) { return epi == kEpiSwiGLU; }
 // WV1: waves of a one-tile workgroup (4, or 8 where the kernel fits four
 // waves per SIMD: one x staging for twice the waves).  TALL: a one-tile
 // matrix with the wide row grouping (two rows per item for the one-row
-// formats), for very tall matrices.
-template <int QT, bool ONE_TILE, int PRO, int EPI, int WV1, bool TALL = false>
+// formats), for very tall matrices.  XW: float4 of x each thread of a wide
+// workgroup loads (enough for its tiles; loads past them are branches).
+template <int QT, bool ONE_TILE, int PRO, int EPI, int WV1, bool TALL = false, int XW = 28>
 __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob job,
                                                                            MvTheta<EPI> th) {
     using F = MvFmt<QT>;
@@ -613,8 +614,11 @@ __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob
     // would make the x staging, the norm and the RoPE table wait for the
     // weights' HBM latency instead of overlapping it.  x (zero past the last
     // value): XPT float4 per thread cover the staged tiles (one tile: 1024
-    // float4 over 256 threads; at most 7 tiles over 256 or 512 threads).
-    constexpr int XPT = ONE_TILE ? 16 / WV1 : 28;
+    // float4 over 64 WV1 threads; wide: XW, chosen by the launcher for the
+    // tile count: unneeded slots would each cost a branch and 4 registers,
+    // and the 4-tile down projection stages in 9.4 against 10.2 us with 8
+    // slots instead of 28).
+    constexpr int XPT = ONE_TILE ? 16 / WV1 : XW;
     // float4 number of slot k: plane formats take word groups of two
     // consecutive float4 (group threadIdx.x + (k / 2) blockDim.x)
     auto fi = [&](int k) {
@@ -979,8 +983,19 @@ static int mv_run(MvJob job, int cols, const MvTheta<EPI>& th, hipStream_t strea
         if (job.nt == 1)
             return launch(matvec_kernel<QT, true, PRO, EPI, WV1>, dim3(grid), dim3(waves * kWave),
                           shmem, stream, job, th);
-        return launch(matvec_kernel<QT, false, PRO, EPI, 4>, dim3(grid), dim3(waves * kWave),
-                      shmem, stream, job, th);
+        // x float4 per thread for the wide kernel: nt tiles of 1024 float4
+        const int xw = (job.nt * 1024 + waves * kWave - 1) / (waves * kWave);
+        if (xw <= 4)
+            return launch(matvec_kernel<QT, false, PRO, EPI, 4, false, 4>, dim3(grid),
+                          dim3(waves * kWave), shmem, stream, job, th);
+        if (xw <= 8)
+            return launch(matvec_kernel<QT, false, PRO, EPI, 4, false, 8>, dim3(grid),
+                          dim3(waves * kWave), shmem, stream, job, th);
+        if (xw <= 14)
+            return launch(matvec_kernel<QT, false, PRO, EPI, 4, false, 14>, dim3(grid),
+                          dim3(waves * kWave), shmem, stream, job, th);
+        return launch(matvec_kernel<QT, false, PRO, EPI, 4, false, 28>, dim3(grid),
+                      dim3(waves * kWave), shmem, stream, job, th);
     }
     const int any_groups = G::groups(job);
     if ((any_groups + 3) / 4 > 0x7FFFFFFF / 4) return JINF_HIP_ERR_INVALID;
