@@ -391,66 +391,80 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
 // three workgroups per CU.  (8-wave shapes over 128 or 256 rows sharing each
 // x record, with two slots so that the next slab's weights are in flight
 // during the matrix-core work, measured slower.)
-// LDS slot: the weight chunks (NWI KiB), then the x record (NXI KiB), filled
-// by 1 KiB direct-to-LDS instructions dealt round-robin to the waves.
+// Where the x fragments go: one M-tile (up to 32 sequences) straight into
+// registers, each wave its own k-steps' fragments; two M-tiles, and Q6_K
+// (whose decode needs more registers), through the LDS slot with the weights
+// (the registers would not fit beside the accumulators).
+template <int QT, int MT> constexpr bool mb_xlds() { return MT > 1 || QT == kQ6_K; }
+// LDS slot: the weight chunks (NWI KiB), then the record's x fragments and
+// sums (x through LDS) or, for Q4_K, only its x sums (NXI KiB), filled by
+// 1 KiB direct-to-LDS instructions dealt round-robin to the waves.
 template <int QT, int NT> constexpr int mb_nwi() { return (32 * NT * mb_nch<QT>() * 16 + 1023) / 1024; }
-template <int MT> constexpr int mb_nxi() { return mb_rec(MT) / 1024; }
+template <int QT, int MT> constexpr int mb_nxi() {
+    return mb_xlds<QT, MT>() ? mb_rec(MT) / 1024 : QT == kQ4_K ? mb_meta(MT) / 1024 : 0;
+}
 template <int QT, int MT, int NT> constexpr int mb_slot() {
-    return (mb_nwi<QT, NT>() + mb_nxi<MT>()) * 1024;
+    return (mb_nwi<QT, NT>() + mb_nxi<QT, MT>()) * 1024;
 }
-constexpr int kMbLdsBudget = 160 * 1024 - 512;  // room for the kernel's static LDS
-template <int QT, int MT, int NT, int WV> constexpr int mb_nbuf() {
-    return WV == 4 ? 1 : 2 * mb_slot<QT, MT, NT>() <= kMbLdsBudget ? 2 : 1;
-}
-template <int QT, int MT, int NT, int WV> constexpr int mb_lds_bytes() {
-    return mb_nbuf<QT, MT, NT, WV>() * mb_slot<QT, MT, NT>() > (8 * MT * 4096)
-               ? mb_nbuf<QT, MT, NT, WV>() * mb_slot<QT, MT, NT>()
-               : (8 * MT * 4096);
+// weight slots (slabs whose weights are in LDS or in flight; one slot when
+// x goes through LDS) and x register sets (slabs whose fragments are in
+// registers or in flight)
+template <int QT, int MT> constexpr int mb_nbuf() { return mb_xlds<QT, MT>() ? 1 : 2; }
+template <int QT, int MT> constexpr int mb_xbuf() { return mb_xlds<QT, MT>() ? 1 : 2; }
+constexpr int mb_lcm(int a, int b) { return a % b == 0 ? a : b % a == 0 ? b : a * b; }
+template <int QT, int MT, int NT> constexpr int mb_lds_bytes() {
+    return mb_nbuf<QT, MT>() * mb_slot<QT, MT, NT>() > (8 * MT * 4096) ? mb_nbuf<QT, MT>() * mb_slot<QT, MT, NT>()
+                                                                   : (8 * MT * 4096);
 }
 // loads per lane per slab for wave w of WV
 constexpr int mb_share(int n, int w, int wv) { return (n - w + wv - 1) / wv; }
 
-template <int N>
-__device__ __forceinline__ void mb_wait_n(int after) {
-    // at most `after` slabs' loads (N per slab) still outstanding
-    if (after >= 1)
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm<N>());
-    else
+// Wait until this wave's LDS loads of the current step have landed: the
+// NBUF - 2 later steps' loads (NXL x register loads and the wave's share of
+// the slot's instructions per step) may still be in flight (none with one
+// slot: its loads are issued in the step itself).
+template <int NWI, int NXI, int NXL, int NBUF, int WV, int W = 0>
+__device__ __forceinline__ void mb_wait_w(int wave) {
+    if constexpr (NBUF == 1) {
         __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
-}
-
-template <int NWI, int NXI, int WV, int W = 0>
-__device__ __forceinline__ void mb_wait_slabs(int wave, int after) {
-    if constexpr (W < WV) {
+    } else if constexpr (W < WV) {
         if (wave == W) {
-            mb_wait_n<mb_share(NWI, W, WV) + mb_share(NXI, W, WV)>(after);
+            constexpr int n = (NBUF - 2) * (NXL + mb_share(NWI, W, WV) + mb_share(NXI, W, WV));
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm<n>());
             return;
         }
-        mb_wait_slabs<NWI, NXI, WV, W + 1>(wave, after);
+        mb_wait_w<NWI, NXI, NXL, NBUF, WV, W + 1>(wave);
     }
 }
 
+template <int MT> constexpr int mb_occ() { return 2; }  // waves per SIMD the kernel is sized for
 template <int QT, int MT, int EPI, int NT, int WV, int KSW>
-__global__ __launch_bounds__(64 * WV) void matvec_batch_kernel(MbJob j, MbTheta<EPI> th) {
+__global__ __launch_bounds__(64 * WV, 4 * mb_occ<MT>() / WV) void matvec_batch_kernel(MbJob j, MbTheta<EPI> th) {
     constexpr int THREADS = 64 * WV;
     constexpr int ROWS = 32 * NT;
     constexpr int NCH = mb_nch<QT>();
     constexpr int SB = MbFmt<QT>::SB;
     constexpr int NWI = mb_nwi<QT, NT>();
-    constexpr int NXI = mb_nxi<MT>();
+    constexpr bool XL = mb_xlds<QT, MT>();
+    constexpr int NXI = mb_nxi<QT, MT>();
     constexpr int WB = NWI * 1024;
     constexpr int REC = mb_rec(MT);
     constexpr int SLOT = mb_slot<QT, MT, NT>();
-    constexpr int NBUF = mb_nbuf<QT, MT, NT, WV>();
+    constexpr int NBUF = mb_nbuf<QT, MT>();
+    constexpr int XB = mb_xbuf<QT, MT>();
     constexpr int NWL = (NWI + WV - 1) / WV;  // most weight loads of one lane per slab
     constexpr int TPW = NT * KSW / WV;        // tiles per wave
     constexpr int KPW = 16 / KSW;             // k-steps per wave
+    constexpr int NXL = XL ? 0 : MT * KPW * 2;  // x register loads of one lane per slab
     static_assert(TPW >= 1 && NT * KSW == TPW * WV && KPW % 4 == 0, "shape");
-    static_assert(NBUF < 2 || NWL + (NXI + WV - 1) / WV < 64, "vmcnt range");
+    static_assert(XL ? NBUF == 1 && XB == 1 : NBUF >= 2 && XB >= 1 && XB <= NBUF, "pipeline depths");
+    static_assert(NBUF < 2 || (NBUF - 2) * (NXL + NWL + (NXI + WV - 1) / WV) < 64, "vmcnt range");
     extern __shared__ __attribute__((aligned(16))) uint8_t mb_lds[];
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63, h = lane >> 5, col = lane & 31;
+    // wave index in a scalar register (wave-uniform branches)
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, h = lane >> 5, col = lane & 31;
     const int kpart = wave / (WV / KSW);
     const int tile0 = (wave % (WV / KSW)) * TPW;
     const int k0 = kpart * KPW;
@@ -470,8 +484,10 @@ __global__ __launch_bounds__(64 * WV) void matvec_batch_kernel(MbJob j, MbTheta<
         wch[k] = row < ROWS ? ci % NCH : 0;
         wrow[k] = mb_row<EPI, ROWS>(j, group, row < ROWS ? row : ROWS - 1);
     }
-    auto issue = [&](int s) {
-        uint8_t* slot = mb_lds + ((s - s0) % NBUF) * SLOT;
+    // Weights (and Q4_K's x sums) of slab s into LDS slot si: 1 KiB
+    // direct-to-LDS instructions dealt round-robin to the waves.
+    auto issue_w = [&](int s, int si) {
+        uint8_t* slot = mb_lds + si * SLOT;
 #pragma unroll
         for (int k = 0; k < NWL; ++k) {
             const int ins = wave + WV * k;
@@ -482,13 +498,32 @@ __global__ __launch_bounds__(64 * WV) void matvec_batch_kernel(MbJob j, MbTheta<
             const int c = wch[k] < last ? wch[k] : last;
             lds_load16(reinterpret_cast<const void*>(a0 + 16 * (uintptr_t)c), slot + ins * 1024);
         }
-        const uint8_t* src = j.xrec + (int64_t)s * REC;
+        if constexpr (NXI > 0) {
+            // the whole record (x through LDS), else its x sums
+            const uint8_t* src = j.xrec + (int64_t)s * REC + (XL ? 0 : MT * 32768);
 #pragma unroll
-        for (int k = 0; k < (NXI + WV - 1) / WV; ++k) {
-            const int ins = wave + WV * k;
-            if (ins >= NXI) break;
-            lds_load16(src + ins * 1024 + 16 * lane, slot + WB + ins * 1024);
+            for (int k = 0; k < (NXI + WV - 1) / WV; ++k) {
+                const int ins = wave + WV * k;
+                if (ins >= NXI) break;
+                lds_load16(src + ins * 1024 + 16 * lane, slot + WB + ins * 1024);
+            }
         }
+    };
+    // The wave's x fragments of slab s (its k-steps, hi and lo, every
+    // M-tile) into registers: each fragment is 1 KiB of the record, one
+    // 16-byte load per lane.
+    using XR = mb_h8[MT][KPW][2];
+    auto issue_x = [&](int s, XR& xr) {
+        if constexpr (XL) return;
+        const uint8_t* src = j.xrec + (int64_t)s * REC + lane * 16;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int k = 0; k < KPW; ++k)
+#pragma unroll
+                for (int hl = 0; hl < 2; ++hl)
+                    xr[mt][k][hl] = *reinterpret_cast<const mb_h8*>(
+                        src + ((mt * 16 + k0 + k) * 2 + hl) * 1024);
     };
 
     mb_f16 acc[TPW][MT];
@@ -499,163 +534,181 @@ __global__ __launch_bounds__(64 * WV) void matvec_batch_kernel(MbJob j, MbTheta<
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[nt][mt][r] = 0.0f;
 
-    int issued = s0;
-    for (; issued < s1 && issued < s0 + NBUF - 1; ++issued) issue(issued);
-    for (int s = s0; s < s1; ++s) {
-        if (issued < s1) {
-            issue(issued);
-            ++issued;
-        }
-        mb_wait_slabs<NWI, NXI, WV>(wave, issued - 1 - s);
-        __syncthreads();
-        const uint8_t* slot = mb_lds + ((s - s0) % NBUF) * SLOT;
-        const uint8_t* xa = slot + WB + lane * 16;
-        const float* meta = reinterpret_cast<const float*>(slot + WB + MT * 32768);
+    // Offset of each of the lane's rows' slab start inside its first 16-byte
+    // chunk: the low bits of the row's address, taken once here (the row
+    // pointer is picked from the job's matrices with a lane-dependent index,
+    // a memory load that inside the loop would wait for every load in flight).
+    uint32_t rlow[TPW];
+#pragma unroll
+    for (int nt = 0; nt < TPW; ++nt)
+        rlow[nt] = (uint32_t)(uintptr_t)mb_row<EPI, ROWS>(j, group, (tile0 + nt) * 32 + col) & 15u;
 
-        // the wave's tiles advance together: their matrix-core chains are
-        // independent, and each x fragment is read once per k-step
-        const uint8_t* rb[TPW];
+    auto compute = [&](const uint8_t* slot, const XR& xr, int s) {
+            // Q4_K: x sums
+            const float* meta = reinterpret_cast<const float*>(slot + WB + (XL ? MT * 32768 : 0));
+            // x fragment (M-tile mt, the wave's k-step kl, hi or lo)
+            auto xfrag = [&](int mt, int kl, int hl) -> mb_h8 {
+                if constexpr (XL)
+                    return *reinterpret_cast<const mb_h8*>(slot + WB + ((mt * 16 + k0 + kl) * 2 + hl) * 1024 +
+                                                           lane * 16);
+                else
+                    return xr[mt][kl][hl];
+            };
+
+            // The wave's tiles one after the other: a tile's block sums are
+            // finished and scaled before the next tile's start, so the
+            // partial-sum registers are those of one tile (MT chains).
+            const uint8_t* rb[TPW];
 #pragma unroll
-        for (int nt = 0; nt < TPW; ++nt) {
-            const int row = (tile0 + nt) * 32 + col;
-            const uintptr_t a = (uintptr_t)(mb_row<EPI, ROWS>(j, group, row) + (int64_t)s * SB);
-            rb[nt] = slot + row * NCH * 16 + (int)(a & 15);
-        }
-        // k-step t: tmp[nt][mt] += A(t) B[nt](t) for the hi and lo halves of A
-        auto mfma_step = [&](int t, const mb_h8 (&B)[TPW], mb_f16 (&tmp)[TPW][MT]) {
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                const uint8_t* xp = xa + (mt * 16 + t) * 2048;
-                const mb_h8 ah = *reinterpret_cast<const mb_h8*>(xp);
-                const mb_h8 al = *reinterpret_cast<const mb_h8*>(xp + 1024);
-#pragma unroll
-                for (int nt = 0; nt < TPW; ++nt) tmp[nt][mt] = mfma(ah, B[nt], tmp[nt][mt]);
-#pragma unroll
-                for (int nt = 0; nt < TPW; ++nt) tmp[nt][mt] = mfma(al, B[nt], tmp[nt][mt]);
+            for (int nt = 0; nt < TPW; ++nt) {
+                const int row = (tile0 + nt) * 32 + col;
+                rb[nt] = slot + row * NCH * 16 + (int)((rlow[nt] + (uint32_t)s * SB) & 15u);
             }
-        };
-        auto zero = [](mb_f16 (&tmp)[TPW][MT]) {
+            // the wave's k-step kl (k0 + kl of the slab): tmp[mt] += A B for
+            // the hi and lo halves of A
+            auto mfma_step = [&](int kl, const mb_h8& B, mb_f16 (&tmp)[MT]) {
 #pragma unroll
-            for (int nt = 0; nt < TPW; ++nt)
+                for (int mt = 0; mt < MT; ++mt) {
+                    tmp[mt] = mfma(xfrag(mt, kl, 0), B, tmp[mt]);
+                    tmp[mt] = mfma(xfrag(mt, kl, 1), B, tmp[mt]);
+                }
+            };
+            auto zero = [&](mb_f16 (&tmp)[MT]) {
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) tmp[nt][mt][r] = 0.0f;
-        };
+                    for (int r = 0; r < 16; ++r) tmp[mt][r] = 0.0f;
+            };
 
-        if constexpr (QT == kQ4_0 || QT == kQ8_0) {
-            constexpr int BB = QT == kQ4_0 ? 18 : 34;
-#pragma unroll
-            for (int bi = 0; bi < KPW / 2; ++bi) {
-                const int blk = k0 / 2 + bi;
-                float d[TPW];
-                mb_f16 tmp[TPW][MT];
-                zero(tmp);
-#pragma unroll
-                for (int part = 0; part < 2; ++part) {
-                    mb_h8 B[TPW];
-#pragma unroll
-                    for (int nt = 0; nt < TPW; ++nt) {
-                        const uint8_t* bp = rb[nt] + BB * blk;
-                        if (part == 0) d[nt] = h2f((uint16_t)lds_u16(bp));
-                        if constexpr (QT == kQ4_0) {
-                            B[nt] = mb_nibbles(lds_u32(bp + 2 + 8 * part + 4 * h), 0u, -8.0f);
-                        } else {
-                            const uint8_t* qp = bp + 2 + 16 * part + 8 * h;
-                            B[nt] = mb_int8(lds_u32(qp), lds_u32(qp + 4));
-                        }
-                    }
-                    mfma_step(2 * blk + part, B, tmp);
-                }
-#pragma unroll
-                for (int nt = 0; nt < TPW; ++nt)
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r)
-                            acc[nt][mt][r] = fmaf(d[nt], tmp[nt][mt][r], acc[nt][mt][r]);
-            }
-        } else if constexpr (QT == kQ4_K) {
-            constexpr int NSB = KPW / 2;  // sub-blocks of this wave
-            float d[TPW], mn[TPW][NSB];
-            _Float16 f[TPW][NSB];
 #pragma unroll
             for (int nt = 0; nt < TPW; ++nt) {
-                d[nt] = h2f((uint16_t)lds_u16(rb[nt]));
-                const float dmin = h2f((uint16_t)lds_u16(rb[nt] + 2));
-                uint32_t sw[3];
+                if constexpr (QT == kQ4_0 || QT == kQ8_0) {
+                    constexpr int BB = QT == kQ4_0 ? 18 : 34;
 #pragma unroll
-                for (int k = 0; k < 3; ++k) sw[k] = lds_u32(rb[nt] + 4 + 4 * k);
+                    for (int bi = 0; bi < KPW / 2; ++bi) {
+                        const uint8_t* bp = rb[nt] + BB * (k0 / 2 + bi);
+                        const float d = h2f((uint16_t)lds_u16(bp));
+                        mb_f16 tmp[MT];
+                        zero(tmp);
 #pragma unroll
-                for (int q = 0; q < NSB; ++q) {
-                    int sc, m;
-                    q4_K_scale_min(sw, k0 / 2 + q, sc, m);
-                    f[nt][q] = (_Float16)(float)sc;
-                    mn[nt][q] = dmin * (float)m;
-                }
-            }
-            mb_f16 tmp[TPW][MT];
-            zero(tmp);
+                        for (int part = 0; part < 2; ++part) {
+                            mb_h8 B;
+                            if constexpr (QT == kQ4_0) {
+                                B = mb_nibbles(lds_u32(bp + 2 + 8 * part + 4 * h), 0u, -8.0f);
+                            } else {
+                                const uint8_t* qp = bp + 2 + 16 * part + 8 * h;
+                                B = mb_int8(lds_u32(qp), lds_u32(qp + 4));
+                            }
+                            mfma_step(2 * bi + part, B, tmp);
+                        }
 #pragma unroll
-            for (int k = 0; k < KPW; ++k) {
-                const int t = k0 + k;
-                mb_h8 B[TPW];
+                        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int nt = 0; nt < TPW; ++nt) {
-                    const _Float16 g = f[nt][k >> 1];
-                    B[nt] = mb_nibbles(lds_u32(rb[nt] + 16 + 8 * t + 4 * h), 0u, 0.0f) *
-                            mb_h8{g, g, g, g, g, g, g, g};  // sc * q <= 945: exact
-                }
-                mfma_step(t, B, tmp);
-            }
-            const float* xs = meta + 32 * MT;
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int b = mb_token(mt, r, h);
-                    float xq[NSB];
-#pragma unroll
-                    for (int q = 0; q < NSB; ++q) xq[q] = xs[(k0 / 2 + q) * 32 * MT + b];
-#pragma unroll
-                    for (int nt = 0; nt < TPW; ++nt) {
-                        float mins = 0.0f;
-#pragma unroll
-                        for (int q = 0; q < NSB; ++q) mins = fmaf(mn[nt][q], xq[q], mins);
-                        acc[nt][mt][r] += d[nt] * tmp[nt][mt][r] - mins;
+                            for (int r = 0; r < 16; ++r)
+                                acc[nt][mt][r] = fmaf(d, tmp[mt][r], acc[nt][mt][r]);
                     }
-                }
-        } else {
-            static_assert(QT == kQ6_K, "format");
-            float d[TPW];
+                } else if constexpr (QT == kQ4_K) {
+                    constexpr int NSB = KPW / 2;  // sub-blocks of this wave
+                    const float d = h2f((uint16_t)lds_u16(rb[nt]));
+                    const float dmin = h2f((uint16_t)lds_u16(rb[nt] + 2));
+                    uint32_t sw[3];
 #pragma unroll
-            for (int nt = 0; nt < TPW; ++nt) d[nt] = h2f((uint16_t)lds_u16(rb[nt] + 208));
+                    for (int k = 0; k < 3; ++k) sw[k] = lds_u32(rb[nt] + 4 + 4 * k);
+                    float mn[NSB];
+                    _Float16 f[NSB];
 #pragma unroll
-            for (int k = 0; k < KPW; ++k) {
-                const int t = k0 + k;
-                mb_h8 B[TPW];
-                float ds[TPW];
+                    for (int q = 0; q < NSB; ++q) {
+                        int sc, m;
+                        q4_K_scale_min(sw, k0 / 2 + q, sc, m);
+                        f[q] = (_Float16)(float)sc;
+                        mn[q] = dmin * (float)m;
+                    }
+                    mb_f16 tmp[MT];
+                    zero(tmp);
 #pragma unroll
-                for (int nt = 0; nt < TPW; ++nt) {
-                    ds[nt] = d[nt] * (float)(int8_t)rb[nt][192 + t];
-                    const uint32_t hq = lds_u16(rb[nt] + 128 + 4 * t + 2 * h);
-                    const uint32_t hs = (hq & 0xFFu) | ((hq & 0xFF00u) << 8);
-                    B[nt] = mb_nibbles(lds_u32(rb[nt] + 8 * t + 4 * h), hs, -32.0f);
-                }
-                mb_f16 tmp[TPW][MT];
-                zero(tmp);
-                mfma_step(t, B, tmp);
-#pragma unroll
-                for (int nt = 0; nt < TPW; ++nt)
+                    for (int k = 0; k < KPW; ++k) {
+                        const _Float16 g = f[k >> 1];
+                        const mb_h8 B = mb_nibbles(lds_u32(rb[nt] + 16 + 8 * (k0 + k) + 4 * h), 0u, 0.0f) *
+                                        mb_h8{g, g, g, g, g, g, g, g};  // sc * q <= 945: exact
+                        mfma_step(k, B, tmp);
+                    }
+                    const float* xs = meta + 32 * MT;
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r)
-                            acc[nt][mt][r] = fmaf(ds[nt], tmp[nt][mt][r], acc[nt][mt][r]);
+                        for (int r = 0; r < 16; ++r) {
+                            const int b = mb_token(mt, r, h);
+                            float mins = 0.0f;
+#pragma unroll
+                            for (int q = 0; q < NSB; ++q)
+                                mins = fmaf(mn[q], xs[(k0 / 2 + q) * 32 * MT + b], mins);
+                            acc[nt][mt][r] += d * tmp[mt][r] - mins;
+                        }
+                } else {
+                    static_assert(QT == kQ6_K, "format");
+                    const float d = h2f((uint16_t)lds_u16(rb[nt] + 208));
+#pragma unroll
+                    for (int k = 0; k < KPW; ++k) {
+                        const int t = k0 + k;
+                        const float ds = d * (float)(int8_t)rb[nt][192 + t];
+                        const uint32_t hq = lds_u16(rb[nt] + 128 + 4 * t + 2 * h);
+                        const uint32_t hs = (hq & 0xFFu) | ((hq & 0xFF00u) << 8);
+                        const mb_h8 B = mb_nibbles(lds_u32(rb[nt] + 8 * t + 4 * h), hs, -32.0f);
+                        mb_f16 tmp[MT];
+                        zero(tmp);
+                        mfma_step(k, B, tmp);
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                                acc[nt][mt][r] = fmaf(ds, tmp[mt][r], acc[nt][mt][r]);
+                    }
+                }
+            }
+    };
+
+    // Pipeline: step i (slab s0 + i) waits for its weights and x, passes the
+    // workgroup barrier (after which every wave has finished step i - 1, so
+    // its slot may be refilled), issues x for step i + XB - 1 and weights for
+    // step i + NBUF - 1, then multiplies.  Every step issues the same loads
+    // (steps past the last slab re-read the last slab: cache hits, never
+    // multiplied), so the wait count is one constant per wave and the
+    // compiler's own waits on the x registers see the same loads in flight
+    // on every path.  The prologue issues NBUF - 1 steps' loads in the same
+    // order (x of steps before 0 re-reads slab s0 into the register set that
+    // step XB - 1's load overwrites).
+    const int ns = s1 - s0;
+    auto clamp = [&](int i) { return s0 + (i < ns ? i : ns - 1); };
+    XR xr[XB];
+#pragma unroll
+    for (int v = -(NBUF - 1); v < 0; ++v) {
+        const int xi = v + XB - 1;
+        issue_x(clamp(xi < 0 ? 0 : xi), xr[(xi + XB * NBUF) % XB]);
+        issue_w(clamp(v + NBUF - 1), (v + NBUF - 1) % NBUF);
+    }
+    constexpr int U = mb_lcm(NBUF, XB);
+    for (int base = 0; base < ns; base += U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = base + u;
+            if constexpr (NBUF == 1) {
+                // one slot: this step's loads, then its product, then a
+                // barrier before the next step refills the slot
+                issue_w(clamp(i), 0);
+                mb_wait_w<NWI, NXI, NXL, NBUF, WV>(wave);
+                __syncthreads();
+                if (i < ns) compute(mb_lds, xr[0], s0 + i);
+                __syncthreads();
+            } else {
+                mb_wait_w<NWI, NXI, NXL, NBUF, WV>(wave);
+                __syncthreads();
+                issue_x(clamp(i + XB - 1), xr[(u + XB - 1) % XB]);
+                issue_w(clamp(i + NBUF - 1), (u + NBUF - 1) % NBUF);
+                if (i < ns) compute(mb_lds + (u % NBUF) * SLOT, xr[u % XB], s0 + i);
             }
         }
-        __syncthreads();  // the slot is refilled by a later issue
     }
+    __syncthreads();  // the reduction below reuses the slots
     // the sums are in units of x * s: 1 / s per token (the same in every
     // slab's record) scales them exactly
     {
@@ -869,7 +922,7 @@ template <int QT, int MT, int EPI, int NT, int WV, int KSW>
 int mb_launch_shape(MbJob& j, const MbTheta<EPI>& th, hipStream_t stream) {
     const dim3 grid((unsigned)(j.n_groups * j.k_splits));
     return launch(matvec_batch_kernel<QT, MT, EPI, NT, WV, KSW>, grid, dim3(64 * WV),
-                  mb_lds_bytes<QT, MT, NT, WV>(), stream, j, th);
+                  mb_lds_bytes<QT, MT, NT>(), stream, j, th);
 }
 
 template <int QT, int MT, int EPI>
@@ -912,7 +965,7 @@ template <int QT, int EPI>
 int mb_dispatch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void* norm_w,
                   int norm_f16, float eps, hipStream_t stream) {
     if (j.n_batch <= 32) return mb_launch_t<QT, 1, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
-    const bool fits = mb_slot<QT, 2, 2>() <= kMbLdsBudget;
+    constexpr bool fits = mb_lds_bytes<QT, 2, 2>() <= 160 * 1024 - 512;  // static LDS aside
     if (fits) return mb_launch_t<QT, 2, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
     MbJob lo = j;
     lo.n_batch = 32;
