@@ -919,14 +919,14 @@ _KERNEL_KEYS = [("ew_vec_kernel<unsigned short, 1", "swiglu"),
                 ("softmax_loop_kernel", "softmax_loop"),
                 # the one-tile kernels serve q, k, v, o, gate, up; the multi-tile
                 # kernels only down (14336 columns) in the GEMV workloads
-                ("matvec_kernel<2, true, 0, 0>", "gemv_one_tile (q,k,v,o,gate,up)"),
-                ("matvec_kernel<8, true, 0, 0>", "gemv_one_tile (q,k,v,o,gate,up)"),
-                ("matvec_kernel<12, true, 0, 0>", "gemv_one_tile Q4_K (q,k,o,gate,up)"),
-                ("matvec_kernel<14, true, 0, 0>", "gemv_one_tile Q6_K (v)"),
-                ("matvec_kernel<2, false, 0, 0>", "gemv_down"),
-                ("matvec_kernel<8, false, 0, 0>", "gemv_down"),
-                ("matvec_kernel<12, false, 0, 0>", "gemv_down"),
-                ("matvec_kernel<14, false, 0, 0>", "gemv_down"),
+                ("matvec_kernel<2, true, 0, 0,", "gemv_one_tile (q,k,v,o,gate,up)"),
+                ("matvec_kernel<8, true, 0, 0,", "gemv_one_tile (q,k,v,o,gate,up)"),
+                ("matvec_kernel<12, true, 0, 0,", "gemv_one_tile Q4_K (q,k,o,gate,up)"),
+                ("matvec_kernel<14, true, 0, 0,", "gemv_one_tile Q6_K (v)"),
+                ("matvec_kernel<2, false, 0, 0,", "gemv_down"),
+                ("matvec_kernel<8, false, 0, 0,", "gemv_down"),
+                ("matvec_kernel<12, false, 0, 0,", "gemv_down"),
+                ("matvec_kernel<14, false, 0, 0,", "gemv_down"),
                 ("matvec_any_kernel", "gemv_generic"),
                 ("attn_decode_kernel", "gqa_attention"),
                 ("attn_mfma_kernel", "gqa_attention"),
@@ -943,6 +943,10 @@ _KERNEL_KEYS = [("ew_vec_kernel<unsigned short, 1", "swiglu"),
                 ("matvec_batch_kernel<2, 1, 1,", "batch o/down+residual (Q4_0)"),
                 ("matvec_batch_kernel<2, 1, 2,", "batch gate/up+swiglu (Q4_0)"),
                 ("matvec_batch_kernel<14, 1, 0,", "batch output head (Q6_K)"),
+                ("matvec_batch_kernel<2, 2, 3,", "batch qkv+rope (Q4_0, 2 M-tiles)"),
+                ("matvec_batch_kernel<2, 2, 1,", "batch o/down+residual (Q4_0, 2 M-tiles)"),
+                ("matvec_batch_kernel<2, 2, 2,", "batch gate/up+swiglu (Q4_0, 2 M-tiles)"),
+                ("matvec_batch_kernel<14, 2, 0,", "batch output head (Q6_K, 2 M-tiles)"),
                 ("matvec_batch_kernel", "batch gemv (other)"),
                 ("mb_prepare_kernel", "batch x preparation"),
                 ("bat_argmax", "batch argmax"),
