@@ -131,7 +131,9 @@ __device__ __forceinline__ const uint8_t* mb_row(const MbJob& j, int group, int 
     }
 }
 
-// Two 16-bit LDS reads (2-byte aligned) as one word.
+// Two 16-bit LDS reads (2-byte aligned) as one word.  (One 32-bit read at
+// the 2-byte aligned address gives the same word, but unaligned LDS reads
+// are slower: 116 against 111 us over the four batch-32 GEMVs of a layer.)
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t* p) {
     const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
     return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
@@ -150,7 +152,8 @@ __device__ __forceinline__ mb_h8 mb_nibbles(uint32_t w, uint32_t hi2, float bias
     mb_h2 p[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        uint32_t v = ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+        // (w >> 4 i) & 0x000F000F | 0x64006400 in one instruction
+        uint32_t v = __builtin_amdgcn_bitop3_b32(w >> (4 * i), 0x000F000Fu, 0x64006400u, 0xEA);
         v |= ((hi2 >> (2 * i)) & 0x00030003u) << 4;
         p[i] = as_h2(v) + b;  // (1024 + q) + (bias - 1024): exact
     }
