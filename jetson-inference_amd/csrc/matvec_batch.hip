@@ -761,21 +761,24 @@ __global__ __launch_bounds__(64 * WV, 4 * mb_occ<MT>() / WV) void matvec_batch_k
             const mb_f4 v = {val[i], val[i + 1], val[i + 2], val[i + 3]};
             __builtin_amdgcn_raw_buffer_store_b128(v, rs, off0 + 4 * i, 0, kMbSc1);
         }
-        // The partials are stored and loaded device-coherent (sc1), so no
-        // cache maintenance is needed: every thread waits until its partial
-        // stores are complete, the barrier orders that before thread 0's
-        // increment of the counter, and the workgroup that sees the final
-        // count reads the partials (after the next barrier) with loads that
-        // see every completed device-coherent store.  (A release increment,
-        // a write-back of the XCD's L2 in every workgroup, with an acquire in
-        // the last one, cost 13 us over the four batch-32 GEMVs of a layer.)
+        // Every thread waits for its partial stores; the barrier orders them
+        // before thread 0's agent-scope release increment of the counter; the
+        // workgroup that sees the final count acquires (so it synchronizes
+        // with every earlier release) and its threads read the partials after
+        // the next barrier.  Only that one workgroup pays the acquire's L2
+        // invalidation.  The ordering is the memory model's, not a hardware
+        // idiom: it holds whatever the compiler reorders.  (Its cost: a
+        // relaxed increment, relying on the partials' device-coherent
+        // accesses alone, measured 13 us less over the four batch-32 GEMVs of
+        // a layer; acquire-release on every increment 7 us more.)
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         __shared__ int last;
         if (tid == 0) {
-            const uint32_t prev = __hip_atomic_fetch_add(j.counters + group, 1u, __ATOMIC_RELAXED,
+            const uint32_t prev = __hip_atomic_fetch_add(j.counters + group, 1u, __ATOMIC_RELEASE,
                                                          __HIP_MEMORY_SCOPE_AGENT);
             last = prev == (uint32_t)(j.k_splits - 1);
+            if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             if (last)
                 __hip_atomic_store(j.counters + group, 0u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
