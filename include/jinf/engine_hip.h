@@ -150,6 +150,27 @@ int jinf_hip_engine_use_graph(jinf_hip_engine* e, int on);
  * row, the norms): the numerator of the decode bandwidth. */
 uint64_t jinf_hip_engine_step_weight_bytes(const jinf_hip_engine* e);
 
+/* Performance counters, the reference's jinf_perf_stats
+ * (include/jinf/engine.h:14-22) field for field: total_ms is the host wall
+ * time spent in forward / prefill / generate calls (each waits for its
+ * work), tokens_generated the tokens they ran through the model (prompt and
+ * fed-back tokens, as the reference's forward counts them,
+ * src/engine.cpp:756-757).  The streaming and per-phase fields stay zero, as
+ * the reference leaves them on its resident path.  Reset clears them. */
+typedef struct jinf_hip_perf_stats {
+    double total_ms;
+    double nvme_read_ms;
+    double gpu_compute_ms;
+    double attention_ms;
+    double ffn_ms;
+    int tokens_generated;
+    double nvme_bytes_read;
+} jinf_hip_perf_stats;
+
+/* The engine's counters (replaces jinf_engine_get_stats,
+ * include/jinf/engine.h:175-176; NULL for a NULL engine). */
+const jinf_hip_perf_stats* jinf_hip_engine_get_stats(const jinf_hip_engine* e);
+
 /* ---- Batched decode: n_seq (1..64) sequences decoded together on one
  * engine's weights (the engine must outlive the batch).  Each sequence has
  * its own position and its own region of a batched KV cache

@@ -18,6 +18,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <chrono>
 #include <functional>
 #include <new>
 #include <string>
@@ -181,6 +182,7 @@ struct jinf_hip_engine {
     // batched GEMVs do not take
     jinf_hip_batch* pre = nullptr;
     int pre_state = 0;
+    jinf_hip_perf_stats perf{};  // host wall time and tokens of the calls
 };
 
 namespace {
@@ -411,8 +413,23 @@ int zero_state(jinf_hip_engine* e) {
                    "hipMemsetAsync"));
     ENG_TRY(hip_ok(hipStreamSynchronize(e->stream), "hipStreamSynchronize"));
     e->n_past = 0;
+    e->perf = jinf_hip_perf_stats{};
     return JINF_HIP_OK;
 }
+
+// Accumulates a call's host wall time and tokens into the engine's counters
+// when it goes out of scope (src/engine.cpp:756-757 time the forward call).
+struct PerfScope {
+    jinf_hip_engine* e;
+    int tokens = 0;
+    std::chrono::steady_clock::time_point t0 = std::chrono::steady_clock::now();
+    explicit PerfScope(jinf_hip_engine* eng) : e(eng) {}
+    ~PerfScope() {
+        const std::chrono::duration<double, std::milli> dt = std::chrono::steady_clock::now() - t0;
+        e->perf.total_ms += dt.count();
+        e->perf.tokens_generated += tokens;
+    }
+};
 
 int create(jinf_hip_engine** out, const jinf_hip_engine_desc* desc, void* owned) {
     jinf_hip_engine* e = new (std::nothrow) jinf_hip_engine();
@@ -741,10 +758,14 @@ extern "C" int jinf_hip_engine_forward(jinf_hip_engine* e, const int32_t* tokens
                                   e->stream),
                    "hipMemcpyAsync"));
     e->bound = bound_for(e->n_past + n_tokens, d.max_context);
+    PerfScope perf(e);
     int rc = JINF_HIP_OK;
     for (int t = 0; t < n_tokens && rc == JINF_HIP_OK; ++t) {
         rc = step(e);
-        if (rc == JINF_HIP_OK) ++e->n_past;
+        if (rc == JINF_HIP_OK) {
+            ++e->n_past;
+            ++perf.tokens;
+        }
     }
     const int sc = hip_ok(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
     if (rc != JINF_HIP_OK) return rc;
@@ -766,6 +787,7 @@ extern "C" int jinf_hip_engine_prefill(jinf_hip_engine* e, const int32_t* tokens
     if (n_tokens == 1 || !e->pre) return jinf_hip_engine_forward(e, tokens, n_tokens, logits);
     // the batch validates the ids and the context against position n_past
     batch_set_pos(e->pre, e->n_past);
+    PerfScope perf(e);
     const float* lg = nullptr;
     ENG_TRY(jinf_hip_batch_prefill(e->pre, 0, tokens, n_tokens, &lg));
     // the prefill has finished (the call waits): bring the engine's tokens,
@@ -782,6 +804,7 @@ extern "C" int jinf_hip_engine_prefill(jinf_hip_engine* e, const int32_t* tokens
                    batch_argmax(e->pre), p1, d.max_context));
     ENG_TRY(hip_ok(hipStreamSynchronize(e->stream), "hipStreamSynchronize"));
     e->n_past = p1;
+    perf.tokens = n_tokens;
     *logits = e->logits;
     return JINF_HIP_OK;
 }
@@ -799,6 +822,7 @@ extern "C" int jinf_hip_engine_generate(jinf_hip_engine* e, const int32_t* promp
     int32_t* best = e->h_tokens + e->d.max_context + 1;
     int generated = 0;
     e->bound = bound_for(e->n_past + (max_tokens > 0 ? max_tokens : 0), e->d.max_context);
+    PerfScope perf(e);  // the prompt's forward call counts itself
     for (int i = 0; i < max_tokens; ++i) {
         // the argmax of the last step (already the token at position n_past)
         ENG_TRY(hip_ok(hipMemcpyAsync(best, e->state + kBest, 4, hipMemcpyDeviceToHost,
@@ -812,6 +836,7 @@ extern "C" int jinf_hip_engine_generate(jinf_hip_engine* e, const int32_t* promp
         if (e->n_past >= e->d.max_context) break;
         if (step(e) != JINF_HIP_OK) break;
         ++e->n_past;
+        ++perf.tokens;
     }
     *n_generated = generated;
     return hip_ok(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
@@ -823,6 +848,10 @@ extern "C" int jinf_hip_engine_copy_logits(const jinf_hip_engine* e, float* dst,
     ENG_TRY(hip_ok(hipMemcpyAsync(dst, e->logits, (size_t)n * 4, hipMemcpyDefault, e->stream),
                    "hipMemcpyAsync"));
     return hip_ok(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
+}
+
+extern "C" const jinf_hip_perf_stats* jinf_hip_engine_get_stats(const jinf_hip_engine* e) {
+    return e ? &e->perf : nullptr;
 }
 
 extern "C" uint64_t jinf_hip_engine_step_weight_bytes(const jinf_hip_engine* e) {

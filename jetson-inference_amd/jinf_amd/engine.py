@@ -35,6 +35,15 @@ class EngineDesc(ctypes.Structure):
                 ("layers", ctypes.POINTER(LayerWeights))]
 
 
+class PerfStats(ctypes.Structure):
+    """jinf_hip_perf_stats (include/jinf/engine_hip.h), the reference's
+    jinf_perf_stats field for field (include/jinf/engine.h:14-22)."""
+    _fields_ = [("total_ms", ctypes.c_double), ("nvme_read_ms", ctypes.c_double),
+                ("gpu_compute_ms", ctypes.c_double), ("attention_ms", ctypes.c_double),
+                ("ffn_ms", ctypes.c_double), ("tokens_generated", ctypes.c_int),
+                ("nvme_bytes_read", ctypes.c_double)]
+
+
 class EngineError(RuntimeError):
     def __init__(self, what, status):
         super().__init__(f"{what} returned status {status}")
@@ -148,6 +157,12 @@ class Engine:
     @property
     def step_weight_bytes(self):
         return lib().jinf_hip_engine_step_weight_bytes(self._h)
+
+    def stats(self):
+        """The engine's counters (jinf_hip_engine_get_stats) as a dict."""
+        p = lib().jinf_hip_engine_get_stats(self._h)
+        st = PerfStats.from_address(p)
+        return {name: getattr(st, name) for name, _ in PerfStats._fields_}
 
     def forward(self, tokens):
         """Decode `tokens` (ints) one at a time; returns the device address of

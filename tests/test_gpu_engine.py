@@ -236,6 +236,34 @@ def test_step_weight_bytes(dev):
         assert e.step_weight_bytes == want
 
 
+def test_engine_stats(dev):
+    """jinf_hip_engine_get_stats: the reference's jinf_perf_stats
+    (include/jinf/engine.h:14-22) as its forward keeps them (src/engine.cpp:
+    756-757): wall time and tokens run through the model, summed over forward,
+    prefill and generate calls; the streaming fields stay zero; reset clears."""
+    say("engine stats: tokens and wall time per call, cleared by reset")
+    hp, W = mu.tiny_model(seed=18, n_vocab=64, n_layers=1)
+    with make_engine(hp, W, 32, mu.F32) as e:
+        st = e.stats()
+        assert st["tokens_generated"] == 0 and st["total_ms"] == 0.0
+        e.forward([1, 2, 3])
+        st = e.stats()
+        assert st["tokens_generated"] == 3 and st["total_ms"] > 0.0
+        t0, n0 = st["total_ms"], e.n_past
+        e.generate([], 5)                      # every fed-back token counts
+        st = e.stats()
+        assert st["tokens_generated"] == 3 + (e.n_past - n0) and st["total_ms"] > t0
+        n1 = e.n_past
+        e.prefill([4, 5, 6, 7])
+        st = e.stats()
+        assert st["tokens_generated"] == 3 + (n1 - n0) + 4
+        for k in ("nvme_read_ms", "gpu_compute_ms", "attention_ms", "ffn_ms", "nvme_bytes_read"):
+            assert st[k] == 0.0
+        e.reset()
+        st = e.stats()
+        assert st["tokens_generated"] == 0 and st["total_ms"] == 0.0
+
+
 @pytest.mark.parametrize("ggml_order", [False, True], ids=["jinf-order", "ggml-order"])
 def test_gguf_engine_matches_resident_weights(dev, tmp_path, ggml_order):
     say(f"engine from a GGUF file, Q4_0 in {'ggml' if ggml_order else 'jinf'} order")
