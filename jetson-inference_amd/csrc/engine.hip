@@ -24,6 +24,7 @@
 #include <string>
 #include <vector>
 
+#include "jinf/engine_api.h"
 #include "jinf/engine_hip.h"
 #include "jinf_device.h"
 #include "jinf_host.h"
@@ -852,6 +853,63 @@ extern "C" int jinf_hip_engine_copy_logits(const jinf_hip_engine* e, float* dst,
 
 extern "C" const jinf_hip_perf_stats* jinf_hip_engine_get_stats(const jinf_hip_engine* e) {
     return e ? &e->perf : nullptr;
+}
+
+// ---- the reference's engine API by name (include/jinf/engine_api.h) ----
+
+struct jinf_engine {
+    jinf_hip_nvmw* file = nullptr;  // kept until destroy
+    jinf_hip_engine* e = nullptr;
+};
+
+extern "C" int jinf_engine_create(jinf_engine** out, const jinf_engine_config* cfg) {
+    if (!out) return JINF_HIP_ERR_INVALID;
+    *out = nullptr;
+    if (!cfg || !cfg->model_path || cfg->max_context <= 0) return JINF_HIP_ERR_INVALID;
+    if (cfg->predictor_path) {
+        JINF_LOG("engine: a sparse-FFN predictor (%s) is not supported", cfg->predictor_path);
+        return JINF_HIP_ERR_INVALID;
+    }
+    jinf_engine* w = new (std::nothrow) jinf_engine();
+    if (!w) return JINF_HIP_ERR_OOM;
+    int rc = jinf_hip_nvmw_load(&w->file, cfg->model_path);
+    if (rc == JINF_HIP_OK) rc = jinf_hip_engine_create_nvmw(&w->e, w->file, cfg->max_context, JINF_HIP_F32);
+    if (rc != JINF_HIP_OK) {
+        jinf_engine_destroy(w);
+        return rc;
+    }
+    *out = w;
+    return JINF_HIP_OK;
+}
+
+extern "C" void jinf_engine_destroy(jinf_engine* w) {
+    if (!w) return;
+    jinf_hip_engine_destroy(w->e);
+    if (w->file) jinf_hip_nvmw_free(w->file);
+    delete w;
+}
+
+extern "C" int jinf_engine_forward(jinf_engine* w, const int32_t* tokens, int n_tokens,
+                                   float** logits) {
+    if (!w || !logits) return JINF_HIP_ERR_INVALID;
+    const float* lg = nullptr;
+    const int rc = jinf_hip_engine_forward(w->e, tokens, n_tokens, &lg);
+    if (rc == JINF_HIP_OK) *logits = const_cast<float*>(lg);
+    return rc;
+}
+
+extern "C" int jinf_engine_generate(jinf_engine* w, const int32_t* prompt, int n_prompt,
+                                    int32_t* output, int max_tokens, int* n_generated) {
+    if (!w) return JINF_HIP_ERR_INVALID;
+    return jinf_hip_engine_generate(w->e, prompt, n_prompt, output, max_tokens, n_generated);
+}
+
+extern "C" void jinf_engine_reset(jinf_engine* w) {
+    if (w) (void)jinf_hip_engine_reset(w->e);
+}
+
+extern "C" const jinf_perf_stats* jinf_engine_get_stats(const jinf_engine* w) {
+    return w ? jinf_hip_engine_get_stats(w->e) : nullptr;
 }
 
 extern "C" uint64_t jinf_hip_engine_step_weight_bytes(const jinf_hip_engine* e) {

@@ -131,6 +131,13 @@ SIGNATURES = {
     "jinf_hip_engine_use_graph": (_I, [_P, _I]),
     "jinf_hip_engine_step_weight_bytes": (ctypes.c_uint64, [_P]),
     "jinf_hip_engine_get_stats": (_P, [_P]),
+    # the reference's engine API by name (include/jinf/engine_api.h)
+    "jinf_engine_create": (_I, [ctypes.POINTER(_P), _P]),
+    "jinf_engine_destroy": (None, [_P]),
+    "jinf_engine_forward": (_I, [_P, _P, _I, ctypes.POINTER(_P)]),
+    "jinf_engine_generate": (_I, [_P, _P, _I, _P, _I, ctypes.POINTER(_I)]),
+    "jinf_engine_reset": (None, [_P]),
+    "jinf_engine_get_stats": (_P, [_P]),
     # batched decode (include/jinf/engine_hip.h)
     "jinf_hip_batch_create": (_I, [ctypes.POINTER(_P), _P, _I, _I, _I]),
     "jinf_hip_batch_destroy": (None, [_P]),
