@@ -495,11 +495,19 @@ __global__ __launch_bounds__(64 * WV, 4 * mb_occ<MT>() / WV) void matvec_batch_k
         for (int k = 0; k < NWL; ++k) {
             const int ins = wave + WV * k;
             if (ins >= NWI) break;  // wave-uniform
-            const uintptr_t a = (uintptr_t)(wrow[k] + (int64_t)s * SB);
-            const uintptr_t a0 = a & ~(uintptr_t)15;
-            const int last = (int)((a + SB - 1 - a0) >> 4);  // last chunk of this row's slab
-            const int c = wch[k] < last ? wch[k] : last;
-            lds_load16(reinterpret_cast<const void*>(a0 + 16 * (uintptr_t)c), slot + ins * 1024);
+            if constexpr (SB % 16 == 0) {
+                // Q4_0 / Q8_0 / Q4_K: in a 16-byte aligned matrix every slab
+                // starts 16-byte aligned, so the lane's chunk of slab s is its
+                // chunk of slab 0 plus s * SB (one 64-bit add per load; the
+                // general form below costs about nine VALU operations)
+                lds_load16(wrow[k] + 16 * wch[k] + (int64_t)s * SB, slot + ins * 1024);
+            } else {
+                const uintptr_t a = (uintptr_t)(wrow[k] + (int64_t)s * SB);
+                const uintptr_t a0 = a & ~(uintptr_t)15;
+                const int last = (int)((a + SB - 1 - a0) >> 4);  // last chunk of this row's slab
+                const int c = wch[k] < last ? wch[k] : last;
+                lds_load16(reinterpret_cast<const void*>(a0 + 16 * (uintptr_t)c), slot + ins * 1024);
+            }
         }
         if constexpr (NXI > 0) {
             // the whole record (x through LDS), else its x sums
@@ -711,7 +719,12 @@ __global__ __launch_bounds__(64 * WV, 4 * mb_occ<MT>() / WV) void matvec_batch_k
             }
         }
     }
-    __syncthreads();  // the reduction below reuses the slots
+    // The reduction below reuses the slots.  The last step's direct-to-LDS
+    // loads (a re-read of the last slab) may still be landing there, and a
+    // wave's own wait covers only its own loads: every wave waits for its
+    // loads before the barrier, so none lands after another wave's writes.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
+    __syncthreads();
     // the sums are in units of x * s: 1 / s per token (the same in every
     // slab's record) scales them exactly
     {
