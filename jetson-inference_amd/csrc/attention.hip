@@ -410,7 +410,7 @@ __device__ __forceinline__ void am_merge_last(float* __restrict__ out, int64_t l
     }
 }
 
-// grid (n_heads / G, n_chunks, n_seq), 256 threads.  ws == nullptr, or a
+// grid (n_heads / G, n_seq, n_chunks), 256 threads.  ws == nullptr, or a
 // context that fits in one chunk: the workgroup writes the output directly;
 // otherwise each (sequence, head, chunk) writes an unnormalised partial
 // {O[HD], m, l} to ws, and either the last workgroup of the (sequence, head
@@ -442,15 +442,20 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     const int col = lane & 15, lg = lane >> 4;
     const int slot = col & 7;          // head slot of this column
     const bool lo_col = col >= 8;
-    const int s = blockIdx.z;
+    // grid (head groups, sequences, chunks): the chunk index is the slowest
+    // dimension, so every sequence's first chunk (the longest work items)
+    // is dispatched before any second chunk, and the shorter or empty later
+    // chunks fill the tail (64 sequences x 8192 positions: 260 -> 236 us)
+    const int s = blockIdx.y;
+    const int cix = blockIdx.z;
     const int h0 = blockIdx.x * G;
     const int j = h0 / group;
     const int len = lens ? min(max(lens[s], 0), n_past) : n_past;
-    const int c0 = blockIdx.y * chunk;
+    const int c0 = cix * chunk;
     const int c1 = min(c0 + chunk, len);
     // chunks past the context have nothing to do (chunk 0 always runs, so an
     // empty context still writes its zeros)
-    if (blockIdx.y > 0 && c0 >= len) return;
+    if (cix > 0 && c0 >= len) return;
     const int used = (len + chunk - 1) / chunk;  // chunks holding positions
     uint8_t* vst = am_lds + wave * 2 * kAtTile * PITCH;  // V tile, then K tile
     const uint16_t* kb = kc + (int64_t)s * ld_seq + (int64_t)j * HD;
@@ -479,36 +484,44 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     // the next tile's K rows are requested right after the current score
     // product has read the K buffer, its V rows right after the current P V
     // has read the V buffer; the waits below let the other buffer's loads
-    // stay in flight.  Rows past the end re-read the last live row (finite,
-    // masked out).  K slot (row r, p) holds chunk p ^ swizzle(r) so that the
+    // stay in flight.  Rows past the end read as zeros (masked out).  K slot
+    // (row r, p) holds chunk p ^ swizzle(r) so that the
     // 16 rows of a fragment read hit distinct banks; V slot (r, p) holds
     // chunk p ^ 2 ((r >> 2) & 3) for the same reason.
     uint8_t* kst = vst + kAtTile * PITCH;  // this wave's K tile, after its V tile
     auto kswz = [](int r) { return HD == 128 ? (r & 15) : ((r >> 1) & 7); };
     const int i0 = RB ? VLDW * wave : 0;  // first load instruction of the wave's rows
+    // Positions c0 .. c1 - 1 of this (sequence, kv head) as buffer resources
+    // (the host keeps their bytes below 2^31).  A lane's chunk of a tile sits
+    // at the same offset from the tile's first row in every tile, so those
+    // offsets are computed once here and a tile adds only its wave-uniform
+    // start; rows at or past c1 fall outside the resource and read as zeros
+    // (their scores are masked and their probabilities are 0).
+    const uint32_t rowb = (uint32_t)ld_pos * 2;
+    const int nrec = (int)((uint32_t)(c1 - c0) * rowb);
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(kb + (int64_t)c0 * ld_pos), (short)0, nrec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(vb + (int64_t)c0 * ld_pos), (short)0, nrec, 0x00020000);
+    uint32_t koff[VLDW], voff[VLDW];
+#pragma unroll
+    for (int ii = 0; ii < VLDW; ++ii) {
+        const int slot_i = kWave * (i0 + ii) + lane;
+        const int row = slot_i / VCH;
+        koff[ii] = (uint32_t)row * rowb + 16u * (uint32_t)((slot_i % VCH) ^ kswz(row));
+        voff[ii] = (uint32_t)row * rowb + 16u * (uint32_t)((slot_i % VCH) ^ (2 * ((row >> 2) & 3)));
+    }
     auto load_k = [&](int t0) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only: K buffer reads are done
+        const uint32_t so = (uint32_t)(t0 - c0) * rowb;
 #pragma unroll
-        for (int ii = 0; ii < VLDW; ++ii) {
-            const int i = i0 + ii;
-            const int slot_i = kWave * i + lane;
-            const int row = slot_i / VCH;
-            const int c = (slot_i % VCH) ^ kswz(row);
-            const uint16_t* src = kb + (int64_t)min(t0 + row, c1 - 1) * ld_pos + 8 * c;
-            lds_load16(src, kst + 1024 * i);
-        }
+        for (int ii = 0; ii < VLDW; ++ii) lds_load16_buf(krs, koff[ii], so, kst + 1024 * (i0 + ii));
     };
     auto load_v = [&](int t0) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only: V buffer reads are done
+        const uint32_t so = (uint32_t)(t0 - c0) * rowb;
 #pragma unroll
-        for (int ii = 0; ii < VLDW; ++ii) {
-            const int i = i0 + ii;
-            const int slot_i = kWave * i + lane;
-            const int row = slot_i / VCH;
-            const int c = (slot_i % VCH) ^ (2 * ((row >> 2) & 3));
-            const uint16_t* src = vb + (int64_t)min(t0 + row, c1 - 1) * ld_pos + 8 * c;
-            lds_load16(src, vst + 1024 * i);
-        }
+        for (int ii = 0; ii < VLDW; ++ii) lds_load16_buf(vrs, voff[ii], so, vst + 1024 * (i0 + ii));
     };
     // the wave's first tile and step; wrow: the wave's first row in a tile
     const int tstep = RB ? kAtTile : 4 * kAtTile;
@@ -655,7 +668,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
         mg[(wave * 8 + col) * MS + HD + 1] = lsum;
     }
     __syncthreads();
-    const int nch = gridDim.y;
+    const int nch = gridDim.z;
     const bool direct = !ws || used <= 1;  // this workgroup holds the whole context
     for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
         const int g = idx / HD, d = idx % HD;
@@ -675,7 +688,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
         } else {
             // device-coherent stores only for the in-kernel merge; the
             // merge launch reads ordinary stores after the kernel boundary
-            float* rec = ws + (((int64_t)s * n_heads + h0 + g) * nch + blockIdx.y) * MS;
+            float* rec = ws + (((int64_t)s * n_heads + h0 + g) * nch + cix) * MS;
             if constexpr (MERGE) {
                 rec_store(rec + d, num);
                 if (d == 0) {
@@ -827,7 +840,7 @@ static int am_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, c
     const bool rb = chunk <= 2 * kAtTile;
     auto* kern = counters ? (rb ? attn_mfma_kernel<HD, true, true> : attn_mfma_kernel<HD, true, false>)
                           : (rb ? attn_mfma_kernel<HD, false, true> : attn_mfma_kernel<HD, false, false>);
-    const int st = launch(kern, dim3(n_heads / G, nch, n_seq), dim3(256), shmem, stream, out,
+    const int st = launch(kern, dim3(n_heads / G, n_seq, nch), dim3(256), shmem, stream, out,
                           ld_out, q, ld_q, static_cast<const uint16_t*>(k),
                           static_cast<const uint16_t*>(v), ld_pos, ld_seq, lens, n_past, group,
                           G, n_heads, scale, ws, counters, chunk);
@@ -879,9 +892,12 @@ static int attention_decode(float* out, int64_t ld_out, const float* q, int64_t 
     if (!aligned(out, 4) || !aligned(q, 4)) return JINF_HIP_ERR_INVALID;
     const int group = n_heads / n_heads_kv;
     const int64_t es = kv_type == JINF_HIP_F16 ? 2 : 4;
+    // (the matrix-core kernel addresses one (sequence, kv head)'s positions
+    // through 32-bit buffer offsets: their bytes stay below 2^31)
     const bool fast = (head_dim == 64 || head_dim == 128) && aligned(k, 16) && aligned(v, 16) &&
                       aligned(q, 16) && (ld_pos * es) % 16 == 0 && (ld_seq * es) % 16 == 0 &&
-                      ld_q % 4 == 0;
+                      ld_q % 4 == 0 &&
+                      (kv_type != JINF_HIP_F16 || (int64_t)n_past * ld_pos * es <= 0x7FFFFFFF);
     if (!fast) {
         const dim3 grid(n_heads, n_seq);
         if (kv_type == JINF_HIP_F16)

@@ -307,6 +307,26 @@ __device__ __forceinline__ void lds_load16(const void* gptr, const void* lds_bas
         : "memory");
 }
 
+// The same through a buffer resource: lane l's 16 bytes at byte offset
+// voff + soff of the resource land at lds_base + 16 l.  soff is wave-uniform,
+// so a caller that keeps each lane's voff from one tile to the next pays no
+// vector arithmetic per load; bytes at or past the resource's num_records
+// read as zero (no memory access).
+__device__ __forceinline__ void lds_load16_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff,
+                                               const void* lds_base) {
+    const uint32_t off = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_base;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "buffer_load_dwordx4 %1, %2, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(off)),
+          "s"(__builtin_amdgcn_readfirstlane(soff))
+        : "memory");
+}
+
 // s_waitcnt immediate that waits until at most N vector-memory operations
 // are outstanding (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt and
 // lgkmcnt left at their maxima).
