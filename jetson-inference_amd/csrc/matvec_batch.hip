@@ -24,14 +24,16 @@
 // Data movement.  A preparation launch turns x (RMSNorm applied first when
 // the GEMV reads a normed input, exactly as jinf_rmsnorm_rows computes it)
 // into per-slab records of MFMA fragments (below).  A GEMV workgroup (4
-// waves) owns 64 weight rows (two 32-row tiles) and a range of 256-column
-// slabs.  Per slab its lanes copy, with direct-to-LDS loads, the 64 rows'
-// bytes (the aligned 16-byte chunks covering each row's slab: with a 16-byte
-// aligned matrix they start inside it and end before the next 16-byte
-// boundary past its last byte) and the slab's x record into the workgroup's
-// LDS slot; up to three workgroups per CU keep one slab each in flight while
-// the others multiply.  Wave w multiplies k-steps 4 w .. 4 w + 3 of the slab
-// for both row tiles, and the four waves' sums are added in LDS at the end.
+// waves for up to 32 sequences, 8 for two M-tiles) owns 64 weight rows (two
+// 32-row tiles) and a range of 256-column slabs.  Per slab its lanes copy,
+// with direct-to-LDS loads, the 64 rows' bytes (the aligned 16-byte chunks
+// covering each row's slab: with a 16-byte aligned matrix they start inside
+// it and end before the next 16-byte boundary past its last byte) into the
+// workgroup's LDS slot, one slab ahead of the matrix-core work, and each
+// wave loads its own k-steps' x fragments into registers (Q6_K: the x
+// record goes into the slot too).  Wave w multiplies k-steps 4 w .. 4 w + 3
+// (2 w .. 2 w + 1 with 8 waves) of the slab for both row tiles, and the
+// waves' sums are added in LDS at the end.
 // Within a 16-column k-step, lane l supplies token / row l % 32 and columns
 // 8 (l / 32) .. + 7 in the order (0, 4, 1, 5, 2, 6, 3, 7), the order in
 // which four bytes of packed 4-bit codes unpack into fp16 pairs with two
@@ -389,16 +391,19 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
 // one slot, so a slab's loads are issued after the previous slab's product).
 // Workgroup shapes: NT 32-row tiles (ROWS = 32 NT weight rows) and WV waves;
 // the 16 k-steps of a slab are split into KSW parts, wave w taking k-part
-// w / (WV / KSW) of TPW = NT KSW / WV tiles.  The launches use NT 2, WV 4,
-// KSW 4: 64 rows, each wave both tiles over 4 k-steps, one LDS slot, up to
-// three workgroups per CU.  (8-wave shapes over 128 or 256 rows sharing each
-// x record, with two slots so that the next slab's weights are in flight
-// during the matrix-core work, measured slower.)
-// Where the x fragments go: one M-tile (up to 32 sequences) straight into
-// registers, each wave its own k-steps' fragments; two M-tiles, and Q6_K
-// (whose decode needs more registers), through the LDS slot with the weights
-// (the registers would not fit beside the accumulators).
-template <int QT, int MT> constexpr bool mb_xlds() { return MT > 1 || QT == kQ6_K; }
+// w / (WV / KSW) of TPW = NT KSW / WV tiles.  The launches use 64 rows (NT
+// 2): one M-tile with WV 4, KSW 4 (each wave both tiles over 4 k-steps), two
+// M-tiles with WV 8, KSW 8 (each wave both tiles over 2 k-steps, so that two
+// M-tiles of x fragments fit in its registers beside their accumulators:
+// 214 VGPRs, batch-64 step 6.62 -> 6.26 ms against WV 4 with x through LDS;
+// at one M-tile the 8-wave shape measured the same as the 4-wave one).
+// (8-wave shapes over 128 or 256 rows sharing each x record, with two slots
+// so that the next slab's weights are in flight during the matrix-core work,
+// measured slower.)
+// Where the x fragments go: straight into registers, each wave its own
+// k-steps' fragments; for Q6_K (whose decode needs more registers) through
+// the LDS slot with the weights.
+template <int QT, int MT> constexpr bool mb_xlds() { return QT == kQ6_K; }
 // LDS slot: the weight chunks (NWI KiB), then the record's x fragments and
 // sums (x through LDS) or, for Q4_K, only its x sums (NXI KiB), filled by
 // 1 KiB direct-to-LDS instructions dealt round-robin to the waves.
@@ -415,9 +420,11 @@ template <int QT, int MT, int NT> constexpr int mb_slot() {
 template <int QT, int MT> constexpr int mb_nbuf() { return mb_xlds<QT, MT>() ? 1 : 2; }
 template <int QT, int MT> constexpr int mb_xbuf() { return mb_xlds<QT, MT>() ? 1 : 2; }
 constexpr int mb_lcm(int a, int b) { return a % b == 0 ? a : b % a == 0 ? b : a * b; }
-template <int QT, int MT, int NT> constexpr int mb_lds_bytes() {
-    return mb_nbuf<QT, MT>() * mb_slot<QT, MT, NT>() > (8 * MT * 4096) ? mb_nbuf<QT, MT>() * mb_slot<QT, MT, NT>()
-                                                                   : (8 * MT * 4096);
+// LDS of a launch: the slots, reused after the loop for the KSW k-parts'
+// sums (KSW NT MT 1024 floats)
+template <int QT, int MT, int NT, int KSW> constexpr int mb_lds_bytes() {
+    return mb_nbuf<QT, MT>() * mb_slot<QT, MT, NT>() > (KSW * NT * MT * 4096) ? mb_nbuf<QT, MT>() * mb_slot<QT, MT, NT>()
+                                                                         : (KSW * NT * MT * 4096);
 }
 // loads per lane per slab for wave w of WV
 constexpr int mb_share(int n, int w, int wv) { return (n - w + wv - 1) / wv; }
@@ -459,7 +466,7 @@ __global__ __launch_bounds__(64 * WV, 4 * mb_occ<MT>() / WV) void matvec_batch_k
     constexpr int TPW = NT * KSW / WV;        // tiles per wave
     constexpr int KPW = 16 / KSW;             // k-steps per wave
     constexpr int NXL = XL ? 0 : MT * KPW * 2;  // x register loads of one lane per slab
-    static_assert(TPW >= 1 && NT * KSW == TPW * WV && KPW % 4 == 0, "shape");
+    static_assert(TPW >= 1 && NT * KSW == TPW * WV && KPW % 2 == 0, "shape");
     static_assert(XL ? NBUF == 1 && XB == 1 : NBUF >= 2 && XB >= 1 && XB <= NBUF, "pipeline depths");
     static_assert(NBUF < 2 || (NBUF - 2) * (NXL + NWL + (NXI + WV - 1) / WV) < 64, "vmcnt range");
     extern __shared__ __attribute__((aligned(16))) uint8_t mb_lds[];
@@ -941,7 +948,7 @@ template <int QT, int MT, int EPI, int NT, int WV, int KSW>
 int mb_launch_shape(MbJob& j, const MbTheta<EPI>& th, hipStream_t stream) {
     const dim3 grid((unsigned)(j.n_groups * j.k_splits));
     return launch(matvec_batch_kernel<QT, MT, EPI, NT, WV, KSW>, grid, dim3(64 * WV),
-                  mb_lds_bytes<QT, MT, NT>(), stream, j, th);
+                  mb_lds_bytes<QT, MT, NT, KSW>(), stream, j, th);
 }
 
 template <int QT, int MT, int EPI>
@@ -958,8 +965,11 @@ int mb_launch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void*
                    : kg <= 8 ? prep(mb_prepare_kernel<MT, 8>)
                              : prep(mb_prepare_kernel<MT, 16>);
     if (rc != JINF_HIP_OK) return rc;
-    (void)sh;  // kMbNarrow
-    return mb_launch_shape<QT, MT, EPI, 2, 4, 4>(j, th, stream);
+    (void)sh;  // kMbNarrow: 64 rows
+    if constexpr (MT == 1)
+        return mb_launch_shape<QT, MT, EPI, 2, 4, 4>(j, th, stream);
+    else
+        return mb_launch_shape<QT, MT, EPI, 2, 8, 8>(j, th, stream);
 }
 
 // Sequences 32 .. n_batch - 1 of a job as a job of their own.
@@ -984,7 +994,7 @@ template <int QT, int EPI>
 int mb_dispatch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void* norm_w,
                   int norm_f16, float eps, hipStream_t stream) {
     if (j.n_batch <= 32) return mb_launch_t<QT, 1, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
-    constexpr bool fits = mb_lds_bytes<QT, 2, 2>() <= 160 * 1024 - 512;  // static LDS aside
+    constexpr bool fits = mb_lds_bytes<QT, 2, 2, 8>() <= 160 * 1024 - 512;  // static LDS aside
     if (fits) return mb_launch_t<QT, 2, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
     MbJob lo = j;
     lo.n_batch = 32;
