@@ -24,6 +24,7 @@
 #include "engine_internal.h"
 #include "jinf_device.h"
 #include "jinf_host.h"
+#include "matvec_batch_internal.h"
 #include "quant_device.h"
 
 namespace jinf {
@@ -170,6 +171,8 @@ struct jinf_hip_batch {
     int32_t *acts = nullptr, *positions = nullptr, *lens = nullptr, *hist = nullptr;
     void* mws = nullptr;  // batched-GEMV workspace
     size_t mws_bytes = 0;
+    float* dpart = nullptr;  // partial sums of the deferred residual adds
+    size_t dpart_bytes = 0;
     void* aws = nullptr;  // attention workspace
     size_t aws_bytes = 0;
     int32_t* h_io = nullptr;  // pinned: n_seq tokens, 16 words, 3 n_seq prefill row words
@@ -198,8 +201,10 @@ int bat_embed(jinf_hip_batch* b, int rows) {
                              d.n_embd, b->acts, rows, JINF_HIP_F32, b->stream);
 }
 
+// `pend`: the previous layer's deferred down-projection residual add, merged
+// into the residual stream by the first launch's preparation.
 int bat_qkv(jinf_hip_batch* b, const jinf_hip_layer_weights& w, void* kc, void* vc, int rows,
-            int64_t ld_seq) {
+            int64_t ld_seq, MbDefer& pend) {
     const jinf_hip_engine_desc& d = *b->d;
     const void* W[3] = {w.attn_q, w.attn_k, w.attn_v};
     const int T[3] = {w.attn_q_type, w.attn_k_type, w.attn_v_type};
@@ -212,11 +217,12 @@ int bat_qkv(jinf_hip_batch* b, const jinf_hip_layer_weights& w, void* kc, void* 
                 p[k] = W[k];
                 done[k] = true;
             }
-        BAT_TRY(jinf_rmsnorm_qkv_rope_batch(
+        BAT_TRY(rmsnorm_qkv_rope_batch_m(
             p[0], p[1], p[2], T[i], b->hidden, d.n_embd, w.attn_norm, w.attn_norm_type,
             d.rms_norm_eps, d.n_embd, b->q, b->q_dim, kc, vc, b->kv_type, ld_seq, b->positions,
             b->max_ctx, b->head_dim, d.n_heads, d.n_heads_kv, d.rope_freq_base, rows, b->mws,
-            b->mws_bytes, b->stream));
+            b->mws_bytes, &pend, b->stream));
+        pend = MbDefer{};
     }
     return JINF_HIP_OK;
 }
@@ -240,36 +246,42 @@ int bat_enqueue_rows(jinf_hip_batch* b, int rows, int seq, int new_pos) {
                        b->cur, b->pos, b->acts, b->positions, b->lens, b->hist, b->hist_rows, ns,
                        b->max_ctx));
     BAT_TRY(bat_embed(b, ns));
+    // The output and down projections' residual adds are deferred: their
+    // column-split partial sums are merged into the residual stream by the
+    // next GEMV's preparation launch (which normalizes that stream anyway),
+    // so they need no cross-workgroup merge of their own.
+    MbDefer pend;
     for (int L = 0; L < d.n_layers; ++L) {
         const jinf_hip_layer_weights& w = d.layers[L];
         char* kc = b->kv + (size_t)L * b->kv_layer_bytes + kv_off;
         char* vc = b->kv + (size_t)(d.n_layers + L) * b->kv_layer_bytes + kv_off;
-        BAT_TRY(bat_qkv(b, w, kc, vc, ns, ld_seq));
+        BAT_TRY(bat_qkv(b, w, kc, vc, ns, ld_seq, pend));
         BAT_TRY(jinf_attention_decode(b->attn, b->q_dim, b->q, b->q_dim, kc, vc, b->kv_type,
                                       b->kv_dim, ld_seq, b->lens, ns, b->bound, b->head_dim,
                                       d.n_heads, d.n_heads_kv, 0.0f, b->aws, b->aws_bytes, s));
-        BAT_TRY(jinf_matvec_batch_add(w.attn_output, w.attn_output_type, b->attn, b->q_dim,
-                                      b->hidden, n, n, b->q_dim, ns, b->mws, b->mws_bytes, s));
+        BAT_TRY(matvec_batch_add_defer(w.attn_output, w.attn_output_type, b->attn, b->q_dim, n,
+                                       b->q_dim, ns, b->dpart, b->dpart_bytes, b->mws,
+                                       b->mws_bytes, &pend, s));
         if (w.ffn_gate_type == w.ffn_up_type) {
-            BAT_TRY(jinf_rmsnorm_swiglu_matvec_batch(w.ffn_gate, w.ffn_up, w.ffn_gate_type,
-                                                     b->hidden, n, w.ffn_norm, w.ffn_norm_type,
-                                                     eps, b->ff, nff, nff, n, ns, b->mws,
-                                                     b->mws_bytes, s));
+            BAT_TRY(rmsnorm_swiglu_matvec_batch_m(w.ffn_gate, w.ffn_up, w.ffn_gate_type, b->hidden,
+                                                  n, w.ffn_norm, w.ffn_norm_type, eps, b->ff, nff,
+                                                  nff, n, ns, b->mws, b->mws_bytes, &pend, s));
         } else {
-            BAT_TRY(jinf_rmsnorm_matvec_batch(w.ffn_gate, w.ffn_gate_type, b->hidden, n,
-                                              w.ffn_norm, w.ffn_norm_type, eps, b->ff, nff, nff,
-                                              n, ns, b->mws, b->mws_bytes, s));
-            BAT_TRY(jinf_rmsnorm_matvec_batch(w.ffn_up, w.ffn_up_type, b->hidden, n, w.ffn_norm,
-                                              w.ffn_norm_type, eps, b->up, nff, nff, n, ns,
-                                              b->mws, b->mws_bytes, s));
+            BAT_TRY(rmsnorm_matvec_batch_m(w.ffn_gate, w.ffn_gate_type, b->hidden, n, w.ffn_norm,
+                                           w.ffn_norm_type, eps, b->ff, nff, nff, n, ns, b->mws,
+                                           b->mws_bytes, &pend, s));
+            BAT_TRY(rmsnorm_matvec_batch_m(w.ffn_up, w.ffn_up_type, b->hidden, n, w.ffn_norm,
+                                           w.ffn_norm_type, eps, b->up, nff, nff, n, ns, b->mws,
+                                           b->mws_bytes, nullptr, s));
             BAT_TRY(jinf_swiglu_rows(b->ff, nff, b->ff, nff, b->up, nff, ns, nff, JINF_HIP_F32, s));
         }
-        BAT_TRY(jinf_matvec_batch_add(w.ffn_down, w.ffn_down_type, b->ff, nff, b->hidden, n, n,
-                                      nff, ns, b->mws, b->mws_bytes, s));
+        pend = MbDefer{};
+        BAT_TRY(matvec_batch_add_defer(w.ffn_down, w.ffn_down_type, b->ff, nff, n, nff, ns,
+                                       b->dpart, b->dpart_bytes, b->mws, b->mws_bytes, &pend, s));
     }
-    BAT_TRY(jinf_rmsnorm_matvec_batch(d.output, d.output_type, b->hidden, n, d.output_norm,
-                                      d.output_norm_type, eps, b->logits, d.n_vocab, d.n_vocab, n,
-                                      ns, b->mws, b->mws_bytes, s));
+    BAT_TRY(rmsnorm_matvec_batch_m(d.output, d.output_type, b->hidden, n, d.output_norm,
+                                   d.output_norm_type, eps, b->logits, d.n_vocab, d.n_vocab, n, ns,
+                                   b->mws, b->mws_bytes, &pend, s));
     if (prefill) {
         const float* last = b->logits + (int64_t)(ns - 1) * d.n_vocab;
         BAT_TRY(launch(bat_argmax_part_kernel, dim3(b->arg_parts, 1), dim3(kArgThreads), 0, s,
@@ -412,6 +424,10 @@ int bat_create(jinf_hip_batch** out, const jinf_hip_engine* engine, int n_seq, i
         if (w > b->mws_bytes) b->mws_bytes = w;
     }
     b->aws_bytes = jinf_attention_workspace_bytes(n_seq, d.n_heads, b->head_dim, max_context);
+    for (const int cols : {b->q_dim, nff}) {
+        const size_t w = matvec_batch_defer_bytes(n, cols, n_seq);
+        if (w > b->dpart_bytes) b->dpart_bytes = w;
+    }
 
     size_t off = 0;
     auto take_b = [&](size_t bytes) {
@@ -428,6 +444,7 @@ int bat_create(jinf_hip_batch** out, const jinf_hip_engine* engine, int n_seq, i
     const size_t o_pos = take_b(ns * 4), o_acts = take_b(ns * 4), o_positions = take_b(ns * 4);
     const size_t o_lens = take_b(ns * 4), o_hist = take_b((size_t)b->hist_rows * ns * 4);
     const size_t o_mws = take_b(b->mws_bytes), o_aws = take_b(b->aws_bytes);
+    const size_t o_dpart = take_b(b->dpart_bytes);
 
     int rc = hip_rc(hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking), "hipStreamCreate");
     if (rc == JINF_HIP_OK) rc = hip_rc(hipMalloc((void**)&b->act, off), "hipMalloc");
@@ -462,6 +479,7 @@ int bat_create(jinf_hip_batch** out, const jinf_hip_engine* engine, int n_seq, i
     b->lens = i32(o_lens);
     b->hist = i32(o_hist);
     b->mws = b->act + o_mws;
+    b->dpart = f(o_dpart);
     b->aws = b->aws_bytes ? b->act + o_aws : nullptr;
     // zero everything (the workspaces' counters must start at zero)
     rc = hip_rc(hipMemsetAsync(b->act, 0, off, b->stream), "hipMemsetAsync");

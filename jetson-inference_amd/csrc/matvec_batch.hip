@@ -57,6 +57,7 @@
 #include "jinf_device.h"
 #include "jinf_host.h"
 #include "jinf/kernels_ext.h"
+#include "matvec_batch_internal.h"
 #include "quant_device.h"
 #include "rope_device.h"
 
@@ -106,6 +107,8 @@ struct MbJob {
     int64_t ld_seq;
     float* part;           // split partials [n_groups][k_splits][2 * MT * 1024]
     uint32_t* counters;    // [n_groups]
+    float* dpart;          // kMbEpiAdd, deferred: partial sums [k_splits][n_batch][rows]
+    int64_t dstride;       // (split stride), merged by the next preparation
 };
 
 struct MbNoTheta {};
@@ -241,19 +244,28 @@ __device__ __forceinline__ void mb_norm8(const void* norm_w, int norm_f16, int g
 // 4096 columns, 7 of 8 at 14336).  Every x and norm-weight load is issued
 // before any arithmetic (weights held in registers for KG <= 8), and the two
 // row reductions are DPP wave reductions with one LDS exchange.
-template <int MT, int KG>
-__global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict__ x, int ld_x,
+// MERGE: x is the residual stream that a deferred GEMV (below) added into:
+// its k_splits partial sums dpart[split][token][cols] are summed in split
+// order and added, x + (p_0 + p_1 + ...) (the order of the GEMV's own
+// merge), the new row is written back into x, and the record is made from
+// it.  The grid is then (1, tokens): one workgroup holds and converts the
+// token's whole row, and each thread writes back only the groups it read,
+// so the in-place update has no reader in another workgroup.
+template <int MT, int KG, bool MERGE>
+__global__ __launch_bounds__(256) void mb_prepare_kernel(float* __restrict__ x, int ld_x,
                                                           int n_batch, int cols,
                                                           const void* __restrict__ norm_w,
                                                           int norm_f16, float eps,
-                                                          uint8_t* __restrict__ rec) {
+                                                          uint8_t* __restrict__ rec,
+                                                          const float* __restrict__ dpart,
+                                                          int k_splits, int64_t split_stride) {
     __shared__ double red[4];
     __shared__ float redf[4];
     const int b = blockIdx.y;
     const int tid = threadIdx.x;
     const int ng = cols / 8;  // a multiple of 32
     const bool live = b < n_batch;
-    const float* xr = x + (int64_t)(live ? b : 0) * ld_x;
+    float* xr = x + (int64_t)(live ? b : 0) * ld_x;
     constexpr bool GW_EARLY = KG <= 8;
     float v[KG][8];
     float gwr[GW_EARLY ? KG : 1][8];
@@ -268,6 +280,29 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[k][e] = 0.0f;
+        }
+    }
+    if constexpr (MERGE) {
+        const float* pr = dpart + (int64_t)(live ? b : 0) * cols;
+#pragma unroll
+        for (int k = 0; k < KG; ++k) {
+            const int g = tid + 256 * k;
+            if (live && g < ng) {
+                float sum[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sum[e] = 0.0f;
+                for (int sp = 0; sp < k_splits; ++sp) {
+                    const float* pp = pr + sp * split_stride + 8 * g;
+                    const float4 p = *reinterpret_cast<const float4*>(pp);
+                    const float4 q = *reinterpret_cast<const float4*>(pp + 4);
+                    sum[0] += p.x; sum[1] += p.y; sum[2] += p.z; sum[3] += p.w;
+                    sum[4] += q.x; sum[5] += q.y; sum[6] += q.z; sum[7] += q.w;
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[k][e] = v[k][e] + sum[e];
+                *reinterpret_cast<float4*>(xr + 8 * g) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
+                *reinterpret_cast<float4*>(xr + 8 * g + 4) = make_float4(v[k][4], v[k][5], v[k][6], v[k][7]);
+            }
         }
     }
     if constexpr (GW_EARLY) {
@@ -329,7 +364,7 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
 #pragma unroll
         for (int k = 0; k < KG; ++k) {
             const int g = tid + 256 * k;
-            if (g < ng && k == (int)blockIdx.x) {  // only this workgroup's groups
+            if (g < ng && (MERGE || k == (int)blockIdx.x)) {  // only this workgroup's groups
 #pragma clang fp contract(off)
                 float gw[8];
                 gweights(k, g, gw);
@@ -347,8 +382,9 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
 #pragma unroll
     for (int k = 0; k < KG; ++k) {
         const int g = tid + 256 * k;
-        // this workgroup's 256 groups (uniform over aligned groups of 32 threads)
-        const bool here = g < ng && k == (int)blockIdx.x;
+        // this workgroup's 256 groups (uniform over aligned groups of 32 threads);
+        // every group with MERGE
+        const bool here = g < ng && (MERGE || k == (int)blockIdx.x);
         const int slab = g >> 5, gi = g & 31, t = gi >> 1, h = gi & 1;
         uint8_t* r = rec + (int64_t)slab * mb_rec(MT);
         float sum = 0.0f;
@@ -768,6 +804,27 @@ __global__ __launch_bounds__(64 * WV, 4 * mb_occ<MT>() / WV) void matvec_batch_k
         for (int kp = 1; kp < KSW; ++kp) v += red[kp * NV + idx];
         val[i] = v;
     }
+    auto token_of = [](int idx) {
+        const int mt = (idx >> 10) % MT, r = (idx >> 6) & 15, ln = idx & 63;
+        return mb_token(mt, r, ln >> 5);
+    };
+    auto local_of = [](int idx) { return (idx / (MT * 1024)) * 32 + (idx & 31); };
+    if constexpr (EPI == kMbEpiAdd) {
+        if (j.dpart) {
+            // deferred residual add: this split's sums go to its own partial
+            // array, which the next preparation launch merges and adds (no
+            // counter, no cross-workgroup merge here)
+            float* dp = j.dpart + split * j.dstride;
+#pragma unroll
+            for (int i = 0; i < PV; ++i) {
+                const int idx = tid + THREADS * i;
+                const int b = token_of(idx);
+                const int row = group * ROWS + local_of(idx);
+                if (b < j.n_batch && row < j.rows) dp[(int64_t)b * j.rows + row] = val[i];
+            }
+            return;
+        }
+    }
     if (j.k_splits > 1) {
         // partials in thread-contiguous order ([group][split][thread][PV]),
         // 16-byte device-coherent (sc1) stores and loads, all loads of the
@@ -826,11 +883,6 @@ __global__ __launch_bounds__(64 * WV, 4 * mb_occ<MT>() / WV) void matvec_batch_k
 
     // ---- epilogue ----
     __syncthreads();  // the reduction area is free again
-    auto token_of = [](int idx) {
-        const int mt = (idx >> 10) % MT, r = (idx >> 6) & 15, ln = idx & 63;
-        return mb_token(mt, r, ln >> 5);
-    };
-    auto local_of = [](int idx) { return (idx / (MT * 1024)) * 32 + (idx & 31); };
 
     if constexpr (EPI == kMbEpiStore || EPI == kMbEpiAdd) {
 #pragma unroll
@@ -953,17 +1005,24 @@ int mb_launch_shape(MbJob& j, const MbTheta<EPI>& th, hipStream_t stream) {
 
 template <int QT, int MT, int EPI>
 int mb_launch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void* norm_w,
-                int norm_f16, float eps, hipStream_t stream) {
+                int norm_f16, float eps, const MbDefer* pend, hipStream_t stream) {
     const int kg = (j.n_slabs + 7) / 8;  // 8-column groups per thread
-    auto prep = [&](auto kern) {
-        return launch(kern, dim3((unsigned)kg, 32 * MT), dim3(256), 0, stream, j.x, j.ld_x,
+    float* x = const_cast<float*>(j.x);  // written only when merging `pend`
+    auto prep = [&](auto kern, auto kmerge) {
+        if (pend && pend->part)
+            return launch(kmerge, dim3(1u, 32 * MT), dim3(256), 0, stream, x, j.ld_x, j.n_batch,
+                          j.n_slabs * kMbCols, norm_w, norm_f16, eps,
+                          const_cast<uint8_t*>(j.xrec), pend->part, pend->k, pend->stride);
+        return launch(kern, dim3((unsigned)kg, 32 * MT), dim3(256), 0, stream, x, j.ld_x,
                       j.n_batch, j.n_slabs * kMbCols, norm_w, norm_f16, eps,
-                      const_cast<uint8_t*>(j.xrec));
+                      const_cast<uint8_t*>(j.xrec), static_cast<const float*>(nullptr), 0,
+                      (int64_t)0);
     };
-    const int rc = kg <= 2 ? prep(mb_prepare_kernel<MT, 2>)
-                   : kg <= 4 ? prep(mb_prepare_kernel<MT, 4>)
-                   : kg <= 8 ? prep(mb_prepare_kernel<MT, 8>)
-                             : prep(mb_prepare_kernel<MT, 16>);
+    const int rc =
+        kg <= 2   ? prep(mb_prepare_kernel<MT, 2, false>, mb_prepare_kernel<MT, 2, true>)
+        : kg <= 4 ? prep(mb_prepare_kernel<MT, 4, false>, mb_prepare_kernel<MT, 4, true>)
+        : kg <= 8 ? prep(mb_prepare_kernel<MT, 8, false>, mb_prepare_kernel<MT, 8, true>)
+                  : prep(mb_prepare_kernel<MT, 16, false>, mb_prepare_kernel<MT, 16, true>);
     if (rc != JINF_HIP_OK) return rc;
     (void)sh;  // kMbNarrow: 64 rows
     if constexpr (MT == 1)
@@ -979,6 +1038,7 @@ MbJob mb_upper(const MbJob& j) {
     u.n_batch = j.n_batch - 32;
     u.x = j.x + (int64_t)32 * j.ld_x;
     u.y = j.y + (int64_t)32 * j.ld_y;
+    if (u.dpart) u.dpart += (int64_t)32 * j.rows;
     if constexpr (EPI == kMbEpiQKV) {
         u.pos = j.pos + 32;
         const int64_t es = j.kv_f16 ? 2 : 4;
@@ -992,26 +1052,34 @@ MbJob mb_upper(const MbJob& j) {
 // holds a slot of that size, else two launches of at most 32.
 template <int QT, int EPI>
 int mb_dispatch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void* norm_w,
-                  int norm_f16, float eps, hipStream_t stream) {
-    if (j.n_batch <= 32) return mb_launch_t<QT, 1, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
+                  int norm_f16, float eps, const MbDefer* pend, hipStream_t stream) {
+    if (j.n_batch <= 32)
+        return mb_launch_t<QT, 1, EPI>(j, sh, th, norm_w, norm_f16, eps, pend, stream);
     constexpr bool fits = mb_lds_bytes<QT, 2, 2, 8>() <= 160 * 1024 - 512;  // static LDS aside
-    if (fits) return mb_launch_t<QT, 2, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
+    if (fits) return mb_launch_t<QT, 2, EPI>(j, sh, th, norm_w, norm_f16, eps, pend, stream);
     MbJob lo = j;
     lo.n_batch = 32;
-    const int rc = mb_launch_t<QT, 1, EPI>(lo, sh, th, norm_w, norm_f16, eps, stream);
+    const int rc = mb_launch_t<QT, 1, EPI>(lo, sh, th, norm_w, norm_f16, eps, pend, stream);
     if (rc != JINF_HIP_OK) return rc;
     MbJob hi = mb_upper<EPI>(j);
-    return mb_launch_t<QT, 1, EPI>(hi, sh, th, norm_w, norm_f16, eps, stream);
+    MbDefer ph;
+    if (pend) {
+        ph = *pend;
+        if (ph.part) ph.part += (int64_t)32 * j.n_slabs * kMbCols;
+    }
+    return mb_launch_t<QT, 1, EPI>(hi, sh, th, norm_w, norm_f16, eps, pend ? &ph : nullptr,
+                                   stream);
 }
 
 template <int EPI>
 int mb_dispatch(int qtype, MbJob& j, const MbShape& sh, const MbTheta<EPI>& th,
-                const void* norm_w, int norm_f16, float eps, hipStream_t stream) {
+                const void* norm_w, int norm_f16, float eps, const MbDefer* pend,
+                hipStream_t stream) {
     switch (qtype) {
-        case kQ4_0: return mb_dispatch_t<kQ4_0, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
-        case kQ8_0: return mb_dispatch_t<kQ8_0, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
-        case kQ4_K: return mb_dispatch_t<kQ4_K, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
-        case kQ6_K: return mb_dispatch_t<kQ6_K, EPI>(j, sh, th, norm_w, norm_f16, eps, stream);
+        case kQ4_0: return mb_dispatch_t<kQ4_0, EPI>(j, sh, th, norm_w, norm_f16, eps, pend, stream);
+        case kQ8_0: return mb_dispatch_t<kQ8_0, EPI>(j, sh, th, norm_w, norm_f16, eps, pend, stream);
+        case kQ4_K: return mb_dispatch_t<kQ4_K, EPI>(j, sh, th, norm_w, norm_f16, eps, pend, stream);
+        case kQ6_K: return mb_dispatch_t<kQ6_K, EPI>(j, sh, th, norm_w, norm_f16, eps, pend, stream);
         default: return JINF_HIP_ERR_INVALID;
     }
 }
@@ -1112,7 +1180,7 @@ extern "C" int jinf_matvec_batch(const void* weight, int qtype, const float* x, 
     if (ld_y < rows) return JINF_HIP_ERR_INVALID;
     j.W[0] = j.W[1] = j.W[2] = static_cast<const uint8_t*>(weight);
     j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = rows;
-    return mb_dispatch<kMbEpiStore>(qtype, j, sh, MbNoTheta{}, nullptr, 0, 0.0f, stream);
+    return mb_dispatch<kMbEpiStore>(qtype, j, sh, MbNoTheta{}, nullptr, 0, 0.0f, nullptr, stream);
 }
 
 extern "C" int jinf_matvec_batch_add(const void* weight, int qtype, const float* x, int ld_x,
@@ -1127,14 +1195,15 @@ extern "C" int jinf_matvec_batch_add(const void* weight, int qtype, const float*
     if (ld_y < rows) return JINF_HIP_ERR_INVALID;
     j.W[0] = j.W[1] = j.W[2] = static_cast<const uint8_t*>(weight);
     j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = rows;
-    return mb_dispatch<kMbEpiAdd>(qtype, j, sh, MbNoTheta{}, nullptr, 0, 0.0f, stream);
+    return mb_dispatch<kMbEpiAdd>(qtype, j, sh, MbNoTheta{}, nullptr, 0, 0.0f, nullptr, stream);
 }
 
-extern "C" int jinf_rmsnorm_matvec_batch(const void* weight, int qtype, const float* h, int ld_h,
-                                         const void* norm_w, int norm_type, float eps, float* y,
-                                         int ld_y, int rows, int cols, int n_batch,
-                                         void* workspace, size_t workspace_bytes,
-                                         hipStream_t stream) {
+namespace jinf {
+
+int rmsnorm_matvec_batch_m(const void* weight, int qtype, float* h, int ld_h, const void* norm_w,
+                           int norm_type, float eps, float* y, int ld_y, int rows, int cols,
+                           int n_batch, void* workspace, size_t workspace_bytes,
+                           const MbDefer* pend, hipStream_t stream) {
     MbJob j{};
     MbShape sh;
     int f16 = 0;
@@ -1146,14 +1215,13 @@ extern "C" int jinf_rmsnorm_matvec_batch(const void* weight, int qtype, const fl
     if (ld_y < rows) return JINF_HIP_ERR_INVALID;
     j.W[0] = j.W[1] = j.W[2] = static_cast<const uint8_t*>(weight);
     j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = rows;
-    return mb_dispatch<kMbEpiStore>(qtype, j, sh, MbNoTheta{}, norm_w, f16, eps, stream);
+    return mb_dispatch<kMbEpiStore>(qtype, j, sh, MbNoTheta{}, norm_w, f16, eps, pend, stream);
 }
 
-extern "C" int jinf_rmsnorm_swiglu_matvec_batch(const void* w_gate, const void* w_up, int qtype,
-                                                const float* h, int ld_h, const void* norm_w,
-                                                int norm_type, float eps, float* y, int ld_y,
-                                                int n_ff, int cols, int n_batch, void* workspace,
-                                                size_t workspace_bytes, hipStream_t stream) {
+int rmsnorm_swiglu_matvec_batch_m(const void* w_gate, const void* w_up, int qtype, float* h,
+                                  int ld_h, const void* norm_w, int norm_type, float eps, float* y,
+                                  int ld_y, int n_ff, int cols, int n_batch, void* workspace,
+                                  size_t workspace_bytes, const MbDefer* pend, hipStream_t stream) {
     MbJob j{};
     MbShape sh;
     int f16 = 0;
@@ -1167,18 +1235,16 @@ extern "C" int jinf_rmsnorm_swiglu_matvec_batch(const void* w_gate, const void* 
     j.W[1] = static_cast<const uint8_t*>(w_up);
     j.W[2] = j.W[0];
     j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = n_ff;
-    return mb_dispatch<kMbEpiSwiGLU>(qtype, j, sh, MbNoTheta{}, norm_w, f16, eps, stream);
+    return mb_dispatch<kMbEpiSwiGLU>(qtype, j, sh, MbNoTheta{}, norm_w, f16, eps, pend, stream);
 }
 
-extern "C" int jinf_rmsnorm_qkv_rope_batch(const void* wq, const void* wk, const void* wv,
-                                           int qtype, const float* h, int ld_h,
-                                           const void* norm_w, int norm_type, float eps,
-                                           int n_embd, float* q, int ld_q, void* k_cache,
-                                           void* v_cache, int kv_type, int64_t ld_seq,
-                                           const int32_t* positions, int max_ctx, int head_dim,
-                                           int n_heads, int n_heads_kv, float freq_base,
-                                           int n_batch, void* workspace, size_t workspace_bytes,
-                                           hipStream_t stream) {
+int rmsnorm_qkv_rope_batch_m(const void* wq, const void* wk, const void* wv, int qtype, float* h,
+                             int ld_h, const void* norm_w, int norm_type, float eps, int n_embd,
+                             float* q, int ld_q, void* k_cache, void* v_cache, int kv_type,
+                             int64_t ld_seq, const int32_t* positions, int max_ctx, int head_dim,
+                             int n_heads, int n_heads_kv, float freq_base, int n_batch,
+                             void* workspace, size_t workspace_bytes, const MbDefer* pend,
+                             hipStream_t stream) {
     if (head_dim <= 0 || head_dim % 2 != 0 || head_dim / 2 > kRopeMaxHalf || n_heads < 0 ||
         n_heads_kv < 0 || !(freq_base > 0.0f) || !positions)
         return JINF_HIP_ERR_INVALID;
@@ -1197,7 +1263,7 @@ extern "C" int jinf_rmsnorm_qkv_rope_batch(const void* wq, const void* wk, const
     MbJob j{};
     MbShape sh;
     int f16 = 0;
-    float* yq = q ? q : const_cast<float*>(h);
+    float* yq = q ? q : h;
     int rc = mb_prepare(j, sh, qtype, kMbEpiQKV, rows, n_embd, n_batch, h, ld_h, yq,
                         wq ? ld_q : 1, workspace, workspace_bytes);
     if (rc == JINF_HIP_OK) rc = mb_norm_type(norm_w, norm_type, eps, &f16);
@@ -1222,5 +1288,74 @@ extern "C" int jinf_rmsnorm_qkv_rope_batch(const void* wq, const void* wk, const
     j.ld_seq = ld_seq;
     RopeTheta th;
     theta_table(th, head_dim, freq_base);
-    return mb_dispatch<kMbEpiQKV>(qtype, j, sh, th, norm_w, f16, eps, stream);
+    return mb_dispatch<kMbEpiQKV>(qtype, j, sh, th, norm_w, f16, eps, pend, stream);
+}
+
+size_t matvec_batch_defer_bytes(int rows, int cols, int n_batch) {
+    if (rows <= 0 || cols <= 0 || cols % kMbCols != 0 || cols > kMbMaxCols || n_batch <= 0 ||
+        n_batch > kMbMaxBatch)
+        return 0;
+    const MbShape sh = mb_shape();
+    const int groups = (rows + sh.rows_per_group(kMbEpiAdd) - 1) / sh.rows_per_group(kMbEpiAdd);
+    int per;
+    const int k = mb_split(groups, cols / kMbCols, &per);
+    return (size_t)k * n_batch * rows * sizeof(float);
+}
+
+int matvec_batch_add_defer(const void* weight, int qtype, const float* x, int ld_x, int rows,
+                           int cols, int n_batch, float* part, size_t part_bytes, void* workspace,
+                           size_t workspace_bytes, MbDefer* out, hipStream_t stream) {
+    MbJob j{};
+    MbShape sh;
+    if (!w_ok(weight) || !out || !part || !aligned(part, 16)) return JINF_HIP_ERR_INVALID;
+    const int rc = mb_prepare(j, sh, qtype, kMbEpiAdd, rows, cols, n_batch, x, ld_x, part, rows,
+                              workspace, workspace_bytes);
+    if (rc != JINF_HIP_OK) return rc;
+    if (part_bytes < matvec_batch_defer_bytes(rows, cols, n_batch)) return JINF_HIP_ERR_INVALID;
+    j.W[0] = j.W[1] = j.W[2] = static_cast<const uint8_t*>(weight);
+    j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = rows;
+    j.dpart = part;
+    j.dstride = (int64_t)n_batch * rows;
+    out->part = part;
+    out->k = j.k_splits;
+    out->stride = j.dstride;
+    return mb_dispatch<kMbEpiAdd>(qtype, j, sh, MbNoTheta{}, nullptr, 0, 0.0f, nullptr, stream);
+}
+
+}  // namespace jinf
+
+extern "C" int jinf_rmsnorm_matvec_batch(const void* weight, int qtype, const float* h, int ld_h,
+                                         const void* norm_w, int norm_type, float eps, float* y,
+                                         int ld_y, int rows, int cols, int n_batch,
+                                         void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream) {
+    return rmsnorm_matvec_batch_m(weight, qtype, const_cast<float*>(h), ld_h, norm_w, norm_type,
+                                  eps, y, ld_y, rows, cols, n_batch, workspace, workspace_bytes,
+                                  nullptr, stream);
+}
+
+extern "C" int jinf_rmsnorm_swiglu_matvec_batch(const void* w_gate, const void* w_up, int qtype,
+                                                const float* h, int ld_h, const void* norm_w,
+                                                int norm_type, float eps, float* y, int ld_y,
+                                                int n_ff, int cols, int n_batch, void* workspace,
+                                                size_t workspace_bytes, hipStream_t stream) {
+    return rmsnorm_swiglu_matvec_batch_m(w_gate, w_up, qtype, const_cast<float*>(h), ld_h, norm_w,
+                                         norm_type, eps, y, ld_y, n_ff, cols, n_batch, workspace,
+                                         workspace_bytes, nullptr, stream);
+}
+
+extern "C" int jinf_rmsnorm_qkv_rope_batch(const void* wq, const void* wk, const void* wv,
+                                           int qtype, const float* h, int ld_h,
+                                           const void* norm_w, int norm_type, float eps,
+                                           int n_embd, float* q, int ld_q, void* k_cache,
+                                           void* v_cache, int kv_type, int64_t ld_seq,
+                                           const int32_t* positions, int max_ctx, int head_dim,
+                                           int n_heads, int n_heads_kv, float freq_base,
+                                           int n_batch, void* workspace, size_t workspace_bytes,
+                                           hipStream_t stream) {
+    return rmsnorm_qkv_rope_batch_m(wq, wk, wv, qtype, const_cast<float*>(h), ld_h, norm_w,
+                                    norm_type, eps, n_embd, q, ld_q, k_cache, v_cache, kv_type,
+                                    ld_seq, positions, max_ctx, head_dim, n_heads, n_heads_kv,
+                                    freq_base, n_batch, workspace, workspace_bytes, nullptr,
+                                    stream);
 }
