@@ -247,9 +247,10 @@ int bat_enqueue_rows(jinf_hip_batch* b, int rows, int seq, int new_pos) {
                        b->max_ctx));
     BAT_TRY(bat_embed(b, ns));
     // The output and down projections' residual adds are deferred: their
-    // column-split partial sums are merged into the residual stream by the
-    // next GEMV's preparation launch (which normalizes that stream anyway),
-    // so they need no cross-workgroup merge of their own.
+    // column-split partial sums are added into the residual stream by a merge
+    // launch ahead of the next GEMV's preparation, so the GEMVs need no
+    // cross-workgroup merge (a counter with release / acquire ordering and a
+    // merging workgroup per row group) of their own.
     MbDefer pend;
     for (int L = 0; L < d.n_layers; ++L) {
         const jinf_hip_layer_weights& w = d.layers[L];

@@ -244,28 +244,19 @@ __device__ __forceinline__ void mb_norm8(const void* norm_w, int norm_f16, int g
 // 4096 columns, 7 of 8 at 14336).  Every x and norm-weight load is issued
 // before any arithmetic (weights held in registers for KG <= 8), and the two
 // row reductions are DPP wave reductions with one LDS exchange.
-// MERGE: x is the residual stream that a deferred GEMV (below) added into:
-// its k_splits partial sums dpart[split][token][cols] are summed in split
-// order and added, x + (p_0 + p_1 + ...) (the order of the GEMV's own
-// merge), the new row is written back into x, and the record is made from
-// it.  The grid is then (1, tokens): one workgroup holds and converts the
-// token's whole row, and each thread writes back only the groups it read,
-// so the in-place update has no reader in another workgroup.
-template <int MT, int KG, bool MERGE>
-__global__ __launch_bounds__(256) void mb_prepare_kernel(float* __restrict__ x, int ld_x,
+template <int MT, int KG>
+__global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict__ x, int ld_x,
                                                           int n_batch, int cols,
                                                           const void* __restrict__ norm_w,
                                                           int norm_f16, float eps,
-                                                          uint8_t* __restrict__ rec,
-                                                          const float* __restrict__ dpart,
-                                                          int k_splits, int64_t split_stride) {
+                                                          uint8_t* __restrict__ rec) {
     __shared__ double red[4];
     __shared__ float redf[4];
     const int b = blockIdx.y;
     const int tid = threadIdx.x;
     const int ng = cols / 8;  // a multiple of 32
     const bool live = b < n_batch;
-    float* xr = x + (int64_t)(live ? b : 0) * ld_x;
+    const float* xr = x + (int64_t)(live ? b : 0) * ld_x;
     constexpr bool GW_EARLY = KG <= 8;
     float v[KG][8];
     float gwr[GW_EARLY ? KG : 1][8];
@@ -280,29 +271,6 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(float* __restrict__ x, 
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[k][e] = 0.0f;
-        }
-    }
-    if constexpr (MERGE) {
-        const float* pr = dpart + (int64_t)(live ? b : 0) * cols;
-#pragma unroll
-        for (int k = 0; k < KG; ++k) {
-            const int g = tid + 256 * k;
-            if (live && g < ng) {
-                float sum[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) sum[e] = 0.0f;
-                for (int sp = 0; sp < k_splits; ++sp) {
-                    const float* pp = pr + sp * split_stride + 8 * g;
-                    const float4 p = *reinterpret_cast<const float4*>(pp);
-                    const float4 q = *reinterpret_cast<const float4*>(pp + 4);
-                    sum[0] += p.x; sum[1] += p.y; sum[2] += p.z; sum[3] += p.w;
-                    sum[4] += q.x; sum[5] += q.y; sum[6] += q.z; sum[7] += q.w;
-                }
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[k][e] = v[k][e] + sum[e];
-                *reinterpret_cast<float4*>(xr + 8 * g) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
-                *reinterpret_cast<float4*>(xr + 8 * g + 4) = make_float4(v[k][4], v[k][5], v[k][6], v[k][7]);
-            }
         }
     }
     if constexpr (GW_EARLY) {
@@ -364,7 +332,7 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(float* __restrict__ x, 
 #pragma unroll
         for (int k = 0; k < KG; ++k) {
             const int g = tid + 256 * k;
-            if (g < ng && (MERGE || k == (int)blockIdx.x)) {  // only this workgroup's groups
+            if (g < ng && k == (int)blockIdx.x) {  // only this workgroup's groups
 #pragma clang fp contract(off)
                 float gw[8];
                 gweights(k, g, gw);
@@ -382,9 +350,8 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(float* __restrict__ x, 
 #pragma unroll
     for (int k = 0; k < KG; ++k) {
         const int g = tid + 256 * k;
-        // this workgroup's 256 groups (uniform over aligned groups of 32 threads);
-        // every group with MERGE
-        const bool here = g < ng && (MERGE || k == (int)blockIdx.x);
+        // this workgroup's 256 groups (uniform over aligned groups of 32 threads)
+        const bool here = g < ng && k == (int)blockIdx.x;
         const int slab = g >> 5, gi = g & 31, t = gi >> 1, h = gi & 1;
         uint8_t* r = rec + (int64_t)slab * mb_rec(MT);
         float sum = 0.0f;
@@ -416,6 +383,46 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(float* __restrict__ x, 
             if (gi == 0) meta[b] = ldexpf(1.0f, ex - 15);
         }
     }
+}
+
+// ---- merge of a deferred residual add ----
+//
+// h[b][c] += p_0[b][c] + p_1[b][c] + ... (split order, the order of the
+// GEMV's own merge) for the k partial arrays p_s = part + s * stride of a
+// deferred residual add ([n_batch][cols], cols a multiple of 4).  One lane
+// per 4 columns of one sequence, every partial's load issued before the
+// sums; a launch of its own over many workgroups (folding it into the
+// preparation, one workgroup per sequence so that the in-place update had
+// no reader elsewhere, took 10.5 us per launch: one CU's outstanding loads
+// bound the partials' read).
+__global__ __launch_bounds__(256) void mb_merge_kernel(float* __restrict__ h, int ld_h,
+                                                       int n_batch, int cols,
+                                                       const float* __restrict__ part, int k,
+                                                       int64_t stride) {
+    constexpr int SB = 8;  // partials loaded together
+    const int c4 = cols / 4;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)n_batch * c4) return;
+    const int b = (int)(i / c4), c = 4 * (int)(i % c4);
+    float* hp = h + (int64_t)b * ld_h + c;
+    const float* pp = part + (int64_t)b * cols + c;
+    const float4 x = *reinterpret_cast<const float4*>(hp);
+    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s0 = 0; s0 < k; s0 += SB) {
+        float4 p[SB];
+#pragma unroll
+        for (int u = 0; u < SB; ++u)
+            if (s0 + u < k) p[u] = *reinterpret_cast<const float4*>(pp + (s0 + u) * stride);
+#pragma unroll
+        for (int u = 0; u < SB; ++u)
+            if (s0 + u < k) {
+                sum.x += p[u].x;
+                sum.y += p[u].y;
+                sum.z += p[u].z;
+                sum.w += p[u].w;
+            }
+    }
+    *reinterpret_cast<float4*>(hp) = make_float4(x.x + sum.x, x.y + sum.y, x.z + sum.z, x.w + sum.w);
 }
 
 // ---- the GEMV ----
@@ -1007,22 +1014,25 @@ template <int QT, int MT, int EPI>
 int mb_launch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void* norm_w,
                 int norm_f16, float eps, const MbDefer* pend, hipStream_t stream) {
     const int kg = (j.n_slabs + 7) / 8;  // 8-column groups per thread
-    float* x = const_cast<float*>(j.x);  // written only when merging `pend`
-    auto prep = [&](auto kern, auto kmerge) {
-        if (pend && pend->part)
-            return launch(kmerge, dim3(1u, 32 * MT), dim3(256), 0, stream, x, j.ld_x, j.n_batch,
-                          j.n_slabs * kMbCols, norm_w, norm_f16, eps,
-                          const_cast<uint8_t*>(j.xrec), pend->part, pend->k, pend->stride);
-        return launch(kern, dim3((unsigned)kg, 32 * MT), dim3(256), 0, stream, x, j.ld_x,
+    if (pend && pend->part) {
+        // the pending residual add into x (the residual stream), then the
+        // preparation of the completed stream
+        const int cols = j.n_slabs * kMbCols;
+        const int64_t n4 = (int64_t)j.n_batch * (cols / 4);
+        const int rc = launch(mb_merge_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
+                              stream, const_cast<float*>(j.x), j.ld_x, j.n_batch, cols,
+                              pend->part, pend->k, pend->stride);
+        if (rc != JINF_HIP_OK) return rc;
+    }
+    auto prep = [&](auto kern) {
+        return launch(kern, dim3((unsigned)kg, 32 * MT), dim3(256), 0, stream, j.x, j.ld_x,
                       j.n_batch, j.n_slabs * kMbCols, norm_w, norm_f16, eps,
-                      const_cast<uint8_t*>(j.xrec), static_cast<const float*>(nullptr), 0,
-                      (int64_t)0);
+                      const_cast<uint8_t*>(j.xrec));
     };
-    const int rc =
-        kg <= 2   ? prep(mb_prepare_kernel<MT, 2, false>, mb_prepare_kernel<MT, 2, true>)
-        : kg <= 4 ? prep(mb_prepare_kernel<MT, 4, false>, mb_prepare_kernel<MT, 4, true>)
-        : kg <= 8 ? prep(mb_prepare_kernel<MT, 8, false>, mb_prepare_kernel<MT, 8, true>)
-                  : prep(mb_prepare_kernel<MT, 16, false>, mb_prepare_kernel<MT, 16, true>);
+    const int rc = kg <= 2 ? prep(mb_prepare_kernel<MT, 2>)
+                   : kg <= 4 ? prep(mb_prepare_kernel<MT, 4>)
+                   : kg <= 8 ? prep(mb_prepare_kernel<MT, 8>)
+                             : prep(mb_prepare_kernel<MT, 16>);
     if (rc != JINF_HIP_OK) return rc;
     (void)sh;  // kMbNarrow: 64 rows
     if constexpr (MT == 1)

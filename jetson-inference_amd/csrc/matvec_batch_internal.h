@@ -1,7 +1,8 @@
 // Internal interface of the batched GEMVs for the batch decoder (not in the
 // public headers): a residual add whose column-split partial sums are left
-// for the next preparation launch to merge, instead of being merged by the
-// GEMV's last workgroup of each row group.
+// for the next normed GEMV call to merge (a launch of its own ahead of that
+// call's preparation), instead of being merged by the GEMV's last workgroup
+// of each row group.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -23,9 +24,9 @@ size_t matvec_batch_defer_bytes(int rows, int cols, int n_batch);
 
 // jinf_matvec_batch_add's products, with the residual add left pending in
 // *out (part: matvec_batch_defer_bytes bytes, 16-byte aligned).  y is not
-// touched: the next call below that takes `pend` with h = y adds the merged
-// partial sums into h (in split order, as the GEMV's own merge does) before
-// it normalizes.
+// touched: the next call below that takes `pend` with h = y first adds the
+// partial sums into h (summed in split order, as the GEMV's own merge does),
+// then normalizes.
 int matvec_batch_add_defer(const void* weight, int qtype, const float* x, int ld_x, int rows,
                            int cols, int n_batch, float* part, size_t part_bytes, void* workspace,
                            size_t workspace_bytes, MbDefer* out, hipStream_t stream);
