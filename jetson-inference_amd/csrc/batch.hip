@@ -221,7 +221,7 @@ int bat_qkv(jinf_hip_batch* b, const jinf_hip_layer_weights& w, void* kc, void* 
             p[0], p[1], p[2], T[i], b->hidden, d.n_embd, w.attn_norm, w.attn_norm_type,
             d.rms_norm_eps, d.n_embd, b->q, b->q_dim, kc, vc, b->kv_type, ld_seq, b->positions,
             b->max_ctx, b->head_dim, d.n_heads, d.n_heads_kv, d.rope_freq_base, rows, b->mws,
-            b->mws_bytes, &pend, b->stream));
+            b->mws_bytes, &pend, b->dpart, b->dpart_bytes, b->stream));
         pend = MbDefer{};
     }
     return JINF_HIP_OK;
@@ -425,8 +425,12 @@ int bat_create(jinf_hip_batch** out, const jinf_hip_engine* engine, int n_seq, i
         if (w > b->mws_bytes) b->mws_bytes = w;
     }
     b->aws_bytes = jinf_attention_workspace_bytes(n_seq, d.n_heads, b->head_dim, max_context);
-    for (const int cols : {b->q_dim, nff}) {
-        const size_t w = matvec_batch_defer_bytes(n, cols, n_seq);
+    // partial sums of the deferred merges: output and down projections,
+    // and the Q / K / V launch
+    const int qkv_rows = b->q_dim + 2 * b->kv_dim;
+    for (const auto& sh : {std::make_pair(n, b->q_dim), std::make_pair(n, nff),
+                           std::make_pair(qkv_rows, n)}) {
+        const size_t w = matvec_batch_defer_bytes(sh.first, sh.second, n_seq);
         if (w > b->dpart_bytes) b->dpart_bytes = w;
     }
 

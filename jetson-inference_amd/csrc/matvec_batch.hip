@@ -425,6 +425,66 @@ __global__ __launch_bounds__(256) void mb_merge_kernel(float* __restrict__ h, in
     *reinterpret_cast<float4*>(hp) = make_float4(x.x + sum.x, x.y + sum.y, x.z + sum.z, x.w + sum.w);
 }
 
+// ---- the Q / K / V epilogue ----
+//
+// Virtual rows v0, v0 + 1 (a RoPE pair) of sequence b: q rows are rotated at
+// the sequence's position and stored into y; k rows are rotated and v rows
+// kept, each stored into the sequence's cache row at that position (a
+// position outside [0, max_ctx) stores nothing).
+__device__ __forceinline__ void mb_qkv_store(const MbJob& j, const RopeTheta& th, int b, int v0,
+                                             float a, float c) {
+    const int sgi = v0 < j.seg_end[0] ? 0 : v0 < j.seg_end[1] ? 1 : 2;
+    const int local = v0 - (sgi == 0 ? 0 : j.seg_end[sgi - 1]);
+    const int pos = j.pos[b];
+    if (sgi < 2) {
+        const float2 cs = rope_cs(pos, th.t[(local % j.head_dim) / 2]);
+        rot(a, c, cs.x, cs.y);
+    }
+    if (sgi == 0) {
+        float* yp = j.y + (int64_t)b * j.ld_y + local;
+        yp[0] = a;
+        yp[1] = c;
+    } else if (pos >= 0 && pos < j.max_ctx) {
+        const int64_t ci = (int64_t)b * j.ld_seq + (int64_t)pos * j.kv_dim + local;
+        void* cp = sgi == 1 ? j.kc : j.vc;
+        if (j.kv_f16) {
+            uint16_t* p = static_cast<uint16_t*>(cp) + ci;
+            p[0] = f2h(a);
+            p[1] = f2h(c);
+        } else {
+            float* p = static_cast<float*>(cp) + ci;
+            p[0] = a;
+            p[1] = c;
+        }
+    }
+}
+
+// The Q / K / V launch's epilogue after a deferred column split: one lane
+// per row pair of one sequence sums the k_splits partials in split order
+// (the order of the GEMV's own merge), then rotates and stores as above.
+__global__ __launch_bounds__(256) void mb_qkv_epilogue_kernel(MbJob j, RopeTheta th) {
+    constexpr int SB = 8;  // partials loaded together
+    const int half = j.rows / 2;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= j.n_batch * half) return;
+    const int b = i / half, v0 = 2 * (i % half);
+    const float* pp = j.dpart + (int64_t)b * j.rows + v0;
+    float a = 0.0f, c = 0.0f;
+    for (int s0 = 0; s0 < j.k_splits; s0 += SB) {
+        float2 p[SB];
+#pragma unroll
+        for (int u = 0; u < SB; ++u)
+            if (s0 + u < j.k_splits) p[u] = *reinterpret_cast<const float2*>(pp + (s0 + u) * j.dstride);
+#pragma unroll
+        for (int u = 0; u < SB; ++u)
+            if (s0 + u < j.k_splits) {
+                a += p[u].x;
+                c += p[u].y;
+            }
+    }
+    mb_qkv_store(j, th, b, v0, a, c);
+}
+
 // ---- the GEMV ----
 //
 // Per 256-column slab a workgroup copies, with direct-to-LDS loads, its
@@ -816,11 +876,12 @@ __global__ __launch_bounds__(64 * WV, 4 * mb_occ<MT>() / WV) void matvec_batch_k
         return mb_token(mt, r, ln >> 5);
     };
     auto local_of = [](int idx) { return (idx / (MT * 1024)) * 32 + (idx & 31); };
-    if constexpr (EPI == kMbEpiAdd) {
+    if constexpr (EPI == kMbEpiAdd || EPI == kMbEpiQKV) {
         if (j.dpart) {
-            // deferred residual add: this split's sums go to its own partial
-            // array, which the next preparation launch merges and adds (no
-            // counter, no cross-workgroup merge here)
+            // deferred merge: this split's sums go to its own partial array,
+            // summed afterwards by a launch of its own (the residual add's
+            // merge ahead of the next preparation, the Q / K / V epilogue):
+            // no counter, no cross-workgroup merge here
             float* dp = j.dpart + split * j.dstride;
 #pragma unroll
             for (int i = 0; i < PV; ++i) {
@@ -929,31 +990,7 @@ __global__ __launch_bounds__(64 * WV, 4 * mb_occ<MT>() / WV) void matvec_batch_k
             const int b = token_of(idx);
             const int v0 = group * ROWS + local_of(idx);
             if (b >= j.n_batch || v0 >= j.rows) continue;
-            float a = pv[idx], c = pv[idx + 1];
-            const int sgi = v0 < j.seg_end[0] ? 0 : v0 < j.seg_end[1] ? 1 : 2;
-            const int local = v0 - (sgi == 0 ? 0 : j.seg_end[sgi - 1]);
-            const int pos = j.pos[b];
-            if (sgi < 2) {
-                const float2 cs = rope_cs(pos, th.t[(local % j.head_dim) / 2]);
-                rot(a, c, cs.x, cs.y);
-            }
-            if (sgi == 0) {
-                float* yp = j.y + (int64_t)b * j.ld_y + local;
-                yp[0] = a;
-                yp[1] = c;
-            } else if (pos >= 0 && pos < j.max_ctx) {
-                const int64_t ci = (int64_t)b * j.ld_seq + (int64_t)pos * j.kv_dim + local;
-                void* cp = sgi == 1 ? j.kc : j.vc;
-                if (j.kv_f16) {
-                    uint16_t* p = static_cast<uint16_t*>(cp) + ci;
-                    p[0] = f2h(a);
-                    p[1] = f2h(c);
-                } else {
-                    float* p = static_cast<float*>(cp) + ci;
-                    p[0] = a;
-                    p[1] = c;
-                }
-            }
+            mb_qkv_store(j, th, b, v0, pv[idx], pv[idx + 1]);
         }
     }
 }
@@ -1254,7 +1291,7 @@ int rmsnorm_qkv_rope_batch_m(const void* wq, const void* wk, const void* wv, int
                              int64_t ld_seq, const int32_t* positions, int max_ctx, int head_dim,
                              int n_heads, int n_heads_kv, float freq_base, int n_batch,
                              void* workspace, size_t workspace_bytes, const MbDefer* pend,
-                             hipStream_t stream) {
+                             float* part, size_t part_bytes, hipStream_t stream) {
     if (head_dim <= 0 || head_dim % 2 != 0 || head_dim / 2 > kRopeMaxHalf || n_heads < 0 ||
         n_heads_kv < 0 || !(freq_base > 0.0f) || !positions)
         return JINF_HIP_ERR_INVALID;
@@ -1298,7 +1335,19 @@ int rmsnorm_qkv_rope_batch_m(const void* wq, const void* wk, const void* wv, int
     j.ld_seq = ld_seq;
     RopeTheta th;
     theta_table(th, head_dim, freq_base);
-    return mb_dispatch<kMbEpiQKV>(qtype, j, sh, th, norm_w, f16, eps, pend, stream);
+    if (part && j.k_splits > 1) {
+        // the column splits' merge and the epilogue in a launch of their own
+        if (!aligned(part, 16) ||
+            part_bytes < (size_t)j.k_splits * n_batch * rows * sizeof(float))
+            return JINF_HIP_ERR_INVALID;
+        j.dpart = part;
+        j.dstride = (int64_t)n_batch * rows;
+    }
+    rc = mb_dispatch<kMbEpiQKV>(qtype, j, sh, th, norm_w, f16, eps, pend, stream);
+    if (rc != JINF_HIP_OK || !j.dpart) return rc;
+    const int pairs = n_batch * (rows / 2);
+    return launch(mb_qkv_epilogue_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0,
+                  stream, j, th);
 }
 
 size_t matvec_batch_defer_bytes(int rows, int cols, int n_batch) {
@@ -1367,5 +1416,5 @@ extern "C" int jinf_rmsnorm_qkv_rope_batch(const void* wq, const void* wk, const
                                     norm_type, eps, n_embd, q, ld_q, k_cache, v_cache, kv_type,
                                     ld_seq, positions, max_ctx, head_dim, n_heads, n_heads_kv,
                                     freq_base, n_batch, workspace, workspace_bytes, nullptr,
-                                    stream);
+                                    nullptr, 0, stream);
 }

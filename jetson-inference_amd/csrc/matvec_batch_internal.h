@@ -34,6 +34,11 @@ int matvec_batch_add_defer(const void* weight, int qtype, const float* x, int ld
 // jinf_rmsnorm_matvec_batch, jinf_rmsnorm_swiglu_matvec_batch and
 // jinf_rmsnorm_qkv_rope_batch, first completing the pending residual add
 // `pend` (may be null) into h: h[b] += sum of its partials, written back.
+// The Q / K / V call also takes `part` (may be null; matvec_batch_defer_bytes
+// for its rows, 16-byte aligned): when its columns are split, the splits'
+// partial sums go there and a launch of its own sums them and applies the
+// RoPE / cache-store epilogue, instead of the GEMV's last workgroup of each
+// row group.
 int rmsnorm_matvec_batch_m(const void* weight, int qtype, float* h, int ld_h, const void* norm_w,
                            int norm_type, float eps, float* y, int ld_y, int rows, int cols,
                            int n_batch, void* workspace, size_t workspace_bytes,
@@ -48,6 +53,6 @@ int rmsnorm_qkv_rope_batch_m(const void* wq, const void* wk, const void* wv, int
                              int64_t ld_seq, const int32_t* positions, int max_ctx, int head_dim,
                              int n_heads, int n_heads_kv, float freq_base, int n_batch,
                              void* workspace, size_t workspace_bytes, const MbDefer* pend,
-                             hipStream_t stream);
+                             float* part, size_t part_bytes, hipStream_t stream);
 
 }  // namespace jinf
