@@ -244,19 +244,33 @@ __device__ __forceinline__ void mb_norm8(const void* norm_w, int norm_f16, int g
 // 4096 columns, 7 of 8 at 14336).  Every x and norm-weight load is issued
 // before any arithmetic (weights held in registers for KG <= 8), and the two
 // row reductions are DPP wave reductions with one LDS exchange.
+// chunk_slabs > 0 (no norm only): workgroup (c, b) takes slabs c chunk_slabs
+// .. + chunk_slabs - 1 as its whole row, so the scale s is per chunk: the
+// GEMV splits its columns in the same chunks and takes each split's 1 / s
+// from its first slab's record.  (Without a norm nothing needs the whole
+// row, and each workgroup then reads only the slabs it converts.)
 template <int MT, int KG>
 __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict__ x, int ld_x,
                                                           int n_batch, int cols,
                                                           const void* __restrict__ norm_w,
                                                           int norm_f16, float eps,
-                                                          uint8_t* __restrict__ rec) {
+                                                          uint8_t* __restrict__ rec,
+                                                          int chunk_slabs) {
     __shared__ double red[4];
     __shared__ float redf[4];
     const int b = blockIdx.y;
     const int tid = threadIdx.x;
+    int c0 = 0;                // first column of this workgroup's row
+    int sel = blockIdx.x;      // which of each thread's groups it converts (-1: all)
+    if (chunk_slabs > 0) {
+        c0 = blockIdx.x * chunk_slabs * kMbCols;
+        cols = min(cols - c0, chunk_slabs * kMbCols);
+        rec += (int64_t)blockIdx.x * chunk_slabs * mb_rec(MT);
+        sel = -1;
+    }
     const int ng = cols / 8;  // a multiple of 32
     const bool live = b < n_batch;
-    const float* xr = x + (int64_t)(live ? b : 0) * ld_x;
+    const float* xr = x + (int64_t)(live ? b : 0) * ld_x + c0;
     constexpr bool GW_EARLY = KG <= 8;
     float v[KG][8];
     float gwr[GW_EARLY ? KG : 1][8];
@@ -332,7 +346,7 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
 #pragma unroll
         for (int k = 0; k < KG; ++k) {
             const int g = tid + 256 * k;
-            if (g < ng && k == (int)blockIdx.x) {  // only this workgroup's groups
+            if (g < ng && (sel < 0 || k == sel)) {  // only this workgroup's groups
 #pragma clang fp contract(off)
                 float gw[8];
                 gweights(k, g, gw);
@@ -351,7 +365,7 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
     for (int k = 0; k < KG; ++k) {
         const int g = tid + 256 * k;
         // this workgroup's 256 groups (uniform over aligned groups of 32 threads)
-        const bool here = g < ng && k == (int)blockIdx.x;
+        const bool here = g < ng && (sel < 0 || k == sel);
         const int slab = g >> 5, gi = g & 31, t = gi >> 1, h = gi & 1;
         uint8_t* r = rec + (int64_t)slab * mb_rec(MT);
         float sum = 0.0f;
@@ -836,9 +850,9 @@ __global__ __launch_bounds__(64 * WV, 4 * mb_occ<MT>() / WV) void matvec_batch_k
     __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
     __syncthreads();
     // the sums are in units of x * s: 1 / s per token (the same in every
-    // slab's record) scales them exactly
+    // slab of the split's records) scales them exactly
     {
-        const float* inv = reinterpret_cast<const float*>(j.xrec + MT * 32768);
+        const float* inv = reinterpret_cast<const float*>(j.xrec + (int64_t)s0 * REC + MT * 32768);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -1061,12 +1075,19 @@ int mb_launch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void*
                               pend->part, pend->k, pend->stride);
         if (rc != JINF_HIP_OK) return rc;
     }
+    // without a norm and with split columns: one scale per split's chunk,
+    // each preparation workgroup reading only its chunk
+    const bool chunked = !norm_w && j.k_splits > 1;
     auto prep = [&](auto kern) {
-        return launch(kern, dim3((unsigned)kg, 32 * MT), dim3(256), 0, stream, j.x, j.ld_x,
-                      j.n_batch, j.n_slabs * kMbCols, norm_w, norm_f16, eps,
-                      const_cast<uint8_t*>(j.xrec));
+        return launch(kern, dim3((unsigned)(chunked ? j.k_splits : kg), 32 * MT), dim3(256), 0,
+                      stream, j.x, j.ld_x, j.n_batch, j.n_slabs * kMbCols, norm_w, norm_f16, eps,
+                      const_cast<uint8_t*>(j.xrec), chunked ? j.slabs_per_split : 0);
     };
-    const int rc = kg <= 2 ? prep(mb_prepare_kernel<MT, 2>)
+    const int rc = chunked ? (j.slabs_per_split <= 16   ? prep(mb_prepare_kernel<MT, 2>)
+                              : j.slabs_per_split <= 32 ? prep(mb_prepare_kernel<MT, 4>)
+                              : j.slabs_per_split <= 64 ? prep(mb_prepare_kernel<MT, 8>)
+                                                        : prep(mb_prepare_kernel<MT, 16>))
+                   : kg <= 2 ? prep(mb_prepare_kernel<MT, 2>)
                    : kg <= 4 ? prep(mb_prepare_kernel<MT, 4>)
                    : kg <= 8 ? prep(mb_prepare_kernel<MT, 8>)
                              : prep(mb_prepare_kernel<MT, 16>);
