@@ -949,6 +949,8 @@ _KERNEL_KEYS = [("ew_vec_kernel<unsigned short, 1", "swiglu"),
                 ("matvec_batch_kernel<14, 2, 0,", "batch output head (Q6_K, 2 M-tiles)"),
                 ("matvec_batch_kernel", "batch gemv (other)"),
                 ("mb_prepare_kernel", "batch x preparation"),
+                ("mb_merge_kernel", "batch residual merge"),
+                ("mb_qkv_epilogue_kernel", "batch qkv merge+rope"),
                 ("bat_argmax", "batch argmax"),
                 ("bat_begin_kernel", "batch step begin"),
                 ("bat_embed", "batch embedding")]
