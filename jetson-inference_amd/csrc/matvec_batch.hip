@@ -244,22 +244,29 @@ __device__ __forceinline__ void mb_norm8(const void* norm_w, int norm_f16, int g
 // 4096 columns, 7 of 8 at 14336).  Every x and norm-weight load is issued
 // before any arithmetic (weights held in registers for KG <= 8), and the two
 // row reductions are DPP wave reductions with one LDS exchange.
-// chunk_slabs > 0 (no norm only): workgroup (c, b) takes slabs c chunk_slabs
-// .. + chunk_slabs - 1 as its whole row, so the scale s is per chunk: the
-// GEMV splits its columns in the same chunks and takes each split's 1 / s
-// from its first slab's record.  (Without a norm nothing needs the whole
-// row, and each workgroup then reads only the slabs it converts.)
+// chunk_slabs > 0: workgroup (c, b) reads and converts only slabs c
+// chunk_slabs .. + chunk_slabs - 1.  Without row statistics (no norm only)
+// that chunk is its whole row, so the scale s is per chunk: the GEMV splits
+// its columns in the same chunks and takes each split's 1 / s from its first
+// slab's record.  With row statistics st_ss / st_mx ([n_batch][st_n]: the
+// sums of squares and largest |x g| of the row's slices, written by the
+// residual merge that produced x) the whole row's reduction is read from
+// them instead, in slice order.
 template <int MT, int KG>
 __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict__ x, int ld_x,
                                                           int n_batch, int cols,
                                                           const void* __restrict__ norm_w,
                                                           int norm_f16, float eps,
                                                           uint8_t* __restrict__ rec,
-                                                          int chunk_slabs) {
+                                                          int chunk_slabs,
+                                                          const double* __restrict__ st_ss,
+                                                          const float* __restrict__ st_mx,
+                                                          int st_n) {
     __shared__ double red[4];
     __shared__ float redf[4];
     const int b = blockIdx.y;
     const int tid = threadIdx.x;
+    const int row_cols = cols;
     int c0 = 0;                // first column of this workgroup's row
     int sel = blockIdx.x;      // which of each thread's groups it converts (-1: all)
     if (chunk_slabs > 0) {
@@ -271,6 +278,7 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
     const int ng = cols / 8;  // a multiple of 32
     const bool live = b < n_batch;
     const float* xr = x + (int64_t)(live ? b : 0) * ld_x + c0;
+    const int g0 = c0 / 8;  // norm-weight group of this row's first column
     constexpr bool GW_EARLY = KG <= 8;
     float v[KG][8];
     float gwr[GW_EARLY ? KG : 1][8];
@@ -292,7 +300,7 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
         for (int k = 0; k < KG; ++k) {
             const int g = tid + 256 * k;
             if (g < ng) {
-                mb_norm8(norm_w, norm_f16, g, gwr[k]);
+                mb_norm8(norm_w, norm_f16, g0 + g, gwr[k]);
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) gwr[k][e] = 1.0f;
@@ -304,7 +312,7 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
 #pragma unroll
             for (int e = 0; e < 8; ++e) gw[e] = gwr[k][e];
         } else {
-            mb_norm8(norm_w, norm_f16, g, gw);
+            mb_norm8(norm_w, norm_f16, g0 + g, gw);
         }
     };
     // one workgroup reduction: the sum of squares (norm_w) and the largest
@@ -313,35 +321,45 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
     // 2^15 (1 + 2^-21), far inside fp16's range)
     double ss = 0.0;
     float m = 0.0f;
-#pragma unroll
-    for (int k = 0; k < KG; ++k) {
-        const int g = tid + 256 * k;
-        if (g < ng) {
-            float gw[8];
-            gweights(k, g, gw);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                if (norm_w) ss = fma((double)v[k][e], (double)v[k][e], ss);
-                m = fmaxf(m, fabsf(v[k][e] * gw[e]));
+    if (st_ss) {
+        // the row's reduction, done by the merge that wrote x
+        if (live) {
+            for (int i = 0; i < st_n; ++i) {
+                ss += st_ss[(int64_t)b * st_n + i];
+                m = fmaxf(m, st_mx[(int64_t)b * st_n + i]);
             }
         }
-    }
-    ss = wave_sum_f64(ss);
-    m = wave_max_f32(m);
-    if ((tid & (kWave - 1)) == 0) {
-        red[tid / kWave] = ss;
-        redf[tid / kWave] = m;
-    }
-    __syncthreads();
-    ss = red[0];
-    m = redf[0];
+    } else {
 #pragma unroll
-    for (int i = 1; i < 4; ++i) {
-        ss += red[i];
-        m = fmaxf(m, redf[i]);
+        for (int k = 0; k < KG; ++k) {
+            const int g = tid + 256 * k;
+            if (g < ng) {
+                float gw[8];
+                gweights(k, g, gw);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    if (norm_w) ss = fma((double)v[k][e], (double)v[k][e], ss);
+                    m = fmaxf(m, fabsf(v[k][e] * gw[e]));
+                }
+            }
+        }
+        ss = wave_sum_f64(ss);
+        m = wave_max_f32(m);
+        if ((tid & (kWave - 1)) == 0) {
+            red[tid / kWave] = ss;
+            redf[tid / kWave] = m;
+        }
+        __syncthreads();
+        ss = red[0];
+        m = redf[0];
+#pragma unroll
+        for (int i = 1; i < 4; ++i) {
+            ss += red[i];
+            m = fmaxf(m, redf[i]);
+        }
     }
     if (norm_w && live) {
-        const float rs = rms_scale(ss, cols, eps);
+        const float rs = rms_scale(ss, row_cols, eps);
         m = rs * m;
 #pragma unroll
         for (int k = 0; k < KG; ++k) {
@@ -403,40 +421,87 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
 //
 // h[b][c] += p_0[b][c] + p_1[b][c] + ... (split order, the order of the
 // GEMV's own merge) for the k partial arrays p_s = part + s * stride of a
-// deferred residual add ([n_batch][cols], cols a multiple of 4).  One lane
-// per 4 columns of one sequence, every partial's load issued before the
-// sums; a launch of its own over many workgroups (folding it into the
-// preparation, one workgroup per sequence so that the in-place update had
-// no reader elsewhere, took 10.5 us per launch: one CU's outstanding loads
-// bound the partials' read).
+// deferred residual add ([n_batch][cols], cols a multiple of 256).  Grid
+// (slices of 2048 columns, n_batch), one lane per 8 columns, every
+// partial's load issued before the sums.  It also reduces each slice of the
+// new row for the preparation that follows: the fp64 sum of squares and the
+// largest |h g| (g the RMSNorm weights, or 1), the preparation's own
+// per-element terms, into ss_out / mx_out [n_batch][slices].  (Folding the
+// merge into the preparation, one workgroup per sequence so that the
+// in-place update had no reader elsewhere, took 10.5 us per launch: one
+// CU's outstanding loads bound the partials' read.)
+constexpr int kMbSliceCols = 2048;
 __global__ __launch_bounds__(256) void mb_merge_kernel(float* __restrict__ h, int ld_h,
                                                        int n_batch, int cols,
                                                        const float* __restrict__ part, int k,
-                                                       int64_t stride) {
+                                                       int64_t stride,
+                                                       const void* __restrict__ norm_w,
+                                                       int norm_f16, double* __restrict__ ss_out,
+                                                       float* __restrict__ mx_out) {
+    __shared__ double red[4];
+    __shared__ float redf[4];
     constexpr int SB = 8;  // partials loaded together
-    const int c4 = cols / 4;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t)n_batch * c4) return;
-    const int b = (int)(i / c4), c = 4 * (int)(i % c4);
-    float* hp = h + (int64_t)b * ld_h + c;
-    const float* pp = part + (int64_t)b * cols + c;
-    const float4 x = *reinterpret_cast<const float4*>(hp);
-    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int s0 = 0; s0 < k; s0 += SB) {
-        float4 p[SB];
+    const int b = blockIdx.y, tid = threadIdx.x;
+    const int g = blockIdx.x * (kMbSliceCols / 8) + tid;  // 8-column group
+    double ss = 0.0;
+    float m = 0.0f;
+    if (g < cols / 8) {
+        float* hp = h + (int64_t)b * ld_h + 8 * g;
+        const float* pp = part + (int64_t)b * cols + 8 * g;
+        float v[8];
+        {
+            const float4 p = *reinterpret_cast<const float4*>(hp);
+            const float4 q = *reinterpret_cast<const float4*>(hp + 4);
+            v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w;
+            v[4] = q.x; v[5] = q.y; v[6] = q.z; v[7] = q.w;
+        }
+        float gw[8];
+        mb_norm8(norm_w, norm_f16, g, gw);
+        float sum[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s0 = 0; s0 < k; s0 += SB) {
+            float4 pv[SB][2];
 #pragma unroll
-        for (int u = 0; u < SB; ++u)
-            if (s0 + u < k) p[u] = *reinterpret_cast<const float4*>(pp + (s0 + u) * stride);
+            for (int u = 0; u < SB; ++u)
+                if (s0 + u < k) {
+                    pv[u][0] = *reinterpret_cast<const float4*>(pp + (s0 + u) * stride);
+                    pv[u][1] = *reinterpret_cast<const float4*>(pp + (s0 + u) * stride + 4);
+                }
 #pragma unroll
-        for (int u = 0; u < SB; ++u)
-            if (s0 + u < k) {
-                sum.x += p[u].x;
-                sum.y += p[u].y;
-                sum.z += p[u].z;
-                sum.w += p[u].w;
-            }
+            for (int u = 0; u < SB; ++u)
+                if (s0 + u < k) {
+                    sum[0] += pv[u][0].x; sum[1] += pv[u][0].y;
+                    sum[2] += pv[u][0].z; sum[3] += pv[u][0].w;
+                    sum[4] += pv[u][1].x; sum[5] += pv[u][1].y;
+                    sum[6] += pv[u][1].z; sum[7] += pv[u][1].w;
+                }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            v[e] = v[e] + sum[e];
+            if (norm_w) ss = fma((double)v[e], (double)v[e], ss);
+            m = fmaxf(m, fabsf(v[e] * gw[e]));
+        }
+        *reinterpret_cast<float4*>(hp) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(hp + 4) = make_float4(v[4], v[5], v[6], v[7]);
     }
-    *reinterpret_cast<float4*>(hp) = make_float4(x.x + sum.x, x.y + sum.y, x.z + sum.z, x.w + sum.w);
+    ss = wave_sum_f64(ss);
+    m = wave_max_f32(m);
+    if ((tid & (kWave - 1)) == 0) {
+        red[tid / kWave] = ss;
+        redf[tid / kWave] = m;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        ss = red[0];
+        m = redf[0];
+#pragma unroll
+        for (int i = 1; i < 4; ++i) {
+            ss += red[i];
+            m = fmaxf(m, redf[i]);
+        }
+        ss_out[(int64_t)b * gridDim.x + blockIdx.x] = ss;
+        mx_out[(int64_t)b * gridDim.x + blockIdx.x] = m;
+    }
 }
 
 // ---- the Q / K / V epilogue ----
@@ -1065,25 +1130,32 @@ template <int QT, int MT, int EPI>
 int mb_launch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void* norm_w,
                 int norm_f16, float eps, const MbDefer* pend, hipStream_t stream) {
     const int kg = (j.n_slabs + 7) / 8;  // 8-column groups per thread
-    if (pend && pend->part) {
-        // the pending residual add into x (the residual stream), then the
-        // preparation of the completed stream
+    const bool merged = pend && pend->part;
+    if (merged) {
+        // the pending residual add into x (the residual stream) with the new
+        // rows' slice statistics, then the preparation of the completed
+        // stream from those statistics
         const int cols = j.n_slabs * kMbCols;
-        const int64_t n4 = (int64_t)j.n_batch * (cols / 4);
-        const int rc = launch(mb_merge_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
-                              stream, const_cast<float*>(j.x), j.ld_x, j.n_batch, cols,
-                              pend->part, pend->k, pend->stride);
+        const int rc = launch(mb_merge_kernel, dim3((unsigned)kg, (unsigned)j.n_batch), dim3(256),
+                              0, stream, const_cast<float*>(j.x), j.ld_x, j.n_batch, cols,
+                              pend->part, pend->k, pend->stride, norm_w, norm_f16, pend->ss,
+                              pend->mx);
         if (rc != JINF_HIP_OK) return rc;
     }
     // without a norm and with split columns: one scale per split's chunk,
-    // each preparation workgroup reading only its chunk
-    const bool chunked = !norm_w && j.k_splits > 1;
+    // each preparation workgroup reading only its chunk; after a merge: the
+    // 2048-column chunks of the full-row layout, each reading only its own
+    const bool chunked = !merged && !norm_w && j.k_splits > 1;
     auto prep = [&](auto kern) {
         return launch(kern, dim3((unsigned)(chunked ? j.k_splits : kg), 32 * MT), dim3(256), 0,
                       stream, j.x, j.ld_x, j.n_batch, j.n_slabs * kMbCols, norm_w, norm_f16, eps,
-                      const_cast<uint8_t*>(j.xrec), chunked ? j.slabs_per_split : 0);
+                      const_cast<uint8_t*>(j.xrec),
+                      chunked ? j.slabs_per_split : merged ? kMbSliceCols / kMbCols : 0,
+                      merged ? static_cast<const double*>(pend->ss) : nullptr,
+                      merged ? static_cast<const float*>(pend->mx) : nullptr, kg);
     };
-    const int rc = chunked ? (j.slabs_per_split <= 16   ? prep(mb_prepare_kernel<MT, 2>)
+    const int rc = merged ? prep(mb_prepare_kernel<MT, 2>)
+                   : chunked ? (j.slabs_per_split <= 16   ? prep(mb_prepare_kernel<MT, 2>)
                               : j.slabs_per_split <= 32 ? prep(mb_prepare_kernel<MT, 4>)
                               : j.slabs_per_split <= 64 ? prep(mb_prepare_kernel<MT, 8>)
                                                         : prep(mb_prepare_kernel<MT, 16>))
@@ -1379,7 +1451,9 @@ size_t matvec_batch_defer_bytes(int rows, int cols, int n_batch) {
     const int groups = (rows + sh.rows_per_group(kMbEpiAdd) - 1) / sh.rows_per_group(kMbEpiAdd);
     int per;
     const int k = mb_split(groups, cols / kMbCols, &per);
-    return (size_t)k * n_batch * rows * sizeof(float);
+    // the partials, then the merge's slice statistics (fp64 sums, fp32 maxima)
+    const size_t slices = (size_t)(rows + kMbSliceCols - 1) / kMbSliceCols;
+    return (size_t)k * n_batch * rows * sizeof(float) + slices * n_batch * (8 + 4);
 }
 
 int matvec_batch_add_defer(const void* weight, int qtype, const float* x, int ld_x, int rows,
@@ -1399,6 +1473,9 @@ int matvec_batch_add_defer(const void* weight, int qtype, const float* x, int ld
     out->part = part;
     out->k = j.k_splits;
     out->stride = j.dstride;
+    const int64_t slices = (rows + kMbSliceCols - 1) / kMbSliceCols;
+    out->ss = reinterpret_cast<double*>(part + (int64_t)j.k_splits * j.dstride);
+    out->mx = reinterpret_cast<float*>(out->ss + slices * n_batch);
     return mb_dispatch<kMbEpiAdd>(qtype, j, sh, MbNoTheta{}, nullptr, 0, 0.0f, nullptr, stream);
 }
 

@@ -12,11 +12,15 @@
 namespace jinf {
 
 // Partial sums of a deferred residual add y += W x: part[s][b][r] for split
-// s < k, sequence b < n_batch, row r < rows (stride elements between splits).
+// s < k, sequence b < n_batch, row r < rows (stride elements between splits);
+// ss / mx: room for the merge's statistics of the new rows, per 2048-row
+// slice (sum of squares, largest |y g| for the normed GEMV that follows).
 struct MbDefer {
     float* part = nullptr;
     int k = 0;
     int64_t stride = 0;
+    double* ss = nullptr;
+    float* mx = nullptr;
 };
 
 // Bytes of the partial sums of matvec_batch_add_defer at this shape.
