@@ -416,6 +416,8 @@ __device__ __forceinline__ void am_merge_last(float* __restrict__ out, int64_t l
 // {O[HD], m, l} to ws, and either the last workgroup of the (sequence, head
 // group) to finish merges them (counters: one per (sequence, head group),
 // zero between calls) or, counters == nullptr, attn_combine_kernel does.
+typedef short am_tr4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) am_tr4 am_lds_tr4;
 template <int HD, bool MERGE, bool RB>
 __global__ __launch_bounds__(256) void attn_mfma_kernel(
     float* __restrict__ out, int64_t ld_out, const float* __restrict__ q, int64_t ld_q,
@@ -437,7 +439,9 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     constexpr int NBK = RB ? 1 : 4;    // 16-row blocks of a tile this wave processes
     constexpr int PITCH = HD * 2;      // LDS bytes per staged V row
     constexpr int MS = HD + 2;         // merge record: O[HD], m, l
-    extern __shared__ uint8_t am_lds[];
+    // 16-byte aligned: the merge's static LDS word comes first, and the
+    // tiles' 8- and 16-byte reads need aligned addresses
+    extern __shared__ __attribute__((aligned(16))) uint8_t am_lds[];
     const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
     const int col = lane & 15, lg = lane >> 4;
     const int slot = col & 7;          // head slot of this column
@@ -487,7 +491,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     // stay in flight.  Rows past the end read as zeros (masked out).  K slot
     // (row r, p) holds chunk p ^ swizzle(r) so that the
     // 16 rows of a fragment read hit distinct banks; V slot (r, p) holds
-    // chunk p ^ 2 ((r >> 2) & 3) for the same reason.
+    // chunk p ^ 2 (r & 3), so that the four rows a 16-lane transposing read
+    // touches sit in distinct bank groups.
     uint8_t* kst = vst + kAtTile * PITCH;  // this wave's K tile, after its V tile
     auto kswz = [](int r) { return HD == 128 ? (r & 15) : ((r >> 1) & 7); };
     const int i0 = RB ? VLDW * wave : 0;  // first load instruction of the wave's rows
@@ -509,7 +514,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
         const int slot_i = kWave * (i0 + ii) + lane;
         const int row = slot_i / VCH;
         koff[ii] = (uint32_t)row * rowb + 16u * (uint32_t)((slot_i % VCH) ^ kswz(row));
-        voff[ii] = (uint32_t)row * rowb + 16u * (uint32_t)((slot_i % VCH) ^ (2 * ((row >> 2) & 3)));
+        voff[ii] = (uint32_t)row * rowb + 16u * (uint32_t)((slot_i % VCH) ^ (2 * (row & 3)));
     }
     auto load_k = [&](int t0) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only: K buffer reads are done
@@ -630,14 +635,19 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 #pragma unroll
         for (int bi = 0; bi < NBK; ++bi) {
             const int b = RB ? wave : bi;
-            const uint8_t* vrow = vst + (16 * b + 4 * lg) * PITCH + 2 * (col & 7);
+            // B fragment V[16 b + 4 lg + i][16 n + col], i = 0..3, through
+            // one transposing LDS read (ds_read_b64_tr_b16: within each 16
+            // lanes, lane c receives element c % 4 of the 8 bytes read by
+            // lanes c / 4 + 4 i): lane c reads row 16 b + 4 lg + c / 4,
+            // columns 16 n + 4 (c % 4) .. + 3
+            const int vr = 16 * b + 4 * lg + (col >> 2);
+            const uint8_t* vrow = vst + vr * PITCH + 8 * (col & 1);
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
-                const int p = (2 * n + (col >> 3)) ^ (2 * lg);  // swizzled chunk
-                const uint16_t* p0 = reinterpret_cast<const uint16_t*>(vrow + 16 * p);
-                const uint32_t x0 = p0[0] | ((uint32_t)p0[PITCH / 2] << 16);
-                const uint32_t x1 = p0[PITCH] | ((uint32_t)p0[3 * PITCH / 2] << 16);
-                O[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(P[bi], am_h4_from(x0, x1), O[n], 0, 0, 0);
+                const int p = (2 * n + ((col & 3) >> 1)) ^ (2 * (vr & 3));  // swizzled chunk
+                const am_tr4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (am_lds_tr4*)(vrow + 16 * p));
+                O[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(P[bi], __builtin_bit_cast(am_h4, t), O[n], 0, 0, 0);
             }
         }
         wave_lds_sync();
