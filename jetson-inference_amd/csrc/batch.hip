@@ -171,7 +171,7 @@ struct jinf_hip_batch {
     int32_t *acts = nullptr, *positions = nullptr, *lens = nullptr, *hist = nullptr;
     void* mws = nullptr;  // batched-GEMV workspace
     size_t mws_bytes = 0;
-    float* dpart = nullptr;  // partial sums of the deferred residual adds
+    float* dpart = nullptr;  // partial sums of the deferred split merges
     size_t dpart_bytes = 0;
     void* aws = nullptr;  // attention workspace
     size_t aws_bytes = 0;
@@ -202,7 +202,7 @@ int bat_embed(jinf_hip_batch* b, int rows) {
 }
 
 // `pend`: the previous layer's deferred down-projection residual add, merged
-// into the residual stream by the first launch's preparation.
+// into the residual stream by a launch ahead of the first call's preparation.
 int bat_qkv(jinf_hip_batch* b, const jinf_hip_layer_weights& w, void* kc, void* vc, int rows,
             int64_t ld_seq, MbDefer& pend) {
     const jinf_hip_engine_desc& d = *b->d;
