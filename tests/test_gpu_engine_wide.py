@@ -3,7 +3,11 @@ hidden 4096, 32 query / 8 KV heads of 128, FFN 14336 and a 128256-token
 vocabulary, in the two weight layouts bench.py times (Q4_0 with a Q6_K output
 head, and Q4_K_M: Q4_K with Q6_K for attn_v, ffn_down and the output), fp16
 KV cache, checked after each of 4 tokens against the oracle's decode loop
-(oracle/engine.py).
+(oracle/engine.py).  The batch decoder at the same widths: 5 and 40
+sequences (one and two 32-sequence tiles of the batched GEMVs, whose column
+splits are merged by separate launches and whose residual merges hand 2048-
+column slice statistics to the normalising preparation), a prompt through
+prefill, then decode steps, each sequence against its own oracle loop.
 
 Bar: |logits - logits_oracle| <= 4e-4 * max |logits_oracle| (the fp16-cache
 bar of test_gpu_engine.py).  The kernels at these shapes are checked one at a
@@ -18,7 +22,7 @@ import model_util as mu
 import oracle
 import testutil as tu
 from gpu_util import say
-from jinf_amd.engine import Engine
+from jinf_amd.engine import Batch, Engine
 from oracle import engine as oeng
 
 pytestmark = pytest.mark.gpu
@@ -83,3 +87,46 @@ def test_llama3_8b_widths_match_oracle(dev, layout):
                 assert err <= TOL * scale, f"{layout} token {i}"
     finally:
         oracle.set_threads(1)
+
+
+STREAMS = [(128000, 9906, 1917), (128000, 40, 3), (5, 6, 7)]
+
+
+@pytest.mark.parametrize("n_seq", [5, 40])
+def test_llama3_8b_widths_batch_decode(dev, n_seq):
+    """Sequence s decodes STREAMS[s % 3] after sequence 0 took a 6-token prompt
+    through prefill; sequences of one stream must agree with that stream's
+    oracle loop (and so with each other), sequence 0 with its own."""
+    types, embd_type, out_type = LAYOUTS["q4_0"]
+    say(f"2-layer Llama-3-8B-wide model, q4_0, batch of {n_seq}, fp16 KV cache")
+    hp, W = wide_model(types, embd_type, out_type, seed=8192 + n_seq)
+    prompt = (128000, 791, 6864, 315, 9822, 374)
+    refs = [oeng.Decoder(hp, W, max_context=16, kv_type=mu.F16) for _ in STREAMS]
+    ref0 = oeng.Decoder(hp, W, max_context=16, kv_type=mu.F16)
+    oracle.set_threads(16)
+    try:
+        with Engine(hp, mu.to_device(W), 16, mu.F16) as e, Batch(e, n_seq, 16, mu.F16) as b:
+            got = b.prefill(0, prompt)
+            for tok in prompt:
+                want = ref0.step(tok)
+            check_logits(got, want, f"batch {n_seq} prefill")
+            for k in range(3):
+                row = np.array([STREAMS[s % 3][k] for s in range(n_seq)], np.int32)
+                b.forward(row)
+                lg = b.logits()
+                want = [r.step(st[k]) for r, st in zip(refs, STREAMS)]
+                want0 = ref0.step(int(row[0]))
+                check_logits(lg[0], want0, f"batch {n_seq} step {k} seq 0")
+                for s in range(1, n_seq):
+                    check_logits(lg[s], want[s % 3], f"batch {n_seq} step {k} seq {s}", quiet=s > 3)
+    finally:
+        oracle.set_threads(1)
+
+
+def check_logits(got, want, what, quiet=False):
+    scale = float(np.max(np.abs(want)))
+    err = float(np.max(np.abs(got.astype(np.float64) - want.astype(np.float64))))
+    if not quiet:
+        say(f"{what}: max error / max |logit| = {err / scale:.2e}")
+    assert np.all(np.isfinite(got)), what
+    assert err <= TOL * scale, f"{what}: {err / scale:.2e}"
