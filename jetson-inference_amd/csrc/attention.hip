@@ -45,6 +45,7 @@
 #include "jinf_device.h"
 #include "jinf_host.h"
 #include "jinf/kernels.h"
+#include "matvec_batch_internal.h"
 #include "jinf/kernels_ext.h"
 
 namespace jinf {
@@ -424,7 +425,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t ld_pos,
     int64_t ld_seq, const int32_t* __restrict__ lens, int n_past, int group, int G,
     int n_heads, float scale, float* __restrict__ ws, unsigned* __restrict__ counters,
-    int chunk) {
+    int chunk, uint8_t* __restrict__ xrec, int xmt) {
     constexpr int KS = HD / 16;        // k-steps of the score product
     constexpr int DPG = HD / 4;        // dims per lane group in the score product
     constexpr int KLD = DPG / 8;       // 16-byte K loads per position block
@@ -680,6 +681,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     __syncthreads();
     const int nch = gridDim.z;
     const bool direct = !ws || used <= 1;  // this workgroup holds the whole context
+    float* ov = reinterpret_cast<float*>(am_lds + (4 * 8 * MS * 4 + 15) / 16 * 16);  // [G HD]
+    float omax = 0.0f;  // largest |output| of this thread (x records)
     for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
         const int g = idx / HD, d = idx % HD;
         float M = -INFINITY;
@@ -694,7 +697,12 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
             }
         }
         if (direct) {
-            out[(int64_t)s * ld_out + (int64_t)(h0 + g) * HD + d] = den > 0.0f ? num / den : 0.0f;
+            const float o = den > 0.0f ? num / den : 0.0f;
+            out[(int64_t)s * ld_out + (int64_t)(h0 + g) * HD + d] = o;
+            if (xrec) {
+                ov[idx] = o;
+                omax = fmaxf(omax, fabsf(o));
+            }
         } else {
             // device-coherent stores only for the in-kernel merge; the
             // merge launch reads ordinary stores after the kernel boundary
@@ -713,6 +721,35 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
                 }
             }
         }
+    }
+    if (xrec && direct) {
+        // The output projection's prepared x for this workgroup's G HD
+        // columns of token s (one column chunk of that GEMV's splits): the
+        // power-of-two scale of their largest magnitude, then the same
+        // fragments and slab data as the GEMV's own preparation writes.
+        float* red = ov + G * HD;
+        float mm = wave_max_f32(omax);
+        if (lane == 0) red[wave] = mm;
+        __syncthreads();  // ov and the wave maxima
+        mm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        const int ex = mb_scale_exp(mm);
+        const float sc = ldexpf(1.0f, 15 - ex);
+        const int t = threadIdx.x;
+        const int col0 = h0 * HD + 8 * t;  // the group's first column
+        const bool here = t < G * HD / 8;
+        uint8_t* r = xrec + (int64_t)(col0 / 256) * mb_rec_bytes(xmt);
+        const int gi = (col0 % 256) / 8;
+        float sum = 0.0f;
+        if (here) {
+            float v8[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v8[e] = ov[8 * t + e];
+            sum = mb_put_group(r, s, gi, v8, sc);
+        }
+        // Q4_K sub-block sums: lanes 4 q .. 4 q + 3 hold one 32-column sub-block
+        sum += __shfl_xor(sum, 1, kWave);
+        sum += __shfl_xor(sum, 2, kWave);
+        if (here) mb_put_meta(r, xmt, s, gi, sum, ex);
     }
     // Without MERGE, attn_combine_kernel merges the records.  (The merge is a
     // separate instantiation: its code in the same kernel, even unexecuted,
@@ -799,7 +836,7 @@ template <int HD>
 static int am_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, const void* k,
                      const void* v, int64_t ld_pos, int64_t ld_seq, const int32_t* lens,
                      int n_past, int n_seq, int n_heads, int group, int G, float scale,
-                     const AmScratch& sc, hipStream_t stream) {
+                     const AmScratch& sc, MbXRec* xr, hipStream_t stream) {
     const size_t shmem = (size_t)4 * 2 * kAtTile * HD * 2;  // K and V tile per wave
     // chunk: a multiple of 64 positions, at least kAmChunkMin, giving about
     // kAmTargetItems (sequence, head group, chunk) items
@@ -850,10 +887,18 @@ static int am_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, c
     const bool rb = chunk <= 2 * kAtTile;
     auto* kern = counters ? (rb ? attn_mfma_kernel<HD, true, true> : attn_mfma_kernel<HD, true, false>)
                           : (rb ? attn_mfma_kernel<HD, false, true> : attn_mfma_kernel<HD, false, false>);
+    // the output projection's x records, when every work item writes its
+    // output directly and one item's G HD columns are one of that GEMV's
+    // per-split chunks
+    uint8_t* xrec = nullptr;
+    if (xr && xr->rec && !split && xr->chunk_cols == G * HD && (xr->mt == 1 || xr->mt == 2) &&
+        n_seq <= 32 * xr->mt)
+        xrec = xr->rec;
     const int st = launch(kern, dim3(n_heads / G, n_seq, nch), dim3(256), shmem, stream, out,
                           ld_out, q, ld_q, static_cast<const uint16_t*>(k),
                           static_cast<const uint16_t*>(v), ld_pos, ld_seq, lens, n_past, group,
-                          G, n_heads, scale, ws, counters, chunk);
+                          G, n_heads, scale, ws, counters, chunk, xrec, xr ? xr->mt : 1);
+    if (xr) xr->wrote = st == JINF_HIP_OK && xrec != nullptr;
     if (st != JINF_HIP_OK || !split || in_kernel) return st;
     return launch(attn_combine_kernel, dim3(n_heads, n_seq), dim3(HD), 0, stream, out, ld_out,
                   (const float*)ws, lens, n_past, n_heads, HD, nch, chunk);
@@ -889,7 +934,8 @@ static int attention_decode(float* out, int64_t ld_out, const float* q, int64_t 
                             const void* k, const void* v, int kv_type, int64_t ld_pos,
                             int64_t ld_seq, const int32_t* lens, int n_past, int n_seq,
                             int head_dim, int n_heads, int n_heads_kv, float scale,
-                            const AmScratch& sc, hipStream_t stream) {
+                            const AmScratch& sc, hipStream_t stream, MbXRec* xr = nullptr) {
+    if (xr) xr->wrote = false;
     if (n_seq < 0 || head_dim <= 0 || n_heads <= 0 || n_heads_kv <= 0) return JINF_HIP_ERR_INVALID;
     if (n_seq == 0) return JINF_HIP_OK;
     if (!out || !q || !k || !v || n_heads % n_heads_kv != 0) return JINF_HIP_ERR_INVALID;
@@ -925,9 +971,9 @@ static int attention_decode(float* out, int64_t ld_out, const float* q, int64_t 
         const int G = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
         if (head_dim == 64)
             return am_launch<64>(out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq,
-                                 n_heads, group, G, scale, sc, stream);
+                                 n_heads, group, G, scale, sc, xr, stream);
         return am_launch<128>(out, ld_out, q, ld_q, k, v, ld_pos, ld_seq, lens, n_past, n_seq,
-                              n_heads, group, G, scale, sc, stream);
+                              n_heads, group, G, scale, sc, xr, stream);
     }
     // fp32 cache: enough (sequence, kv head) pairs: one workgroup per pair,
     // all its query heads (up to 8) together.  Otherwise one query head per
@@ -972,6 +1018,21 @@ extern "C" int jinf_attention_decode(float* out, int ld_out, const float* q, int
 }
 
 namespace jinf {
+
+int attention_decode_xrec(float* out, int ld_out, const float* q, int ld_q, const void* k_cache,
+                          const void* v_cache, int kv_type, int64_t ld_pos, int64_t ld_seq,
+                          const int32_t* lens, int n_seq, int max_ctx, int head_dim, int n_heads,
+                          int n_heads_kv, float scale, void* workspace, size_t workspace_bytes,
+                          MbXRec* xr, hipStream_t stream) {
+    if (xr) xr->wrote = false;
+    if ((!lens && n_seq > 0) || max_ctx < 0) return JINF_HIP_ERR_INVALID;
+    if (n_seq > 1 && ld_seq != 0 && ld_seq < (int64_t)max_ctx * ld_pos) return JINF_HIP_ERR_INVALID;
+    if (workspace && !aligned(workspace, 4)) return JINF_HIP_ERR_INVALID;
+    if (scale == 0.0f && head_dim > 0) scale = inv_sqrt_hd(head_dim);
+    return attention_decode(out, ld_out, q, ld_q, k_cache, v_cache, kv_type, ld_pos, ld_seq, lens,
+                            max_ctx, n_seq, head_dim, n_heads, n_heads_kv, scale,
+                            AmScratch{workspace, workspace_bytes, false}, stream, xr);
+}
 
 // This device's address of `scratch`: looked up with hipGetSymbolAddress on
 // the first call made while the device is current, then cached per device.

@@ -257,12 +257,20 @@ int bat_enqueue_rows(jinf_hip_batch* b, int rows, int seq, int new_pos) {
         char* kc = b->kv + (size_t)L * b->kv_layer_bytes + kv_off;
         char* vc = b->kv + (size_t)(d.n_layers + L) * b->kv_layer_bytes + kv_off;
         BAT_TRY(bat_qkv(b, w, kc, vc, ns, ld_seq, pend));
-        BAT_TRY(jinf_attention_decode(b->attn, b->q_dim, b->q, b->q_dim, kc, vc, b->kv_type,
+        // the attention also writes the output projection's x records when
+        // its work items are unsplit (short contexts), and that GEMV then
+        // skips its preparation launch
+        MbXRec xr;
+        xr.rec = matvec_batch_add_xrec(b->mws, w.attn_output_type, n, b->q_dim, ns,
+                                       &xr.chunk_cols);
+        xr.mt = ns > 32 ? 2 : 1;
+        BAT_TRY(attention_decode_xrec(b->attn, b->q_dim, b->q, b->q_dim, kc, vc, b->kv_type,
                                       b->kv_dim, ld_seq, b->lens, ns, b->bound, b->head_dim,
-                                      d.n_heads, d.n_heads_kv, 0.0f, b->aws, b->aws_bytes, s));
+                                      d.n_heads, d.n_heads_kv, 0.0f, b->aws, b->aws_bytes, &xr,
+                                      s));
         BAT_TRY(matvec_batch_add_defer(w.attn_output, w.attn_output_type, b->attn, b->q_dim, n,
                                        b->q_dim, ns, b->dpart, b->dpart_bytes, b->mws,
-                                       b->mws_bytes, &pend, s));
+                                       b->mws_bytes, &pend, xr.wrote, s));
         if (w.ffn_gate_type == w.ffn_up_type) {
             BAT_TRY(rmsnorm_swiglu_matvec_batch_m(w.ffn_gate, w.ffn_up, w.ffn_gate_type, b->hidden,
                                                   n, w.ffn_norm, w.ffn_norm_type, eps, b->ff, nff,
@@ -278,7 +286,8 @@ int bat_enqueue_rows(jinf_hip_batch* b, int rows, int seq, int new_pos) {
         }
         pend = MbDefer{};
         BAT_TRY(matvec_batch_add_defer(w.ffn_down, w.ffn_down_type, b->ff, nff, n, nff, ns,
-                                       b->dpart, b->dpart_bytes, b->mws, b->mws_bytes, &pend, s));
+                                       b->dpart, b->dpart_bytes, b->mws, b->mws_bytes, &pend,
+                                       false, s));
     }
     BAT_TRY(rmsnorm_matvec_batch_m(d.output, d.output_type, b->hidden, n, d.output_norm,
                                    d.output_norm_type, eps, b->logits, d.n_vocab, d.n_vocab, n, ns,

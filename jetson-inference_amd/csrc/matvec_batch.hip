@@ -109,6 +109,7 @@ struct MbJob {
     uint32_t* counters;    // [n_groups]
     float* dpart;          // kMbEpiAdd, deferred: partial sums [k_splits][n_batch][rows]
     int64_t dstride;       // (split stride), merged by the next preparation
+    int x_ready;           // (host) x already prepared in xrec: no preparation launch
 };
 
 struct MbNoTheta {};
@@ -200,6 +201,7 @@ __device__ __forceinline__ int mb_token(int mt, int r, int h) {
 //   columns).
 __host__ __device__ constexpr int mb_meta(int mt) { return 2048 * mt; }
 __host__ __device__ constexpr int mb_rec(int mt) { return mt * 32768 + mb_meta(mt); }
+static_assert(mb_rec(1) == mb_rec_bytes(1) && mb_rec(2) == mb_rec_bytes(2), "record layout");
 
 constexpr int kMbMaxCols = 32768;                 // columns the preparation holds
 
@@ -373,47 +375,21 @@ __global__ __launch_bounds__(256) void mb_prepare_kernel(const float* __restrict
             }
         }
     }
-    int ex = 15;
-    if (m > 0.0f && m <= 3.4e38f) {
-        (void)frexpf(m, &ex);  // m < 2^ex
-        ex = ex < -100 ? -100 : ex;
-    }
+    const int ex = mb_scale_exp(m);
     const float sc = ldexpf(1.0f, 15 - ex);
 #pragma unroll
     for (int k = 0; k < KG; ++k) {
         const int g = tid + 256 * k;
         // this workgroup's 256 groups (uniform over aligned groups of 32 threads)
         const bool here = g < ng && (sel < 0 || k == sel);
-        const int slab = g >> 5, gi = g & 31, t = gi >> 1, h = gi & 1;
+        const int slab = g >> 5, gi = g & 31;
         uint8_t* r = rec + (int64_t)slab * mb_rec(MT);
         float sum = 0.0f;
-        if (here) {
-            uint32_t hw[4], lw[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                // fragment slots 2 i, 2 i + 1 hold columns i and 4 + i of the group
-                const float a0 = v[k][i] * sc, a1 = v[k][4 + i] * sc;
-                const _Float16 h0 = (_Float16)a0, h1 = (_Float16)a1;
-                const _Float16 l0 = (_Float16)(a0 - (float)h0), l1 = (_Float16)(a1 - (float)h1);
-                hw[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
-                        ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-                lw[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
-                        ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sum += v[k][e] * sc;
-            uint8_t* f = r + (((b >> 5) * 16 + t) * 2) * 1024 + ((b & 31) + 32 * h) * 16;
-            *reinterpret_cast<uint4*>(f) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-            *reinterpret_cast<uint4*>(f + 1024) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-        }
+        if (here) sum = mb_put_group(r, b, gi, v[k], sc);
         // Q4_K sub-block sums: threads 4 q .. 4 q + 3 hold sub-block q's 32 columns
         sum += __shfl_xor(sum, 1, kWave);
         sum += __shfl_xor(sum, 2, kWave);
-        if (here) {
-            float* meta = reinterpret_cast<float*>(r + MT * 32768);
-            if ((gi & 3) == 0) meta[32 * MT + (gi >> 2) * 32 * MT + b] = sum;
-            if (gi == 0) meta[b] = ldexpf(1.0f, ex - 15);
-        }
+        if (here) mb_put_meta(r, MT, b, gi, sum, ex);
     }
 }
 
@@ -1154,7 +1130,8 @@ int mb_launch_t(MbJob& j, const MbShape& sh, const MbTheta<EPI>& th, const void*
                       merged ? static_cast<const double*>(pend->ss) : nullptr,
                       merged ? static_cast<const float*>(pend->mx) : nullptr, kg);
     };
-    const int rc = merged ? prep(mb_prepare_kernel<MT, 2>)
+    const int rc = j.x_ready ? JINF_HIP_OK
+                   : merged ? prep(mb_prepare_kernel<MT, 2>)
                    : chunked ? (j.slabs_per_split <= 16   ? prep(mb_prepare_kernel<MT, 2>)
                               : j.slabs_per_split <= 32 ? prep(mb_prepare_kernel<MT, 4>)
                               : j.slabs_per_split <= 64 ? prep(mb_prepare_kernel<MT, 8>)
@@ -1446,6 +1423,22 @@ int rmsnorm_qkv_rope_batch_m(const void* wq, const void* wk, const void* wv, int
                   stream, j, th);
 }
 
+uint8_t* matvec_batch_add_xrec(void* workspace, int qtype, int rows, int cols, int n_batch,
+                               int* chunk_cols) {
+    *chunk_cols = 0;
+    if (!workspace || rows <= 0 || cols <= 0 || cols % kMbCols != 0 || cols > kMbMaxCols ||
+        n_batch <= 0 || n_batch > kMbMaxBatch)
+        return nullptr;
+    const MbShape sh = mb_shape();
+    const int groups = (rows + sh.rows_per_group(kMbEpiAdd) - 1) / sh.rows_per_group(kMbEpiAdd);
+    int per;
+    const int k = mb_split(groups, cols / kMbCols, &per);
+    // (Q6_K at two M-tiles runs as two one-tile launches, each preparing its own)
+    if (k > 1 && (cols / kMbCols) % per == 0 && (n_batch <= 32 || qtype != kQ6_K))
+        *chunk_cols = per * kMbCols;
+    return static_cast<uint8_t*>(workspace) + mb_ctr_bytes(groups);
+}
+
 size_t matvec_batch_defer_bytes(int rows, int cols, int n_batch) {
     if (rows <= 0 || cols <= 0 || cols % kMbCols != 0 || cols > kMbMaxCols || n_batch <= 0 ||
         n_batch > kMbMaxBatch)
@@ -1461,7 +1454,7 @@ size_t matvec_batch_defer_bytes(int rows, int cols, int n_batch) {
 
 int matvec_batch_add_defer(const void* weight, int qtype, const float* x, int ld_x, int rows,
                            int cols, int n_batch, float* part, size_t part_bytes, void* workspace,
-                           size_t workspace_bytes, MbDefer* out, hipStream_t stream) {
+                           size_t workspace_bytes, MbDefer* out, bool x_ready, hipStream_t stream) {
     MbJob j{};
     MbShape sh;
     if (!w_ok(weight) || !out || !part || !aligned(part, 16)) return JINF_HIP_ERR_INVALID;
@@ -1473,6 +1466,10 @@ int matvec_batch_add_defer(const void* weight, int qtype, const float* x, int ld
     j.seg_end[0] = j.seg_end[1] = j.seg_end[2] = rows;
     j.dpart = part;
     j.dstride = (int64_t)n_batch * rows;
+    // records written by the producer: only where the preparation would be
+    // chunked the same way (no norm, split columns) and one launch covers
+    // every sequence (two M-tiles fit)
+    j.x_ready = x_ready && j.k_splits > 1 && (n_batch <= 32 || qtype != kQ6_K) ? 1 : 0;
     out->part = part;
     out->k = j.k_splits;
     out->stride = j.dstride;
