@@ -411,6 +411,13 @@ ENGINE_MODELS = {
                                                       "ffn_down"), 2),
                                    embd=2, out=14, batch=32,
                                    desc="Q4_0 weights, Q6_K output"),
+    # the Q4_K_M model decoding 32 sequences at once
+    "llama3-8b-decode-batch-q4_k_m": dict(mat=dict(attn_q=12, attn_k=12, attn_v=14,
+                                                   attn_output=12, ffn_gate=12, ffn_up=12,
+                                                   ffn_down=14),
+                                          embd=12, out=14, batch=32,
+                                          desc="Q4_K weights, Q6_K for attn_v, ffn_down and "
+                                               "output"),
 }
 LLAMA3_8B = dict(n_layers=32, n_embd=4096, n_heads=32, n_heads_kv=8, n_ff=14336,
                  n_vocab=128256, rope_freq_base=500000.0, rms_norm_eps=1e-5)
