@@ -209,6 +209,9 @@ int bat_qkv(jinf_hip_batch* b, const jinf_hip_layer_weights& w, void* kc, void* 
     const void* W[3] = {w.attn_q, w.attn_k, w.attn_v};
     const int T[3] = {w.attn_q_type, w.attn_k_type, w.attn_v_type};
     bool done[3] = {false, false, false};
+    // x prepared by an earlier call in the one-launch record layout (Q6_K
+    // beyond 32 rows runs two one-tile launches, each preparing its own)
+    bool prepared = false;
     for (int i = 0; i < 3; ++i) {
         if (done[i]) continue;
         const void* p[3] = {nullptr, nullptr, nullptr};
@@ -221,8 +224,9 @@ int bat_qkv(jinf_hip_batch* b, const jinf_hip_layer_weights& w, void* kc, void* 
             p[0], p[1], p[2], T[i], b->hidden, d.n_embd, w.attn_norm, w.attn_norm_type,
             d.rms_norm_eps, d.n_embd, b->q, b->q_dim, kc, vc, b->kv_type, ld_seq, b->positions,
             b->max_ctx, b->head_dim, d.n_heads, d.n_heads_kv, d.rope_freq_base, rows, b->mws,
-            b->mws_bytes, &pend, b->dpart, b->dpart_bytes, b->stream));
+            b->mws_bytes, &pend, b->dpart, b->dpart_bytes, prepared, b->stream));
         pend = MbDefer{};
+        prepared = rows <= 32 || T[i] != kQ6_K;
     }
     return JINF_HIP_OK;
 }

@@ -1084,7 +1084,13 @@ int mb_split(int n_groups, int n_slabs, int* slabs_per_split) {
 // sequences.
 MbShape mb_shape() { return kMbNarrow; }
 
-size_t mb_ctr_bytes(int n_groups) { return ((size_t)n_groups * 4 + 255) / 256 * 256; }
+// The counters' area: at least 16 KiB, so that the x records start at the
+// same offset for every matrix of up to 4096 row groups (262,144 rows) and one
+// preparation can serve several GEMVs of the same input.
+size_t mb_ctr_bytes(int n_groups) {
+    const size_t b = ((size_t)n_groups * 4 + 255) / 256 * 256;
+    return b > 16384 ? b : 16384;
+}
 
 // Workspace: the groups' counters, the x records, then the split partials.
 size_t mb_ws_bytes(const MbShape& sh, int epi, int out_rows, int n_slabs, int mt) {
@@ -1364,7 +1370,7 @@ int rmsnorm_qkv_rope_batch_m(const void* wq, const void* wk, const void* wv, int
                              int64_t ld_seq, const int32_t* positions, int max_ctx, int head_dim,
                              int n_heads, int n_heads_kv, float freq_base, int n_batch,
                              void* workspace, size_t workspace_bytes, const MbDefer* pend,
-                             float* part, size_t part_bytes, hipStream_t stream) {
+                             float* part, size_t part_bytes, bool x_ready, hipStream_t stream) {
     if (head_dim <= 0 || head_dim % 2 != 0 || head_dim / 2 > kRopeMaxHalf || n_heads < 0 ||
         n_heads_kv < 0 || !(freq_base > 0.0f) || !positions)
         return JINF_HIP_ERR_INVALID;
@@ -1408,6 +1414,10 @@ int rmsnorm_qkv_rope_batch_m(const void* wq, const void* wk, const void* wv, int
     j.ld_seq = ld_seq;
     RopeTheta th;
     theta_table(th, head_dim, freq_base);
+    // x prepared by the previous call on the same input (records at a fixed
+    // workspace offset, whole-row scales); not for Q6_K's two one-tile
+    // launches at more than 32 sequences, which prepare per launch
+    j.x_ready = x_ready && !(pend && pend->part) && (n_batch <= 32 || qtype != kQ6_K) ? 1 : 0;
     if (part && j.k_splits > 1) {
         // the column splits' merge and the epilogue in a launch of their own
         if (!aligned(part, 16) ||
@@ -1514,5 +1524,5 @@ extern "C" int jinf_rmsnorm_qkv_rope_batch(const void* wq, const void* wk, const
                                     norm_type, eps, n_embd, q, ld_q, k_cache, v_cache, kv_type,
                                     ld_seq, positions, max_ctx, head_dim, n_heads, n_heads_kv,
                                     freq_base, n_batch, workspace, workspace_bytes, nullptr,
-                                    nullptr, 0, stream);
+                                    nullptr, 0, false, stream);
 }

@@ -126,7 +126,8 @@ int matvec_batch_add_defer(const void* weight, int qtype, const float* x, int ld
 // for its rows, 16-byte aligned): when its columns are split, the splits'
 // partial sums go there and a launch of its own sums them and applies the
 // RoPE / cache-store epilogue, instead of the GEMV's last workgroup of each
-// row group.
+// row group.  x_ready (Q/K/V): the previous Q/K/V call of this layer, on the
+// same workspace and input, already prepared x (the preparation is skipped).
 int rmsnorm_matvec_batch_m(const void* weight, int qtype, float* h, int ld_h, const void* norm_w,
                            int norm_type, float eps, float* y, int ld_y, int rows, int cols,
                            int n_batch, void* workspace, size_t workspace_bytes,
@@ -141,6 +142,6 @@ int rmsnorm_qkv_rope_batch_m(const void* wq, const void* wk, const void* wv, int
                              int64_t ld_seq, const int32_t* positions, int max_ctx, int head_dim,
                              int n_heads, int n_heads_kv, float freq_base, int n_batch,
                              void* workspace, size_t workspace_bytes, const MbDefer* pend,
-                             float* part, size_t part_bytes, hipStream_t stream);
+                             float* part, size_t part_bytes, bool x_ready, hipStream_t stream);
 
 }  // namespace jinf
