@@ -27,8 +27,9 @@ namespace jinf {
 
 constexpr int kNormCPT = 4;  // 16-byte chunks per thread held in registers
 
-// E consecutive weight elements: raw bits loaded with the row (normal cached
-// loads: every row re-reads the weight), widened to fp32 after the reduction.
+// E consecutive weight elements: raw bits loaded with the row or during the
+// reduction's barrier (normal cached loads: every row re-reads the weight),
+// widened to fp32 after the reduction.
 template <typename TW, int E> struct WRaw {
     static constexpr int kWords = (E * (int)sizeof(TW) + 15) / 16;  // 16-byte words
     uint4 w[kWords];
@@ -68,8 +69,17 @@ __device__ __forceinline__ void wunpack(const WRaw<uint16_t, E>& r, float (&v)[E
 }
 
 // BS lanes (a template argument: with the block size known at compile time
-// the chunk offsets are immediates), CPT chunks per lane.
-template <typename TA, typename TW, bool FUSED, int BS, int CPT>
+// the chunk offsets are immediates), CPT chunks per lane.  WLATE issues the
+// weight loads after the row's sum of squares, while the workgroup waits at
+// its barrier: the weight is cache-resident (every row reads it), and keeping
+// it out of the row's load phase shortens the critical path when a few rows
+// each own a CU (64 rows of 8192: 3.40 -> 3.22 us measured, with CPT = 2).
+// EXACT: the row is exactly BS * CPT chunks, so no chunk needs a bounds test.
+// The tests put each chunk's loads inside a branch, after which the compiler
+// waits for every outstanding load before the first store (64 rows of 8192:
+// 3.93 us guarded against 3.22 us exact).
+template <typename TA, typename TW, bool FUSED, int BS, int CPT, bool WLATE = false,
+          bool EXACT = false>
 __global__ __launch_bounds__(BS) void rmsnorm_vec_kernel(
     TA* out, int ld_out, TA* res, int ld_res, const TA* in, int ld_in,
     const TW* __restrict__ w, int n, float eps) {
@@ -85,29 +95,30 @@ __global__ __launch_bounds__(BS) void rmsnorm_vec_kernel(
 
     // The row stays in registers in its storage format (16-byte chunks); every
     // load is issued before any store (out may alias in).
-    // The weight chunks are fetched with the row, so their latency is not
-    // paid again after the reduction.
+    // The weight chunks are fetched with the row (WLATE: while the workgroup
+    // waits at the reduction's barrier), so their latency is not paid again
+    // after the reduction.
     uint4 hv[CPT];
     uint4 dv[CPT];
     WRaw<TW, E> wr[CPT];
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
         const int c = threadIdx.x + j * bs;
-        if (c < nch) {
+        if (EXACT || c < nch) {
             if constexpr (FUSED) {
                 hv[j] = ld16<true>(r + (int64_t)c * E);
                 dv[j] = ld16<true>(x + (int64_t)c * E);
             } else {
                 hv[j] = ld16<true>(x + (int64_t)c * E);
             }
-            wload_raw<E>(w + c * E, wr[j]);
+            if constexpr (!WLATE) wload_raw<E>(w + c * E, wr[j]);
         }
     }
     double ss = 0.0;
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
         const int c = threadIdx.x + j * bs;
-        if (c < nch) {
+        if (EXACT || c < nch) {
             float h[E];
             A::unpack(hv[j], h);
             if constexpr (FUSED) {
@@ -126,6 +137,13 @@ __global__ __launch_bounds__(BS) void rmsnorm_vec_kernel(
     // DPP wave sums, one LDS exchange and one barrier (`red` is not reused)
     ss = wave_sum_f64(ss);
     if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
+    if constexpr (WLATE) {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int c = threadIdx.x + j * bs;
+            if (EXACT || c < nch) wload_raw<E>(w + c * E, wr[j]);
+        }
+    }
     __syncthreads();
     ss = red[0];
 #pragma unroll
@@ -135,7 +153,7 @@ __global__ __launch_bounds__(BS) void rmsnorm_vec_kernel(
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
         const int c = threadIdx.x + j * bs;
-        if (c < nch) {
+        if (EXACT || c < nch) {
             float h[E], wv[E], o[E];
             A::unpack(hv[j], h);
             wunpack<E>(wr[j], wv);
@@ -188,16 +206,44 @@ static int rmsnorm_launch(void* out, int ld_out, void* res, int ld_res, const vo
                      ((int64_t)ld_in * sizeof(TA)) % kVec == 0 &&
                      (!FUSED || (aligned(res, kVec) && ((int64_t)ld_res * sizeof(TA)) % kVec == 0));
     const int nch = n / E;
-    int bs = round_up((nch + kNormCPT - 1) / kNormCPT, kWave);
-    // Few rows cannot fill 256 CUs: spread each row over more lanes so the
-    // row's loads are all in flight at once.
-    if (n_rows < 1024) bs = bs > round_up(nch, kWave) ? bs : round_up(nch, kWave);
-    if (bs > 1024) bs = round_up((nch + kNormCPT - 1) / kNormCPT, kWave);
-    if (bs < kWave) bs = kWave;
     TA* o = static_cast<TA*>(out);
     TA* r = static_cast<TA*>(res);
     const TA* x = static_cast<const TA*>(in);
     const TW* wt = static_cast<const TW*>(w);
+    // Few rows cannot fill 256 CUs, so each row's workgroup owns a CU and the
+    // launch is latency-bound: two chunks per lane (all of a row's loads in
+    // flight at once, half the waves of one chunk per lane), the weight
+    // loaded late.  Measured at 64 rows of 8192 fp16: 1024 x 1 3.40 us,
+    // 512 x 2 3.22 us, 256 x 4 3.30 us (each with the weight loaded late).
+    // Splitting a row over several workgroups that exchange partial sums
+    // through device-coherent memory was slower at every split (4.3 us at 2
+    // workgroups per row, 10.4 us at 16): one exchange costs more than the
+    // shorter per-CU load phase saves.
+    if (vec && n_rows < 1024 && nch > 2 * kWave && nch <= 2 * 1024) {
+        int bp = kWave;
+        while (2 * bp < nch) bp *= 2;
+        auto go = [&](auto kern) {
+            return launch(kern, dim3(n_rows), dim3(bp), 0, stream, o, ld_out, r, ld_res, x,
+                          ld_in, wt, n, eps);
+        };
+        const bool ex = nch == 2 * bp;
+        switch (bp) {
+            case 128: return ex ? go(rmsnorm_vec_kernel<TA, TW, FUSED, 128, 2, true, true>)
+                                : go(rmsnorm_vec_kernel<TA, TW, FUSED, 128, 2, true>);
+            case 256: return ex ? go(rmsnorm_vec_kernel<TA, TW, FUSED, 256, 2, true, true>)
+                                : go(rmsnorm_vec_kernel<TA, TW, FUSED, 256, 2, true>);
+            case 512: return ex ? go(rmsnorm_vec_kernel<TA, TW, FUSED, 512, 2, true, true>)
+                                : go(rmsnorm_vec_kernel<TA, TW, FUSED, 512, 2, true>);
+            default: return ex ? go(rmsnorm_vec_kernel<TA, TW, FUSED, 1024, 2, true, true>)
+                               : go(rmsnorm_vec_kernel<TA, TW, FUSED, 1024, 2, true>);
+        }
+    }
+    int bs = round_up((nch + kNormCPT - 1) / kNormCPT, kWave);
+    // Few short rows: one chunk per lane, so the row's loads are all in
+    // flight at once.
+    if (n_rows < 1024) bs = bs > round_up(nch, kWave) ? bs : round_up(nch, kWave);
+    if (bs > 1024) bs = round_up((nch + kNormCPT - 1) / kNormCPT, kWave);
+    if (bs < kWave) bs = kWave;
     if (vec && bs <= 1024) {
         // block sizes rounded up to a power of two; one chunk per lane when
         // that covers the row, else kNormCPT
@@ -208,6 +254,8 @@ static int rmsnorm_launch(void* out, int ld_out, void* res, int ld_res, const vo
             return launch(kern, dim3(n_rows), dim3(bp), 0, stream, o, ld_out, r, ld_res, x,
                           ld_in, wt, n, eps);
         };
+        // (the guarded form: at 2048 rows of 4096 the exact, unguarded
+        // instantiation measured 12.9 us against 12.1)
         switch (bp) {
             case 64: return one ? go(rmsnorm_vec_kernel<TA, TW, FUSED, 64, 1>)
                                 : go(rmsnorm_vec_kernel<TA, TW, FUSED, 64, kNormCPT>);

@@ -69,7 +69,11 @@ def test_fixture_fused_fp16(dev):
     tu.assert_f16_close(host(y), g["frn_y"], 2, "fixture y")
 
 
-@pytest.mark.parametrize("rows,n", [(64, 8192), (1, 4096), (7, 4104), (300, 512)])
+# Few rows (< 1024) of more than 128 chunks take the two-chunks-per-lane form:
+# 8200 and 4104 leave the last lanes' second chunk (or both) past the row,
+# 16384 fp16 is its widest row (1024 lanes), 1032 its narrowest (128 lanes).
+@pytest.mark.parametrize("rows,n", [(64, 8192), (1, 4096), (7, 4104), (300, 512),
+                                    (64, 8200), (3, 16384), (2, 1032)])
 @pytest.mark.parametrize("act,wdt", [(np.float16, np.float16), (np.float16, np.float32),
                                      (np.float32, np.float32), (np.float32, np.float16)])
 def test_rows_plain_and_fused(dev, rows, n, act, wdt):
