@@ -192,9 +192,10 @@ def build_softmax(torch, jinf, g, n_seq, n_heads, max_len, keep):
     lens = pos + 1
     live = int(lens.sum().item())
     nbytes = 8 * n_heads * live + n_seq * 4
-    foot = n_seq * n_heads * max_len * 4 * 2
+    # sets are counted by the bytes a launch touches (the live prefixes), not
+    # by the padded rows: only touched lines can be left in the 256 MB cache
     sets, probes = [], []
-    for _ in range(n_sets(foot)):
+    for _ in range(n_sets(nbytes)):
         s = torch.randn((n_seq * n_heads, max_len), generator=g, device="cuda") * 3.0
         o = torch.empty_like(s)
         lc = lens.clone()
@@ -215,10 +216,9 @@ def build_attention(torch, jinf, g, name, n_seq, max_ctx, nh, nkv, hd, lens, kv_
     es = 2 if kv_dtype == torch.float16 else 4
     live = int(lens.sum().item())
     nbytes = 2 * live * nkv * hd * es + 2 * n_seq * nh * hd * 4 + n_seq * 4
-    foot = 2 * n_seq * max_ctx * nkv * hd * es
     n_past = int(lens[0].item())  # the drop-in takes the length on the host
     sets = []
-    for _ in range(max(2, n_sets(foot))):
+    for _ in range(n_sets(nbytes)):  # counted by touched bytes (live K/V rows)
         k = torch.randn((n_seq, max_ctx, nkv * hd), generator=g, device="cuda").to(kv_dtype)
         v = torch.randn((n_seq, max_ctx, nkv * hd), generator=g, device="cuda").to(kv_dtype)
         q = torch.randn((n_seq, nh * hd), generator=g, device="cuda") * 2.0

@@ -15,10 +15,10 @@
 // element, against the reference's three reads and two exp evaluations.
 // Every chunk's load is issued before any arithmetic, so a row's loads are in
 // flight together.  Max and sum are DPP wave reductions plus one LDS exchange
-// and one barrier each; each aligned group of 4 exponentials is summed in fp32
-// and the group sums in fp64.  Chunks past the row's live length do no
-// arithmetic (whole waves branch over them), so the VALU cost follows the live
-// length, not the padded stride.
+// and one barrier each; each lane's exponentials and then the wave's lanes are
+// summed in fp32, the per-wave sums in fp64.  Chunks past the row's live
+// length do no arithmetic (whole waves branch over them), so the VALU cost
+// follows the live length, not the padded stride.
 // Grid: (rows per length entry, length entries), so a workgroup finds its
 // length entry from blockIdx.y without an integer division (the earlier
 // 64-bit division sat on every row's critical path, ahead of its loads:
@@ -124,7 +124,11 @@ __global__ __launch_bounds__(BS) void softmax_vec_kernel(
         for (int i = 1; i < nw; ++i) m = fmaxf(m, redf[i]);
         mx = m;
     }
-    double sum = 0.0;
+    // Each lane's exponentials (at most 4 * CPT, all in (0, 1]) and the wave's
+    // lanes are summed in fp32, the wave sums in fp64: the sum's relative error
+    // stays below (4 * CPT + 6) * 2^-24 (2.3e-6 at 8 chunks), and fp32 lane
+    // sums measured 24.7 us against 24.9 us for fp64 lane sums at config 5.
+    float sum = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
         const int c = threadIdx.x + j * bs;
@@ -136,11 +140,11 @@ __global__ __launch_bounds__(BS) void softmax_vec_kernel(
                 v[j][e] = ex;
                 part += ex;
             }
-            sum += (double)part;
+            sum += part;
         }
     }
-    sum = wave_sum_f64(sum);
-    if (lane == 0) redd[wid] = sum;
+    sum = wave_sum_f32(sum);
+    if (lane == 0) redd[wid] = (double)sum;
     __syncthreads();
     double t = redd[0];
 #pragma unroll
