@@ -3,8 +3,8 @@ hidden 4096, 32 query / 8 KV heads of 128, FFN 14336 and a 128256-token
 vocabulary, in the two weight layouts bench.py times (Q4_0 with a Q6_K output
 head, and Q4_K_M: Q4_K with Q6_K for attn_v, ffn_down and the output), fp16
 KV cache, checked after each of 4 tokens against the oracle's decode loop
-(oracle/engine.py).  The batch decoder at the same widths: 5 and 40
-sequences (one and two 32-sequence tiles of the batched GEMVs, whose column
+(oracle/engine.py).  The batch decoder at the same widths, in both layouts: 5
+and 40 sequences (one and two 32-sequence tiles of the batched GEMVs, whose column
 splits are merged by separate launches and whose residual merges hand 2048-
 column slice statistics to the normalising preparation), a prompt through
 prefill, then decode steps, each sequence against its own oracle loop.
@@ -92,14 +92,19 @@ def test_llama3_8b_widths_match_oracle(dev, layout):
 STREAMS = [(128000, 9906, 1917), (128000, 40, 3), (5, 6, 7)]
 
 
+@pytest.mark.parametrize("layout", list(LAYOUTS))
 @pytest.mark.parametrize("n_seq", [5, 40])
-def test_llama3_8b_widths_batch_decode(dev, n_seq):
+def test_llama3_8b_widths_batch_decode(dev, n_seq, layout):
     """Sequence s decodes STREAMS[s % 3] after sequence 0 took a 6-token prompt
     through prefill; sequences of one stream must agree with that stream's
-    oracle loop (and so with each other), sequence 0 with its own."""
-    types, embd_type, out_type = LAYOUTS["q4_0"]
-    say(f"2-layer Llama-3-8B-wide model, q4_0, batch of {n_seq}, fp16 KV cache")
-    hp, W = wide_model(types, embd_type, out_type, seed=8192 + n_seq)
+    oracle loop (and so with each other), sequence 0 with its own.  The
+    Q4_K_M layout mixes formats within the Q/K/V projections (Q4_K q and k,
+    Q6_K v share one x preparation) and puts the 14336-column down projection
+    and the 128256-row output head in Q6_K; 40 sequences take the batched
+    GEMVs' second 32-sequence tile."""
+    types, embd_type, out_type = LAYOUTS[layout]
+    say(f"2-layer Llama-3-8B-wide model, {layout}, batch of {n_seq}, fp16 KV cache")
+    hp, W = wide_model(types, embd_type, out_type, seed=8192 + n_seq + 97 * len(layout))
     prompt = (128000, 791, 6864, 315, 9822, 374)
     refs = [oeng.Decoder(hp, W, max_context=16, kv_type=mu.F16) for _ in STREAMS]
     ref0 = oeng.Decoder(hp, W, max_context=16, kv_type=mu.F16)
