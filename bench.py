@@ -273,6 +273,110 @@ def build_matvec(torch, jinf, g, name, rows, cols, keep, qtype=2):
                   keep[-len(sets)][:2], lambda o, W, x: o.matvec(qtype, W, x))
 
 
+# --------------------------------------------------------------------------
+# geometry-free attainable rate: the fastest of many launch layouts of a plain
+# stream with a kernel's read:write mix, at the kernel's own size
+# --------------------------------------------------------------------------
+
+# mix -> (inputs, outputs, first output written in place of the first input)
+FLAT_MIXES = {"2:1": (2, 1, False), "2:1 in place": (2, 1, True),
+              "2:2 in place": (2, 2, True), "1:1 in place": (1, 1, True), "1:1": (1, 1, False)}
+KERNEL_MIX = {"rope": "1:1 in place", "residual_rmsnorm": "2:2 in place", "swiglu": "2:1",
+              "residual_add": "2:1 in place", "masked_softmax": "1:1", "q4_0_gather": "gather"}
+# (units per lane, cross-lane exchange, lanes per workgroup, workgroups: 0 = one
+# pass over the data, else a grid-stride loop over that many)
+FLAT_LAYOUTS = tuple((u, x, b, gr) for u in (1, 2, 4) for x in (True, False)
+                     for b, gr in ((64, 0), (128, 0), (256, 0), (512, 0), (1024, 0),
+                                   (256, 2048), (1024, 512)))
+GATHER_LAYOUTS = ((1, True), (2, True), (4, True), (1, False), (2, False), (4, False))
+
+
+def build_flat(torch, jinf, mix, nbytes, keep):
+    """Buffer sets of a plain stream of about `nbytes` algorithmic bytes with
+    read:write mix `mix` (rotated over >= 512 MiB of touched memory); its
+    probe variants are the launch layouts FLAT_LAYOUTS.  "gather" is the Q4_0
+    gather's row mix (2304-byte rows read : 8192-byte rows written)."""
+    if mix == "gather":
+        # every table row read once, in a random order (as random token ids
+        # read them), each into the next output row
+        ri, ro = 2304, 8192
+        n = max(1, nbytes // (ri + ro + 4))
+        probes = []
+        for _ in range(n_sets(n * (ri + ro))):
+            t = torch.ones((n, ri), dtype=torch.uint8, device="cuda")
+            o = torch.empty((n, ro), dtype=torch.uint8, device="cuda")
+            ids = torch.randperm(n, device="cuda").to(torch.int32)
+            keep.append((t, o, ids))
+            probes.append(lambda u, t=t, o=o, ids=ids:
+                          jinf.ops.probe_gather(o, t, ids, ri, *u))
+        k = Kernel("row gather", n * (ri + ro + 4), 0, "", [], "probe_gather_kernel",
+                   probes=probes, probe_name="probe_gather_kernel")
+        k.probe_upls = GATHER_LAYOUTS
+        return k
+    ni, no, inplace = FLAT_MIXES[mix]
+    n_units = max(1, nbytes // (16 * (ni + no)))
+    touched = 16 * n_units * (ni + no - (1 if inplace else 0))
+    probes = []
+    for _ in range(n_sets(touched)):
+        ins = [torch.ones(n_units * 4, dtype=torch.float32, device="cuda") for _ in range(ni)]
+        outs = [torch.empty(n_units * 4, dtype=torch.float32, device="cuda")
+                for _ in range(no - (1 if inplace else 0))]
+        if inplace:
+            outs.insert(0, ins[0])
+        keep.append((ins, outs))
+        probes.append(lambda lay, o0=outs[0], i0=ins[0], o1=outs[1] if no > 1 else None,
+                      i1=ins[1] if ni > 1 else None:
+                      jinf.ops.probe_stream_layout(o0, i0, o1, i1, *lay))
+    k = Kernel(f"flat {mix}", 16 * n_units * (ni + no), 0, "", [], "probe_flat_kernel",
+               probes=probes, probe_name="probe_flat_kernel")
+    k.probe_upls = FLAT_LAYOUTS
+    return k
+
+
+def attainable(torch, jinf, timed, mix, nbytes, n_launch):
+    """(us per launch scaled to nbytes, layout) of the fastest layout of a
+    plain stream with read:write mix `mix` moving about nbytes."""
+    scratch = []
+    fk = build_flat(torch, jinf, mix, nbytes, scratch)
+    torch.cuda.synchronize()
+    best = None
+    for lay in fk.probe_upls:
+        ms = timed(n_launch, [fk], probe=lay)
+        if best is None or ms < best[0]:
+            best = (ms, lay)
+    us = best[0] / n_launch * 1e3 * nbytes / fk.nbytes
+    del fk, scratch
+    torch.cuda.empty_cache()
+    return us, best[1]
+
+
+CURVE_MB = (2.0, 2.36, 3.15, 4.0, 4.21, 8.0, 10.49, 11.01, 16.0, 32.0, 43.01, 64.0, 67.12,
+            128.0, 136.49, 176.16, 256.0, 512.0)
+
+
+def stream_curve(torch, jinf, timed, n_launch):
+    """Text table: best attainable stream rate per read:write mix and size."""
+    lines = ["attainable HBM stream rate on one MI355X: the fastest of "
+             f"{len(FLAT_LAYOUTS)} launch layouts (flat mixes) or {len(GATHER_LAYOUTS)} "
+             "(row gather) per point, each timed over "
+             f"{n_launch} back-to-back launches in one HIP graph, buffer sets rotated over "
+             ">= 512 MiB of touched memory",
+             "layout = (units per lane, cross-lane exchange[, lanes per workgroup, "
+             "workgroups (0 = one pass, else grid-stride)])", ""]
+    for mix in list(FLAT_MIXES) + ["gather"]:
+        lines.append(f"mix {mix}:")
+        lines.append(f"  {'MB':>8} {'us':>9} {'GB/s':>8} {'% of 8 TB/s':>12}  layout")
+        for mb in CURVE_MB:
+            nb = int(mb * 1e6)
+            us, lay = attainable(torch, jinf, timed, mix, nb, n_launch)
+            gbs = nb / (us * 1e-6) / 1e9
+            lines.append(f"  {mb:8.2f} {us:9.3f} {gbs:8.1f} {100 * gbs / PEAK_GBS:11.1f}%  "
+                         f"{lay}")
+            log(f"curve {mix} {mb} MB: {us:.3f} us")
+        lines.append("")
+    return "\n".join(lines)
+
+
 def config5(torch, jinf, g, keep):
     """the Llama-3-70B decode chain for 64 sequences."""
     pos = torch.randint(0, 8192, (64,), generator=g, device="cuda", dtype=torch.int32)
@@ -580,6 +684,69 @@ def batch_bench(args, torch, jinf_amd, spec):
         "cpu_baseline": cpu,
     }
     print(json.dumps(out_line), flush=True)
+
+
+def f4_figures(args, torch, jinf_amd):
+    """The engine rows (f1 GEMVs, f2 attention, f4 loop) on the Q4_0
+    Llama-3-8B-shaped model of `--workload llama3-8b-decode`, measured inside
+    the default run: batch-1 decode (K tokens in one forward call, one
+    captured graph per token) and the 32-sequence batched decode (K steps of
+    jinf_hip_batch_generate).  Weight GB/s = weight bytes read per step / step
+    time; the KV-cache rows read are reported beside it."""
+    from jinf_amd.engine import Batch, Engine
+
+    spec = ENGINE_MODELS["llama3-8b-decode"]
+    hp = dict(LLAMA3_8B)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(args.seed)
+    W = engine_weights(torch, g, spec, hp)
+    torch.cuda.synchronize()
+    kvd = hp["n_heads_kv"] * hp["n_embd"] // hp["n_heads"]
+    erow = weight_row_bytes(spec["embd"], hp["n_embd"])
+    steps = max(8, min(args.steps, 32))
+    out = {"model": "Llama-3-8B-shaped, 32 layers, " + spec["desc"] + ", f16 KV cache, random "
+                    "weights (--workload llama3-8b-decode / llama3-8b-decode-batch)",
+           "steps_timed": steps}
+    with Engine(hp, W, 1024, jinf_amd.F16) as e:
+        e.use_graph(not args.no_graph)
+        wbytes = e.step_weight_bytes
+        e.forward(PROMPT)
+        e.forward([PROMPT[-1]] * 2)
+        toks = [int(t) for t in torch.randint(0, hp["n_vocab"], (steps,), generator=g,
+                                              device="cuda").cpu()]
+        start = e.n_past
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e.forward(toks)
+        ms = (time.perf_counter() - t0) / steps * 1e3
+        kv = 2 * hp["n_layers"] * kvd * 2 * (start + (steps + 1) / 2)
+        out["batch1"] = {"ms_per_token": round(ms, 4), "tokens_per_s": round(1e3 / ms, 1),
+                         "weight_bytes": wbytes, "kv_bytes_mean": int(kv),
+                         "weight_GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                         "frac_of_8TBs": round((wbytes + kv) / (ms * 1e-3) / 1e9 / PEAK_GBS, 4),
+                         "context": [start, start + steps]}
+        n_seq = 32
+        with Batch(e, n_seq, 256, jinf_amd.F16) as b:
+            b.use_graph(not args.no_graph)
+            for tok in PROMPT:
+                b.forward([tok] * n_seq)
+            b.generate(2)
+            start = b.n_past(0)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            b.generate(steps)
+            ms = (time.perf_counter() - t0) / steps * 1e3
+            wb = wbytes - erow + n_seq * erow
+            kv = n_seq * 2 * hp["n_layers"] * kvd * 2 * (start + (steps + 1) / 2)
+            out["batch32"] = {"ms_per_step": round(ms, 4),
+                              "tokens_per_s": round(n_seq * 1e3 / ms, 1),
+                              "weight_bytes": wb, "kv_bytes_mean": int(kv),
+                              "weight_GB/s": round(wb / (ms * 1e-3) / 1e9, 1),
+                              "frac_of_8TBs": round((wb + kv) / (ms * 1e-3) / 1e9 / PEAK_GBS, 4),
+                              "context": [start, start + steps]}
+    del W
+    torch.cuda.empty_cache()
+    return out
 
 
 def weight_row_bytes(qtype, n):
@@ -1011,6 +1178,12 @@ def main():
     ap.add_argument("--per-step", type=int, default=0, metavar="STEPS",
                     help="with --rocprof-summary: also every kernel's time per step, the run "
                          "holding STEPS steps")
+    ap.add_argument("--no-f4", action="store_true",
+                    help="default workload: skip the engine figures (batch-1 and batch-32 "
+                         "decode of the Q4_0 Llama-3-8B-shaped model)")
+    ap.add_argument("--stream-curve", action="store_true",
+                    help="print the geometry-free attainable stream rate per read:write mix "
+                         "over transfer sizes 2-512 MB (a text table) and exit")
     args = ap.parse_args()
 
     if args.rocprof_summary:
@@ -1036,28 +1209,6 @@ def main():
 
     jinf_amd.lib()
     torch.cuda.set_device(0)
-    log(f"{jinf_amd.version()} on {torch.cuda.get_device_name(0)}; workload {args.workload}")
-    if args.workload in ENGINE_MODELS:
-        engine_bench(args, torch, jinf_amd)
-        return
-    ks, cfg, keep = workload(args.workload, torch, jinf_amd, args.seed)
-    # the default run also measures config 5 (the 70B decode chain)
-    ks70 = []
-    if args.workload == "llama3-8b-layer" and not args.no_config5:
-        g70 = torch.Generator(device="cuda")
-        g70.manual_seed(args.seed)  # the same draw as --workload llama3-70b-decode
-        ks70, cfg70 = config5(torch, jinf_amd, g70, keep)
-    torch.cuda.synchronize()
-    log("buffers ready: " + ", ".join(f"{k.name} x{len(k.launches)} sets"
-                                      for k in ks + ks70))
-
-    for _ in range(args.warmup):
-        for k in ks + ks70:
-            k.run()
-            if k.probes and args.workload != "calibrate" and not args.no_ceilings:
-                for u in k.probe_upls:
-                    k.run(probe=u)
-    torch.cuda.synchronize()
 
     # The K timed steps are captured into one HIP graph and replayed once: the
     # GPU then runs the kernels back to back, as an engine's captured decode
@@ -1089,6 +1240,33 @@ def main():
         torch.cuda.synchronize()
         return start.elapsed_time(end)
 
+    log(f"{jinf_amd.version()} on {torch.cuda.get_device_name(0)}; workload {args.workload}")
+    if args.stream_curve:
+        print(stream_curve(torch, jinf_amd, timed, max(args.steps, args.kernel_launches)),
+              flush=True)
+        return
+    if args.workload in ENGINE_MODELS:
+        engine_bench(args, torch, jinf_amd)
+        return
+    ks, cfg, keep = workload(args.workload, torch, jinf_amd, args.seed)
+    # the default run also measures config 5 (the 70B decode chain)
+    ks70 = []
+    if args.workload == "llama3-8b-layer" and not args.no_config5:
+        g70 = torch.Generator(device="cuda")
+        g70.manual_seed(args.seed)  # the same draw as --workload llama3-70b-decode
+        ks70, cfg70 = config5(torch, jinf_amd, g70, keep)
+    torch.cuda.synchronize()
+    log("buffers ready: " + ", ".join(f"{k.name} x{len(k.launches)} sets"
+                                      for k in ks + ks70))
+
+    for _ in range(args.warmup):
+        for k in ks + ks70:
+            k.run()
+            if k.probes and args.workload != "calibrate" and not args.no_ceilings:
+                for u in k.probe_upls:
+                    k.run(probe=u)
+    torch.cuda.synchronize()
+
     t0 = time.perf_counter()
     total_ms = timed(args.steps, ks)
     wall = time.perf_counter() - t0
@@ -1105,6 +1283,13 @@ def main():
                 ms = timed(n_launch, [k], probe=u)
                 if k.ceil_ms is None or ms < k.ceil_ms:
                     k.ceil_ms, k.ceil_upl = ms, u
+    # the geometry-free attainable rate of each kernel's mix at its size (after
+    # every kernel is timed: these allocate and free their own buffer sets)
+    if args.workload != "calibrate" and not args.no_ceilings:
+        for k in ks + ks70:
+            if k.probes and k.name in KERNEL_MIX:
+                k.att_us, k.att_lay = attainable(torch, jinf_amd, timed, KERNEL_MIX[k.name],
+                                                 k.nbytes, n_launch)
     ms_step = total_ms / args.steps
     step_bytes = sum(k.nbytes for k in ks)
     kern_ms = sum(k.ms / k.n for k in ks)
@@ -1118,12 +1303,22 @@ def main():
                  "rows_per_s": round(k.rows / (us * 1e-6), 1), "row_unit": k.row_unit,
                  "bytes": k.nbytes, "sets": len(k.launches), "launches_timed": k.n}
             if k.ceil_ms is not None:
-                cus = k.ceil_ms / k.n * 1e3
+                # ceiling: the faster of the probe in the kernel's own geometry
+                # and the geometry-free attainable stream of its mix and size
+                pus = k.ceil_ms / k.n * 1e3
+                cus = pus
+                e.update({"probe_us": round(pus, 3), "probe_frac": round(pus / us, 4),
+                          "ceiling_probe": k.probe_name, "ceiling_units_per_lane": k.ceil_upl[0],
+                          "ceiling_exchange": k.ceil_upl[1]})
+                if getattr(k, "att_us", None) is not None:
+                    cus = min(pus, k.att_us)
+                    e.update({"attainable_us": round(k.att_us, 3),
+                              "attainable_frac": round(k.att_us / us, 4),
+                              "attainable_mix": KERNEL_MIX[k.name],
+                              "attainable_layout": list(k.att_lay)})
                 e.update({"ceiling_us": round(cus, 3),
                           "ceiling_GB/s": round(k.nbytes / (cus * 1e-6) / 1e9, 1),
-                          "frac_of_ceiling": round(cus / us, 4), "ceiling_probe": k.probe_name,
-                          "ceiling_units_per_lane": k.ceil_upl[0],
-                          "ceiling_exchange": k.ceil_upl[1]})
+                          "frac_of_ceiling": round(cus / us, 4)})
             t = traffic_from_profiles({"residual_add": "residual_add_f16"}.get(k.name, k.name),
                                       workload)
             if t is not None:
@@ -1153,6 +1348,7 @@ def main():
     if args.calibrate_copy:
         calibrate_copy(torch)
 
+
     cpu = None
     if args.cpu_seconds > 0 and args.workload != "calibrate":
         try:
@@ -1160,6 +1356,16 @@ def main():
         except Exception as exc:  # the baseline is reported, never required
             log(f"cpu baseline failed: {exc!r}")
             cpu = None
+
+    # the engine rows, timed after the kernels (their buffers stay resident:
+    # 288 GB of HBM holds both)
+    f4 = None
+    if args.workload == "llama3-8b-layer" and not args.no_f4:
+        t0 = time.perf_counter()
+        f4 = f4_figures(args, torch, jinf_amd)
+        log(f"engine figures in {time.perf_counter() - t0:.1f} s: batch 1 "
+            f"{f4['batch1']['ms_per_token']} ms/token, batch 32 "
+            f"{f4['batch32']['ms_per_step']} ms/step")
 
     out = {
         "metric": METRIC,
@@ -1178,6 +1384,7 @@ def main():
         "wall_s_timed": round(wall, 4),
         "kernels": per,
         "config5": c5,
+        "f4": f4,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

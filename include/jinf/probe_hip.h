@@ -40,6 +40,15 @@ int jinf_probe_rows_inplace(void* a, int64_t ld_a, int units_a, void* b, int64_t
 int jinf_probe_stream(void* out0, void* out1, const void* in0, const void* in1,
                       int64_t n_units, int units_per_lane, int exchange, hipStream_t stream);
 
+/* Flat streams as jinf_probe_stream, in a chosen launch layout (for the
+ * geometry-free bandwidth curve): block_lanes (64, 128, 256, 512 or 1024)
+ * lanes of units_per_lane units per workgroup; max_groups 0 launches one pass
+ * over enough workgroups to cover n_units, max_groups > 0 caps the grid at
+ * that many workgroups, which loop over the units with a grid stride. */
+int jinf_probe_stream_layout(void* out0, void* out1, const void* in0, const void* in1,
+                             int64_t n_units, int units_per_lane, int exchange,
+                             int block_lanes, int max_groups, hipStream_t stream);
+
 /* Row gather (the Q4_0 embedding gather's geometry): output row r
  * (ld_out bytes apart, out_units units) is written from table row ids[r]
  * (row r when ids is NULL; ld_table bytes apart, in_units <= out_units units,

@@ -9,8 +9,10 @@
 // accesses.  Consecutive lanes touch consecutive 16-byte chunks, so each wave
 // instruction moves 1 KiB of contiguous bytes.  Contiguous tensors are
 // flattened to one row, making the grid one long 1-D sweep.  Measured on
-// MI355X at [2048, 14336] fp16, one chunk per thread in 256-lane workgroups
-// (many small workgroups) beats 2-4 chunks per thread: 28.7 us vs 29.8 / 30.6.
+// MI355X at [2048, 14336] fp16, one chunk per thread beats 2-4 chunks per
+// thread (28.7 us vs 29.8 / 30.6 in 256-lane workgroups), and one-wave
+// workgroups beat 256 lanes: a plain stream of the same 2:1 mix takes 27.6 us
+// with 64-lane workgroups, the fastest of 30 launch layouts.
 //
 // Arithmetic:
 //   fp32 storage (the drop-in's precision) uses accurate expf and an IEEE
@@ -32,7 +34,7 @@
 
 namespace jinf {
 
-constexpr int kEwBlock = 256;
+constexpr int kEwBlock = 64;
 constexpr int kEwUnroll = 1;
 
 enum EwOp { kSwigluExact = 0, kSwigluFast = 1, kAdd = 2 };

@@ -96,6 +96,45 @@ __global__ __launch_bounds__(kProbeStreamBlock) void probe_stream_kernel(
     }
 }
 
+// Flat streams in any of several launch layouts (the geometry-free curve):
+// BS lanes of U units per workgroup, either one pass over a grid that covers
+// the units or a grid-stride loop over a capped number of workgroups.  Unit i
+// of every input is read and unit i of every output written by one lane.
+template <int U, bool X, int BS>
+__global__ __launch_bounds__(BS) void probe_flat_kernel(uint8_t* out0, uint8_t* out1,
+                                                       const uint8_t* in0, const uint8_t* in1,
+                                                       int64_t n_units) {
+    const int64_t step = (int64_t)gridDim.x * BS * U;
+    for (int64_t i0 = (int64_t)blockIdx.x * BS * U + threadIdx.x; i0 - threadIdx.x < n_units;
+         i0 += step) {
+        uint4 v0[U], v1[U];
+        uint32_t acc = 0;
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const int64_t i = i0 + (int64_t)BS * j;
+            v0[j] = make_uint4(0, 0, 0, 0);
+            v1[j] = make_uint4(0, 0, 0, 0);
+            if (i < n_units) {
+                v0[j] = ld16<true>(in0 + i * 16);
+                if (in1) v1[j] = ld16<true>(in1 + i * 16);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < U; ++j) acc ^= v0[j].y ^ v1[j].z;
+        const uint32_t z = X ? wave_token(acc) : (acc & 1u);
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const int64_t i = i0 + (int64_t)BS * j;
+            if (i < n_units) {
+                v0[j].x ^= z;
+                v1[j].x ^= z;
+                st16<true>(out0 + i * 16, v0[j]);
+                if (out1) st16<true>(out1 + i * 16, v1[j]);
+            }
+        }
+    }
+}
+
 // Gather geometry: grid (ids, ceil(out_units / (256 U))), 256 lanes of U
 // output units; output unit u of row r is written from unit about
 // u * in_units / out_units of table row ids[r] (in_units <= out_units), so
@@ -230,6 +269,45 @@ extern "C" int jinf_probe_stream(void* out0, void* out1, const void* in0, const 
                       : U == 2 ? go(probe_stream_kernel<2, true>) : go(probe_stream_kernel<4, true>);
     return U == 1 ? go(probe_stream_kernel<1, false>)
                   : U == 2 ? go(probe_stream_kernel<2, false>) : go(probe_stream_kernel<4, false>);
+}
+
+extern "C" int jinf_probe_stream_layout(void* out0, void* out1, const void* in0,
+                                        const void* in1, int64_t n_units, int units_per_lane,
+                                        int exchange, int block_lanes, int max_groups,
+                                        hipStream_t stream) {
+    using namespace jinf;
+    const int U = units_per_lane;
+    const int B = block_lanes;
+    if (n_units < 0 || (U != 1 && U != 2 && U != 4) || max_groups < 0 ||
+        (B != 64 && B != 128 && B != 256 && B != 512 && B != 1024))
+        return JINF_HIP_ERR_INVALID;
+    if (n_units == 0) return JINF_HIP_OK;
+    if (!out0 || !in0 || !al16(out0) || !al16(in0) || (out1 && !al16(out1)) ||
+        (in1 && !al16(in1)))
+        return JINF_HIP_ERR_INVALID;
+    int64_t gx = (n_units + (int64_t)B * U - 1) / ((int64_t)B * U);
+    if (max_groups > 0 && gx > max_groups) gx = max_groups;
+    if (gx > 0x7FFFFFFF) return JINF_HIP_ERR_INVALID;
+    auto go = [&](auto kern) {
+        return launch(kern, dim3((unsigned)gx), dim3(B), 0, stream, static_cast<uint8_t*>(out0),
+                      static_cast<uint8_t*>(out1), static_cast<const uint8_t*>(in0),
+                      static_cast<const uint8_t*>(in1), n_units);
+    };
+#define JINF_PROBE_FLAT(BS)                                                                 \
+    (exchange ? (U == 1 ? go(probe_flat_kernel<1, true, BS>)                                \
+                        : U == 2 ? go(probe_flat_kernel<2, true, BS>)                       \
+                                 : go(probe_flat_kernel<4, true, BS>))                      \
+              : (U == 1 ? go(probe_flat_kernel<1, false, BS>)                               \
+                        : U == 2 ? go(probe_flat_kernel<2, false, BS>)                      \
+                                 : go(probe_flat_kernel<4, false, BS>)))
+    switch (B) {
+        case 64: return JINF_PROBE_FLAT(64);
+        case 128: return JINF_PROBE_FLAT(128);
+        case 256: return JINF_PROBE_FLAT(256);
+        case 512: return JINF_PROBE_FLAT(512);
+        default: return JINF_PROBE_FLAT(1024);
+    }
+#undef JINF_PROBE_FLAT
 }
 
 extern "C" int jinf_probe_gather(void* out, int64_t ld_out, int out_units, const void* table,

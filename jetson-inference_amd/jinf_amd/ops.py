@@ -470,6 +470,17 @@ def probe_stream(out0, in0, out1=None, in1=None, units_per_lane=1, exchange=True
            "jinf_probe_stream")
 
 
+def probe_stream_layout(out0, in0, out1=None, in1=None, units_per_lane=1, exchange=True,
+                        block_lanes=256, max_groups=0):
+    """probe_stream in a chosen launch layout: block_lanes lanes per workgroup,
+    one pass (max_groups 0) or a grid-stride loop over max_groups workgroups."""
+    nbytes = out0.numel() * out0.element_size()
+    _check(lib().jinf_probe_stream_layout(_ptr(out0), _ptr(out1), _ptr(in0), _ptr(in1),
+                                          nbytes // 16, int(units_per_lane), int(bool(exchange)),
+                                          int(block_lanes), int(max_groups), _stream()),
+           "jinf_probe_stream_layout")
+
+
 def probe_gather(out, table, ids, in_row_bytes, units_per_lane=1, exchange=True):
     """The gather's traffic: out row r from table row ids[r] (table viewed as
     byte rows; in_row_bytes of each row read)."""
