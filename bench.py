@@ -910,6 +910,14 @@ def host_threads(args):
     return (args.cpu_threads or min(16, aff)), aff
 
 
+def oracle_build():
+    """The -march of the oracle library this host loads."""
+    sys.path.insert(0, ROOT)
+    import oracle
+
+    return "-march=x86-64-v4" if oracle.ORACLE_PATH.endswith("_v4.so") else "-march=x86-64-v3"
+
+
 def cpu_baseline_both(ks, ks70, args):
     """The oracle timed at 1 thread (the reference's CPU code is
     single-threaded) and at every core this run may use (at most 16, the GPU
@@ -936,8 +944,8 @@ def cpu_baseline_both(ks, ks70, args):
            "cpu_model": cpu_model(), "cpu_info": cpu_info(),
            "sample": (f"every kernel of the step (configs 2-4) and of config 5 at full shape on "
                       f"a host copy of buffer set 0; median of >= 3 runs after a warm-up, about "
-                      f"{budget:.0f} s per thread count; oracle C restatement (-O3 -march="
-                      f"x86-64-v3, no FMA contraction, no fast-math), 1 thread and {n_all} "
+                      f"{budget:.0f} s per thread count; oracle C restatement ({oracle_build()}, "
+                      f"-O3, no FMA contraction, no fast-math), 1 thread and {n_all} "
                       f"OpenMP threads")}
     if ks70:
         c1, _ = rate(ks70, 1)

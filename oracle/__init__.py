@@ -16,7 +16,25 @@ import os
 import numpy as np
 
 _DIR = os.path.dirname(os.path.abspath(__file__))
-ORACLE_PATH = os.path.join(_DIR, "libjinf_oracle.so")
+
+
+def _has_avx512():
+    """x86-64-v4's AVX-512 subsets (F, BW, CD, DQ, VL) on this host."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    fl = set(line.split(":", 1)[1].split())
+                    return {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"} <= fl
+    except OSError:
+        pass
+    return False
+
+
+# the AVX-512 build where the host has it and it was built, else the AVX2 one
+ORACLE_PATH = os.path.join(_DIR, "libjinf_oracle_v4.so")
+if not (_has_avx512() and os.path.exists(ORACLE_PATH)):
+    ORACLE_PATH = os.path.join(_DIR, "libjinf_oracle.so")
 REF_PATH = os.path.join(_DIR, "_ref", "libjinf_ref.so")
 
 F32, F16 = 0, 1
