@@ -1,10 +1,14 @@
 /* jinf's engine API under the reference's own names, for callers written
  * against it (e.g. the reference's bench/inference_bench.cpp:53-140): the
- * same entry points, argument meanings and ABI as include/jinf/engine.h:
- * 12-47 and :159-176 of the reference, over the resident-weight engine of
- * engine_hip.h.  Status returns are the reference's jinf_status values (an
- * int-sized enum there, int here: the same ABI), 0 OK, 1 I/O, 2 parse,
- * 3 device, 4 out of memory, 5 invalid.
+ * same entry points, argument meanings and struct layouts as
+ * include/jinf/engine.h:12-47 and :159-176 of the reference, over the
+ * resident-weight engine of engine_hip.h.  Linkage differs: the reference
+ * declares these functions with C++ linkage (mangled names), this library
+ * exports them extern "C", so a caller compiles against this header or a
+ * stand-in engine.h that declares them extern "C" (INTEGRATION.md shows one),
+ * not against the reference's engine.h unchanged.  Status returns are the
+ * reference's jinf_status values (an int-sized enum there, int here), 0 OK,
+ * 1 I/O, 2 parse, 3 device, 4 out of memory, 5 invalid.
  *
  * config->model_path names a .nvmw file (as in the reference); every tensor is
  * uploaded into device memory, so the streaming settings (gpu_memory_budget,

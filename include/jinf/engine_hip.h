@@ -152,10 +152,12 @@ uint64_t jinf_hip_engine_step_weight_bytes(const jinf_hip_engine* e);
 
 /* Performance counters, the reference's jinf_perf_stats
  * (include/jinf/engine.h:14-22) field for field: total_ms is the host wall
- * time spent in forward / prefill / generate calls (each waits for its
- * work), tokens_generated the tokens they ran through the model (prompt and
- * fed-back tokens, as the reference's forward counts them,
- * src/engine.cpp:756-757).  The streaming and per-phase fields stay zero, as
+ * time spent running tokens through the model (each forward / prefill call,
+ * and in generate each fed-back token's step up to its completion, as the
+ * reference's generate counts only its forward calls; the argmax reads
+ * between steps are not counted), tokens_generated the tokens run through
+ * the model (prompt and fed-back tokens, as the reference's forward counts
+ * them, src/engine.cpp:756-757).  The streaming and per-phase fields stay zero, as
  * the reference leaves them on its resident path.  Reset clears them. */
 typedef struct jinf_hip_perf_stats {
     double total_ms;

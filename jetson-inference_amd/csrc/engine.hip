@@ -823,7 +823,6 @@ extern "C" int jinf_hip_engine_generate(jinf_hip_engine* e, const int32_t* promp
     int32_t* best = e->h_tokens + e->d.max_context + 1;
     int generated = 0;
     e->bound = bound_for(e->n_past + (max_tokens > 0 ? max_tokens : 0), e->d.max_context);
-    PerfScope perf(e);  // the prompt's forward call counts itself
     for (int i = 0; i < max_tokens; ++i) {
         // the argmax of the last step (already the token at position n_past)
         ENG_TRY(hip_ok(hipMemcpyAsync(best, e->state + kBest, 4, hipMemcpyDeviceToHost,
@@ -835,9 +834,14 @@ extern "C" int jinf_hip_engine_generate(jinf_hip_engine* e, const int32_t* promp
         // feeding the token back would overrun the cache: stop, as the
         // reference does when its forward call fails (src/engine.cpp:800-801)
         if (e->n_past >= e->d.max_context) break;
+        // the counters take each fed-back token's step up to its completion,
+        // as the reference's forward call per token counts itself
+        // (src/engine.cpp:753-757); the argmax read above stays outside
+        PerfScope perf(e);
         if (step(e) != JINF_HIP_OK) break;
+        if (hipStreamSynchronize(e->stream) != hipSuccess) break;
         ++e->n_past;
-        ++perf.tokens;
+        perf.tokens = 1;
     }
     *n_generated = generated;
     return hip_ok(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
