@@ -302,11 +302,15 @@ size_t jinf_attention_workspace_bytes(int n_seq, int n_heads, int head_dim, int 
  * the process ends.  Nothing is allocated or freed by the call.
  *   - The first call on a device looks the scratch up (hipGetSymbolAddress)
  *     with that device current; make each call with the stream's device
- *     current.
- *   - A shape whose split needs more than the scratch holds (records of
+ *     current.  A caller that captures the call in a graph makes one call on
+ *     the device before capturing (a call with n_seq 0 does the lookup and
+ *     enqueues nothing); the captured call then records only kernel nodes
+ *     (its counters are cleared by a kernel, not a memset node).
+ *   - A shape whose split would need more than the scratch holds (records of
  *     n_seq * n_heads * chunks * (head_dim + 2) floats above 8 MiB, e.g.
- *     127 sequences x 64 heads over 8192 positions) returns
- *     JINF_HIP_ERR_INVALID with a stderr line and enqueues nothing.
+ *     127 sequences x 64 heads over 8192 positions) runs its contexts
+ *     unsplit, as jinf_attention_decode does with too small a workspace, and
+ *     gives that call's bits.
  *   - Every call on one device shares that device's scratch (each clears the
  *     counters it uses first): calls that may run at the same time on one
  *     device, on different streams, race and must not be issued. */

@@ -806,8 +806,8 @@ static size_t am_workspace_bytes(int n_seq, int n_heads, int head_dim, int max_c
 //     above and used only when it holds am_workspace_bytes for the call;
 //   fixed == true: this device's copy of `scratch` (below), with a fixed
 //     layout: kScratchCounterBytes of merge counters, then
-//     kScratchRecordBytes of records.  A call whose split needs more is
-//     rejected.
+//     kScratchRecordBytes of records.  A call whose split needs more runs
+//     unsplit.
 struct AmScratch {
     void* base;
     size_t bytes;
@@ -849,6 +849,18 @@ static int am_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, c
                  ((n_past + ch - 1) / ch * 16 + 8) * sizeof(float) <= shmem;
     if (split && !sc.fixed && sc.bytes < am_workspace_bytes(n_seq, n_heads, HD, n_past))
         split = false;
+    // The fixed scratch: a split whose records or in-launch merge counters do
+    // not fit runs unsplit, as a call with too small a workspace does (such a
+    // split has about as many (sequence, head group) pairs as work items to
+    // aim for, so the unsplit launch still fills the GPU).
+    if (split && sc.fixed) {
+        const size_t need = (size_t)n_seq * n_heads * ((n_past + ch - 1) / ch) * (HD + 2) *
+                            sizeof(float);
+        const bool ink = (int64_t)n_seq * (n_heads / G) < kAmInKernelMerge;
+        if (need > kScratchRecordBytes ||
+            (ink && (size_t)n_seq * n_heads * sizeof(unsigned) > kScratchCounterBytes))
+            split = false;
+    }
     const int chunk = split ? (int)ch : (n_past > 0 ? n_past : 1);
     const int nch = split ? (n_past + chunk - 1) / chunk : 1;
     // Few (sequence, head group) pairs: the last workgroup of each merges in
@@ -860,15 +872,7 @@ static int am_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, c
     unsigned* counters = nullptr;
     float* ws = nullptr;
     if (split && sc.fixed) {
-        const size_t need = (size_t)n_seq * n_heads * nch * (HD + 2) * sizeof(float);
-        const size_t slots = (size_t)n_seq * n_heads;
-        if (need > kScratchRecordBytes || (in_kernel && slots * 4 > kScratchCounterBytes)) {
-            JINF_LOG("jinf_attention_decode_noalloc: this shape splits its contexts into %d "
-                     "chunks and needs %zu bytes of records (at most %zu) and %zu merge counters "
-                     "(at most %zu); nothing was enqueued", nch, need, kScratchRecordBytes,
-                     in_kernel ? slots : (size_t)0, kScratchCounterBytes / 4);
-            return JINF_HIP_ERR_INVALID;
-        }
+        const size_t slots = (size_t)n_seq * n_heads;  // fits: checked above
         counters = in_kernel ? static_cast<unsigned*>(sc.base) : nullptr;
         ws = reinterpret_cast<float*>(static_cast<uint8_t*>(sc.base) + kScratchCounterBytes);
         if (counters) {

@@ -7,8 +7,11 @@ case makes two calls in a row into the shared per-device scratch, the second
 with a smaller input, so the second call runs on the first call's leftover
 records and counters.  The cases cover the in-launch merge (few sequence /
 head-group pairs), the separate merge launch (many pairs), unsplit contexts
-(no scratch use), and a shape whose split needs more records than the
-scratch holds, which is rejected on the host with nothing enqueued.
+(no scratch use), a shape whose split would need more records than the
+scratch holds (it runs unsplit: the workspace entry point's bits without a
+workspace), and the call captured in a HIP graph and replayed three times,
+with eager work between the replays, each replay against the workspace entry
+point's bits.
 """
 import numpy as np
 import pytest
@@ -83,16 +86,55 @@ def test_noalloc_fp32_cache_needs_no_scratch(dev):
     assert tu.bits_equal(host(out), want)
 
 
-def test_noalloc_rejects_a_split_beyond_the_scratch(dev):
+def test_noalloc_runs_unsplit_beyond_the_scratch(dev):
     # 127 sequences x 8 head groups = 1016 pairs over 8192 positions: chunks
     # of 8128 positions (8192 * 1016 / 1024 items), so two per sequence, and
     # 127 * 64 * 2 * 130 * 4 = 8,453,120 bytes of records > 8 MiB
-    # (8,388,608).  The call is rejected before any launch.
-    say("127 x 8192 x 64/8 x 128: split needs more than the scratch")
+    # (8,388,608): the call runs unsplit, as the workspace entry point does
+    # without a workspace, and gives its bits.
+    say("127 x 8192 x 64/8 x 128: split would need more than the scratch; unsplit")
     n_seq, max_ctx, nh, nkv, hd = 127, 8192, 64, 8, 128
-    k = torch.zeros((n_seq, max_ctx, nkv * hd), dtype=torch.float16, device=dev)
-    q = torch.zeros((n_seq, nh * hd), dtype=torch.float32, device=dev)
-    lens = torch.full((n_seq,), max_ctx, dtype=torch.int32, device=dev)
-    out = torch.full((n_seq, nh * hd), 7.0, dtype=torch.float32, device=dev)
-    assert _noalloc(out, q, k, k, lens, nh, nkv) == jinf_amd._lib.JINF_HIP_ERR_INVALID
-    assert bool((out == 7.0).all())
+    g = torch.Generator(device=dev)
+    g.manual_seed(127)
+    k = torch.randn((n_seq, max_ctx, nkv * hd), generator=g, device=dev, dtype=torch.float16)
+    v = torch.randn((n_seq, max_ctx, nkv * hd), generator=g, device=dev, dtype=torch.float16)
+    q = torch.randn((n_seq, nh * hd), generator=g, device=dev) * 2.0
+    lens = torch.randint(1, max_ctx + 1, (n_seq,), generator=g, device=dev, dtype=torch.int32)
+    lens[0] = max_ctx
+    want = host(jinf_amd.attention_decode(q, k, v, lens, nh, nkv))
+    out = torch.full((n_seq, nh * hd), float("nan"), dtype=torch.float32, device=dev)
+    assert _noalloc(out, q, k, v, lens, nh, nkv) == jinf_amd._lib.JINF_HIP_OK
+    assert tu.bits_equal(host(out), want)
+
+
+@pytest.mark.parametrize("shape", [(1, 8192, 32, 8, 128), (64, 2048, 64, 8, 128)])
+def test_noalloc_captured_in_a_graph(dev, shape):
+    """The in-launch merge (1 x 8192) and the separate merge launch (64 x
+    2048) captured in a HIP graph after one lookup call (n_seq 0), replayed
+    three times with eager work in between: every replay gives the workspace
+    entry point's bits."""
+    n_seq, max_ctx, nh, nkv, hd = shape
+    say(f"graph capture: n_seq={n_seq} ctx={max_ctx} heads={nh}/{nkv} hd={hd}")
+    r = tu.rng(sum(shape))
+    qd, kd, vd, ld = _case(r, n_seq, max_ctx, nh, nkv, hd)
+    ws = jinf_amd.attention_workspace(n_seq, nh, hd, max_ctx)
+    want = host(jinf_amd.attention_decode(qd, kd, vd, ld, nh, nkv, workspace=ws))
+    fn = jinf_amd.lib().jinf_attention_decode_noalloc
+    # the lookup call: no sequences, nothing enqueued
+    assert fn(0, 0, 0, 0, 0, 0, jinf_amd.F16, 0, 0, 0, 0, 0, hd, nh, nkv, 0.0,
+              torch.cuda.current_stream().cuda_stream) == jinf_amd._lib.JINF_HIP_OK
+    out = torch.full((n_seq, nh * hd), float("nan"), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = _noalloc(out, qd, kd, vd, ld, nh, nkv)
+    assert rc == jinf_amd._lib.JINF_HIP_OK
+    for i in range(3):
+        out.fill_(float("nan"))
+        # eager work between replays, through the same scratch: a smaller call
+        small = torch.empty((1, nh * hd), dtype=torch.float32, device=dev)
+        assert _noalloc(small, qd[:1], kd[:1], vd[:1], ld[:1], nh, nkv) == jinf_amd._lib.JINF_HIP_OK
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert tu.bits_equal(host(out), want), f"replay {i + 1}"
