@@ -166,6 +166,29 @@ def test_q4_x_scales(dev, qtype, rows, cols, scale):
     check(y, ref, a, f"{NAMES[qtype]} scale {scale}")
 
 
+# The 4-bit kernels round x to steps of 2^-23 of its 32-value block's largest
+# |x|.  An outlier that meets a zero weight (Q4_0 code 8) adds nothing to
+# sum |w x|, so the bar then measures the rounding of the block's small values
+# against their own products: with an outlier R times the typical |x| in
+# every block of every row (element 0 of each block, its code set to 8) the
+# bar holds at R = 2^8 (about 2e-6); at R = 2^10 this draw measured 1.2e-5 on
+# the GPU, past the bar: the limit of the 24-bit fixed point, between 2^8 and
+# 2^10 for outliers on zero weights in every block.
+@pytest.mark.parametrize("ratio", [2.0 ** 8])
+def test_q4_0_outlier_meets_zero_weight(dev, ratio):
+    rows, cols = 512, 4096
+    say(f"Q4_0 matvec {rows}x{cols}, an outlier x{ratio:.0f} per block on a zero weight")
+    r = tu.rng(int(ratio) + 3)
+    W = tu.quant_table(r, 2, rows, cols)
+    blk = W.reshape(rows, cols // 32, 18)
+    blk[:, :, 2] = (blk[:, :, 2] & 0xF0) | 0x08  # element 0 of every block: q = 8, w = 0
+    x = tu.normal(r, (cols,), 0.0, 1.0, np.float32)
+    x[::32] = (ratio * np.sign(r.normal(size=cols // 32))).astype(np.float32)
+    ref, a = _oracle(2, W, x)
+    y = host(jinf_amd.matvec(to_dev(W), to_dev(x), 2))
+    check(y, ref, a, f"outlier ratio {ratio:.0f}")
+
+
 # A non-finite x value makes every row NaN in the tiled 4-bit kernel (its
 # block's scale is NaN); the reference's fp32 products give NaN (a zero
 # weight times inf, or any NaN) or +-inf there.
