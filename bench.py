@@ -1119,6 +1119,7 @@ _KERNEL_KEYS = [("ew_vec_kernel<unsigned short, 1", "swiglu"),
                 ("probe_stream_kernel", "probe_stream"),
                 ("probe_gather_kernel", "probe_gather"),
                 ("probe_rows_ragged_kernel", "probe_rows_ragged"),
+                ("probe_flat_kernel", "probe_flat"),
                 ("am_clear_kernel", "attention counter clear"),
                 # batched decode: matvec_batch_kernel<qtype, M-tiles, epilogue, tiles, waves, k-parts>
                 ("matvec_batch_kernel<2, 1, 3,", "batch qkv+rope (Q4_0)"),
