@@ -202,32 +202,20 @@ int bat_embed(jinf_hip_batch* b, int rows) {
 }
 
 // `pend`: the previous layer's deferred down-projection residual add, merged
-// into the residual stream by a launch ahead of the first call's preparation.
+// into the residual stream by a launch ahead of the first GEMV's preparation.
+// One GEMV launch per weight format of q, k and v (Q4_K_M: Q4_K q and k, Q6_K
+// v), one epilogue launch for all of them.
 int bat_qkv(jinf_hip_batch* b, const jinf_hip_layer_weights& w, void* kc, void* vc, int rows,
             int64_t ld_seq, MbDefer& pend) {
     const jinf_hip_engine_desc& d = *b->d;
     const void* W[3] = {w.attn_q, w.attn_k, w.attn_v};
     const int T[3] = {w.attn_q_type, w.attn_k_type, w.attn_v_type};
-    bool done[3] = {false, false, false};
-    // x prepared by an earlier call in the one-launch record layout (Q6_K
-    // beyond 32 rows runs two one-tile launches, each preparing its own)
-    bool prepared = false;
-    for (int i = 0; i < 3; ++i) {
-        if (done[i]) continue;
-        const void* p[3] = {nullptr, nullptr, nullptr};
-        for (int k = i; k < 3; ++k)
-            if (!done[k] && T[k] == T[i]) {
-                p[k] = W[k];
-                done[k] = true;
-            }
-        BAT_TRY(rmsnorm_qkv_rope_batch_m(
-            p[0], p[1], p[2], T[i], b->hidden, d.n_embd, w.attn_norm, w.attn_norm_type,
-            d.rms_norm_eps, d.n_embd, b->q, b->q_dim, kc, vc, b->kv_type, ld_seq, b->positions,
-            b->max_ctx, b->head_dim, d.n_heads, d.n_heads_kv, d.rope_freq_base, rows, b->mws,
-            b->mws_bytes, &pend, b->dpart, b->dpart_bytes, prepared, b->stream));
-        pend = MbDefer{};
-        prepared = rows <= 32 || T[i] != kQ6_K;
-    }
+    BAT_TRY(rmsnorm_qkv_rope_batch_mixed(
+        W, T, b->hidden, d.n_embd, w.attn_norm, w.attn_norm_type, d.rms_norm_eps, d.n_embd, b->q,
+        b->q_dim, kc, vc, b->kv_type, ld_seq, b->positions, b->max_ctx, b->head_dim, d.n_heads,
+        d.n_heads_kv, d.rope_freq_base, rows, b->mws, b->mws_bytes, &pend, b->dpart,
+        b->dpart_bytes, b->stream));
+    pend = MbDefer{};
     return JINF_HIP_OK;
 }
 
@@ -440,10 +428,15 @@ int bat_create(jinf_hip_batch** out, const jinf_hip_engine* engine, int n_seq, i
     b->aws_bytes = jinf_attention_workspace_bytes(n_seq, d.n_heads, b->head_dim, max_context);
     // partial sums of the deferred merges: output and down projections,
     // and the Q / K / V launch
-    const int qkv_rows = b->q_dim + 2 * b->kv_dim;
-    for (const auto& sh : {std::make_pair(n, b->q_dim), std::make_pair(n, nff),
-                           std::make_pair(qkv_rows, n)}) {
+    for (const auto& sh : {std::make_pair(n, b->q_dim), std::make_pair(n, nff)}) {
         const size_t w = matvec_batch_defer_bytes(sh.first, sh.second, n_seq);
+        if (w > b->dpart_bytes) b->dpart_bytes = w;
+    }
+    // each layer's Q / K / V launches keep one partials region per format
+    for (int L = 0; L < d.n_layers; ++L) {
+        const jinf_hip_layer_weights& lw = d.layers[L];
+        const int T[3] = {lw.attn_q_type, lw.attn_k_type, lw.attn_v_type};
+        const size_t w = qkv_defer_bytes(T, b->q_dim, b->kv_dim, n, n_seq);
         if (w > b->dpart_bytes) b->dpart_bytes = w;
     }
 

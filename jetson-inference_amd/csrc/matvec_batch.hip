@@ -514,14 +514,27 @@ __device__ __forceinline__ void mb_qkv_store(const MbJob& j, const RopeTheta& th
     }
 }
 
-// The Q / K / V launch's epilogue after a deferred column split: one lane
-// per row pair of one sequence sums the k_splits partials in split order
+// The deferred Q / K / V launches of one layer, one per weight format (q, k
+// and v may each have their own), finished by one epilogue launch: (sequence,
+// row pair) items [pairs[g - 1], pairs[g]) belong to job g.
+struct MbQkvJobs {
+    MbJob j[3];
+    int pairs[3];
+    int n;
+};
+
+// The Q / K / V epilogue after deferred column splits: one lane per row pair
+// of one sequence of one job sums that job's k_splits partials in split order
 // (the order of the GEMV's own merge), then rotates and stores as above.
-__global__ __launch_bounds__(256) void mb_qkv_epilogue_kernel(MbJob j, RopeTheta th) {
+__global__ __launch_bounds__(256) void mb_qkv_epilogue_kernel(MbQkvJobs js, RopeTheta th) {
     constexpr int SB = 8;  // partials loaded together
+    int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= js.pairs[js.n - 1]) return;
+    // the job of item i (a wave-uniform choice except at job boundaries)
+    const int g = i < js.pairs[0] ? 0 : (i < js.pairs[1] || js.n < 3) ? 1 : 2;
+    if (g > 0) i -= js.pairs[g - 1];
+    const MbJob& j = js.j[g];
     const int half = j.rows / 2;
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= j.n_batch * half) return;
     const int b = i / half, v0 = 2 * (i % half);
     const float* pp = j.dpart + (int64_t)b * j.rows + v0;
     float a = 0.0f, c = 0.0f;
@@ -1364,13 +1377,19 @@ int rmsnorm_swiglu_matvec_batch_m(const void* w_gate, const void* w_up, int qtyp
     return mb_dispatch<kMbEpiSwiGLU>(qtype, j, sh, MbNoTheta{}, norm_w, f16, eps, pend, stream);
 }
 
-int rmsnorm_qkv_rope_batch_m(const void* wq, const void* wk, const void* wv, int qtype, float* h,
-                             int ld_h, const void* norm_w, int norm_type, float eps, int n_embd,
-                             float* q, int ld_q, void* k_cache, void* v_cache, int kv_type,
-                             int64_t ld_seq, const int32_t* positions, int max_ctx, int head_dim,
-                             int n_heads, int n_heads_kv, float freq_base, int n_batch,
-                             void* workspace, size_t workspace_bytes, const MbDefer* pend,
-                             float* part, size_t part_bytes, bool x_ready, hipStream_t stream) {
+// rmsnorm_qkv_rope_batch_m; collect (may be null): with split columns the
+// deferred job is appended to it, its partials' bytes written to *part_used,
+// and no epilogue launched (rmsnorm_qkv_rope_batch_mixed finishes every
+// format's job in one launch).
+static int qkv_rope_batch(const void* wq, const void* wk, const void* wv, int qtype, float* h,
+                          int ld_h, const void* norm_w, int norm_type, float eps, int n_embd,
+                          float* q, int ld_q, void* k_cache, void* v_cache, int kv_type,
+                          int64_t ld_seq, const int32_t* positions, int max_ctx, int head_dim,
+                          int n_heads, int n_heads_kv, float freq_base, int n_batch,
+                          void* workspace, size_t workspace_bytes, const MbDefer* pend,
+                          float* part, size_t part_bytes, bool x_ready, hipStream_t stream,
+                          MbQkvJobs* collect, size_t* part_used) {
+    if (part_used) *part_used = 0;
     if (head_dim <= 0 || head_dim % 2 != 0 || head_dim / 2 > kRopeMaxHalf || n_heads < 0 ||
         n_heads_kv < 0 || !(freq_base > 0.0f) || !positions)
         return JINF_HIP_ERR_INVALID;
@@ -1429,8 +1448,98 @@ int rmsnorm_qkv_rope_batch_m(const void* wq, const void* wk, const void* wv, int
     rc = mb_dispatch<kMbEpiQKV>(qtype, j, sh, th, norm_w, f16, eps, pend, stream);
     if (rc != JINF_HIP_OK || !j.dpart) return rc;
     const int pairs = n_batch * (rows / 2);
+    if (collect) {
+        // finished by the caller's one epilogue launch for the layer
+        collect->j[collect->n] = j;
+        collect->pairs[collect->n] = (collect->n ? collect->pairs[collect->n - 1] : 0) + pairs;
+        ++collect->n;
+        *part_used = (size_t)j.k_splits * n_batch * rows * sizeof(float);
+        return JINF_HIP_OK;
+    }
+    MbQkvJobs js{};
+    js.j[0] = j;
+    js.pairs[0] = pairs;
+    js.n = 1;
     return launch(mb_qkv_epilogue_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0,
-                  stream, j, th);
+                  stream, js, th);
+}
+
+int rmsnorm_qkv_rope_batch_m(const void* wq, const void* wk, const void* wv, int qtype, float* h,
+                             int ld_h, const void* norm_w, int norm_type, float eps, int n_embd,
+                             float* q, int ld_q, void* k_cache, void* v_cache, int kv_type,
+                             int64_t ld_seq, const int32_t* positions, int max_ctx, int head_dim,
+                             int n_heads, int n_heads_kv, float freq_base, int n_batch,
+                             void* workspace, size_t workspace_bytes, const MbDefer* pend,
+                             float* part, size_t part_bytes, bool x_ready, hipStream_t stream) {
+    return qkv_rope_batch(wq, wk, wv, qtype, h, ld_h, norm_w, norm_type, eps, n_embd, q, ld_q,
+                          k_cache, v_cache, kv_type, ld_seq, positions, max_ctx, head_dim,
+                          n_heads, n_heads_kv, freq_base, n_batch, workspace, workspace_bytes,
+                          pend, part, part_bytes, x_ready, stream, nullptr, nullptr);
+}
+
+// Partials region of one format group's deferred Q / K / V launch: 256-byte
+// aligned, so that the next group's partials start 16-byte aligned.
+static size_t mb_qkv_part_span(size_t used) { return (used + 255) / 256 * 256; }
+
+int rmsnorm_qkv_rope_batch_mixed(const void* const w[3], const int types[3], float* h, int ld_h,
+                                 const void* norm_w, int norm_type, float eps, int n_embd,
+                                 float* q, int ld_q, void* k_cache, void* v_cache, int kv_type,
+                                 int64_t ld_seq, const int32_t* positions, int max_ctx,
+                                 int head_dim, int n_heads, int n_heads_kv, float freq_base,
+                                 int n_batch, void* workspace, size_t workspace_bytes,
+                                 const MbDefer* pend, float* part, size_t part_bytes,
+                                 hipStream_t stream) {
+    bool done[3] = {false, false, false};
+    MbQkvJobs js{};
+    const MbDefer* pd = pend;
+    // x prepared by an earlier call in the one-launch record layout (Q6_K
+    // beyond 32 rows runs two one-tile launches, each preparing its own)
+    bool prepared = false;
+    size_t off = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (done[i]) continue;
+        const void* p[3] = {nullptr, nullptr, nullptr};
+        for (int k = i; k < 3; ++k)
+            if (!done[k] && types[k] == types[i]) {
+                p[k] = w[k];
+                done[k] = true;
+            }
+        size_t used = 0;
+        const int rc = qkv_rope_batch(
+            p[0], p[1], p[2], types[i], h, ld_h, norm_w, norm_type, eps, n_embd, q, ld_q,
+            k_cache, v_cache, kv_type, ld_seq, positions, max_ctx, head_dim, n_heads, n_heads_kv,
+            freq_base, n_batch, workspace, workspace_bytes, pd,
+            part ? reinterpret_cast<float*>(reinterpret_cast<char*>(part) + off) : nullptr,
+            part_bytes > off ? part_bytes - off : 0, prepared, stream, &js, &used);
+        if (rc != JINF_HIP_OK) return rc;
+        off += mb_qkv_part_span(used);
+        pd = nullptr;
+        prepared = n_batch <= 32 || types[i] != kQ6_K;
+    }
+    if (js.n == 0) return JINF_HIP_OK;
+    RopeTheta th;
+    theta_table(th, head_dim, freq_base);
+    const int pairs = js.pairs[js.n - 1];
+    return launch(mb_qkv_epilogue_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0,
+                  stream, js, th);
+}
+
+size_t qkv_defer_bytes(const int types[3], int q_dim, int kv_dim, int n_embd, int n_batch) {
+    const int dims[3] = {q_dim, kv_dim, kv_dim};
+    bool done[3] = {false, false, false};
+    size_t total = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (done[i]) continue;
+        int rows = 0;
+        for (int k = i; k < 3; ++k)
+            if (!done[k] && types[k] == types[i]) {
+                rows += dims[k];
+                done[k] = true;
+            }
+        // (matvec_batch_defer_bytes counts the same 64-row groups and splits)
+        total += mb_qkv_part_span(matvec_batch_defer_bytes(rows, n_embd, n_batch));
+    }
+    return total;
 }
 
 uint8_t* matvec_batch_add_xrec(void* workspace, int qtype, int rows, int cols, int n_batch,

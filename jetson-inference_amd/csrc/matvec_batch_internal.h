@@ -144,4 +144,22 @@ int rmsnorm_qkv_rope_batch_m(const void* wq, const void* wk, const void* wv, int
                              void* workspace, size_t workspace_bytes, const MbDefer* pend,
                              float* part, size_t part_bytes, bool x_ready, hipStream_t stream);
 
+// A layer's Q / K / V projections whose matrices may be of up to three
+// formats (w / types in q, k, v order): one GEMV launch per format, all
+// reading the x the first one prepares (except Q6_K beyond 32 sequences,
+// whose two one-tile launches prepare their own), their split partials laid
+// one after another in `part` (qkv_defer_bytes), and one epilogue launch for
+// all of them.  `pend` is merged ahead of the first launch.
+int rmsnorm_qkv_rope_batch_mixed(const void* const w[3], const int types[3], float* h, int ld_h,
+                                 const void* norm_w, int norm_type, float eps, int n_embd,
+                                 float* q, int ld_q, void* k_cache, void* v_cache, int kv_type,
+                                 int64_t ld_seq, const int32_t* positions, int max_ctx,
+                                 int head_dim, int n_heads, int n_heads_kv, float freq_base,
+                                 int n_batch, void* workspace, size_t workspace_bytes,
+                                 const MbDefer* pend, float* part, size_t part_bytes,
+                                 hipStream_t stream);
+
+// Bytes of `part` that rmsnorm_qkv_rope_batch_mixed needs for these formats.
+size_t qkv_defer_bytes(const int types[3], int q_dim, int kv_dim, int n_embd, int n_batch);
+
 }  // namespace jinf
