@@ -282,13 +282,16 @@ def build_matvec(torch, jinf, g, name, rows, cols, keep, qtype=2):
 FLAT_MIXES = {"2:1": (2, 1, False), "2:1 in place": (2, 1, True),
               "2:2 in place": (2, 2, True), "1:1 in place": (1, 1, True), "1:1": (1, 1, False)}
 KERNEL_MIX = {"rope": "1:1 in place", "residual_rmsnorm": "2:2 in place", "swiglu": "2:1",
-              "residual_add": "2:1 in place", "masked_softmax": "1:1", "q4_0_gather": "gather"}
+              "residual_add": "2:1 in place", "masked_softmax": "1:1", "q4_0_gather": "gather",
+              "gemv_q": "read", "gemv_k": "read", "gemv_v": "read", "gemv_o": "read",
+              "gemv_gate": "read", "gemv_up": "read", "gemv_down": "read"}
 # (units per lane, cross-lane exchange, lanes per workgroup, workgroups: 0 = one
 # pass over the data, else a grid-stride loop over that many)
 FLAT_LAYOUTS = tuple((u, x, b, gr) for u in (1, 2, 4) for x in (True, False)
                      for b, gr in ((64, 0), (128, 0), (256, 0), (512, 0), (1024, 0),
                                    (256, 2048), (1024, 512)))
 GATHER_LAYOUTS = ((1, True), (2, True), (4, True), (1, False), (2, False), (4, False))
+READ_LAYOUTS = tuple(lay for lay in FLAT_LAYOUTS if not lay[1])  # no stores to exchange for
 
 
 def build_flat(torch, jinf, mix, nbytes, keep):
@@ -312,6 +315,20 @@ def build_flat(torch, jinf, mix, nbytes, keep):
         k = Kernel("row gather", n * (ri + ro + 4), 0, "", [], "probe_gather_kernel",
                    probes=probes, probe_name="probe_gather_kernel")
         k.probe_upls = GATHER_LAYOUTS
+        return k
+    if mix == "read":
+        # a GEMV's weight traffic: reads only
+        n_units = max(1, nbytes // 16)
+        sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+        probes = []
+        for _ in range(n_sets(16 * n_units)):
+            t = torch.ones(n_units * 4, dtype=torch.float32, device="cuda")
+            keep.append((t, sink))
+            probes.append(lambda lay, t=t: jinf.ops.probe_read_layout(t, sink, lay[0], lay[2],
+                                                                      lay[3]))
+        k = Kernel("flat read", 16 * n_units, 0, "", [], "probe_read_kernel", probes=probes,
+                   probe_name="probe_read_kernel")
+        k.probe_upls = READ_LAYOUTS
         return k
     ni, no, inplace = FLAT_MIXES[mix]
     n_units = max(1, nbytes // (16 * (ni + no)))
@@ -357,13 +374,13 @@ CURVE_MB = (2.0, 2.36, 3.15, 4.0, 4.21, 8.0, 10.49, 11.01, 16.0, 32.0, 43.01, 64
 def stream_curve(torch, jinf, timed, n_launch):
     """Text table: best attainable stream rate per read:write mix and size."""
     lines = ["attainable HBM stream rate on one MI355X: the fastest of "
-             f"{len(FLAT_LAYOUTS)} launch layouts (flat mixes) or {len(GATHER_LAYOUTS)} "
-             "(row gather) per point, each timed over "
+             f"{len(FLAT_LAYOUTS)} launch layouts (flat mixes), {len(GATHER_LAYOUTS)} "
+             f"(row gather) or {len(READ_LAYOUTS)} (read only) per point, each timed over "
              f"{n_launch} back-to-back launches in one HIP graph, buffer sets rotated over "
              ">= 512 MiB of touched memory",
              "layout = (units per lane, cross-lane exchange[, lanes per workgroup, "
              "workgroups (0 = one pass, else grid-stride)])", ""]
-    for mix in list(FLAT_MIXES) + ["gather"]:
+    for mix in list(FLAT_MIXES) + ["gather", "read"]:
         lines.append(f"mix {mix}:")
         lines.append(f"  {'MB':>8} {'us':>9} {'GB/s':>8} {'% of 8 TB/s':>12}  layout")
         for mb in CURVE_MB:
@@ -1296,7 +1313,7 @@ def main():
     # every kernel is timed: these allocate and free their own buffer sets)
     if args.workload != "calibrate" and not args.no_ceilings:
         for k in ks + ks70:
-            if k.probes and k.name in KERNEL_MIX:
+            if k.name in KERNEL_MIX:
                 k.att_us, k.att_lay = attainable(torch, jinf_amd, timed, KERNEL_MIX[k.name],
                                                  k.nbytes, n_launch)
     ms_step = total_ms / args.steps
@@ -1311,20 +1328,21 @@ def main():
             e = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac_of_8TBs": round(gbs / PEAK_GBS, 4),
                  "rows_per_s": round(k.rows / (us * 1e-6), 1), "row_unit": k.row_unit,
                  "bytes": k.nbytes, "sets": len(k.launches), "launches_timed": k.n}
+            # ceiling: the faster of the probe in the kernel's own geometry
+            # and the geometry-free attainable stream of its mix and size
+            cus = None
             if k.ceil_ms is not None:
-                # ceiling: the faster of the probe in the kernel's own geometry
-                # and the geometry-free attainable stream of its mix and size
-                pus = k.ceil_ms / k.n * 1e3
-                cus = pus
-                e.update({"probe_us": round(pus, 3), "probe_frac": round(pus / us, 4),
+                cus = k.ceil_ms / k.n * 1e3
+                e.update({"probe_us": round(cus, 3), "probe_frac": round(cus / us, 4),
                           "ceiling_probe": k.probe_name, "ceiling_units_per_lane": k.ceil_upl[0],
                           "ceiling_exchange": k.ceil_upl[1]})
-                if getattr(k, "att_us", None) is not None:
-                    cus = min(pus, k.att_us)
-                    e.update({"attainable_us": round(k.att_us, 3),
-                              "attainable_frac": round(k.att_us / us, 4),
-                              "attainable_mix": KERNEL_MIX[k.name],
-                              "attainable_layout": list(k.att_lay)})
+            if getattr(k, "att_us", None) is not None:
+                cus = k.att_us if cus is None else min(cus, k.att_us)
+                e.update({"attainable_us": round(k.att_us, 3),
+                          "attainable_frac": round(k.att_us / us, 4),
+                          "attainable_mix": KERNEL_MIX[k.name],
+                          "attainable_layout": list(k.att_lay)})
+            if cus is not None:
                 e.update({"ceiling_us": round(cus, 3),
                           "ceiling_GB/s": round(k.nbytes / (cus * 1e-6) / 1e9, 1),
                           "frac_of_ceiling": round(cus / us, 4)})

@@ -49,6 +49,13 @@ int jinf_probe_stream_layout(void* out0, void* out1, const void* in0, const void
                              int64_t n_units, int units_per_lane, int exchange,
                              int block_lanes, int max_groups, hipStream_t stream);
 
+/* A read-only stream (a GEMV's weight traffic) in the layouts of
+ * jinf_probe_stream_layout: n_units 16-byte units of `in` read once; sink (4
+ * bytes) is written only if the loaded words xor to one fixed value, which no
+ * probe input produces, so in practice nothing is written. */
+int jinf_probe_read_layout(const void* in, int64_t n_units, void* sink, int units_per_lane,
+                           int block_lanes, int max_groups, hipStream_t stream);
+
 /* Row gather (the Q4_0 embedding gather's geometry): output row r
  * (ld_out bytes apart, out_units units) is written from table row ids[r]
  * (row r when ids is NULL; ld_table bytes apart, in_units <= out_units units,

@@ -135,6 +135,30 @@ __global__ __launch_bounds__(BS) void probe_flat_kernel(uint8_t* out0, uint8_t* 
     }
 }
 
+// Read-only streams (a GEMV's weight traffic) in the layouts above: every
+// unit of `in` is read once; the xor of a workgroup's loads is stored to
+// sink[0] only when it equals a value no input of the probe produces, so the
+// loads cannot be dropped and nothing is written in practice.
+template <int U, int BS>
+__global__ __launch_bounds__(BS) void probe_read_kernel(const uint8_t* in, int64_t n_units,
+                                                       uint32_t* sink) {
+    const int64_t step = (int64_t)gridDim.x * BS * U;
+    uint32_t acc = 0;
+    for (int64_t i0 = (int64_t)blockIdx.x * BS * U + threadIdx.x; i0 - threadIdx.x < n_units;
+         i0 += step) {
+        uint4 v[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const int64_t i = i0 + (int64_t)BS * j;
+            v[j] = make_uint4(0, 0, 0, 0);
+            if (i < n_units) v[j] = ld16<true>(in + i * 16);
+        }
+#pragma unroll
+        for (int j = 0; j < U; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    }
+    if (acc == 0x7F3A1C5Du) sink[0] = acc;
+}
+
 // Gather geometry: grid (ids, ceil(out_units / (256 U))), 256 lanes of U
 // output units; output unit u of row r is written from unit about
 // u * in_units / out_units of table row ids[r] (in_units <= out_units), so
@@ -308,6 +332,37 @@ extern "C" int jinf_probe_stream_layout(void* out0, void* out1, const void* in0,
         default: return JINF_PROBE_FLAT(1024);
     }
 #undef JINF_PROBE_FLAT
+}
+
+extern "C" int jinf_probe_read_layout(const void* in, int64_t n_units, void* sink,
+                                      int units_per_lane, int block_lanes, int max_groups,
+                                      hipStream_t stream) {
+    using namespace jinf;
+    const int U = units_per_lane;
+    const int B = block_lanes;
+    if (n_units < 0 || (U != 1 && U != 2 && U != 4) || max_groups < 0 ||
+        (B != 64 && B != 128 && B != 256 && B != 512 && B != 1024))
+        return JINF_HIP_ERR_INVALID;
+    if (n_units == 0) return JINF_HIP_OK;
+    if (!in || !sink || !al16(in) || !aligned(sink, 4)) return JINF_HIP_ERR_INVALID;
+    int64_t gx = (n_units + (int64_t)B * U - 1) / ((int64_t)B * U);
+    if (max_groups > 0 && gx > max_groups) gx = max_groups;
+    if (gx > 0x7FFFFFFF) return JINF_HIP_ERR_INVALID;
+    auto go = [&](auto kern) {
+        return launch(kern, dim3((unsigned)gx), dim3(B), 0, stream,
+                      static_cast<const uint8_t*>(in), n_units, static_cast<uint32_t*>(sink));
+    };
+#define JINF_PROBE_READ(BS)                                                                  \
+    (U == 1 ? go(probe_read_kernel<1, BS>)                                                   \
+            : U == 2 ? go(probe_read_kernel<2, BS>) : go(probe_read_kernel<4, BS>))
+    switch (B) {
+        case 64: return JINF_PROBE_READ(64);
+        case 128: return JINF_PROBE_READ(128);
+        case 256: return JINF_PROBE_READ(256);
+        case 512: return JINF_PROBE_READ(512);
+        default: return JINF_PROBE_READ(1024);
+    }
+#undef JINF_PROBE_READ
 }
 
 extern "C" int jinf_probe_gather(void* out, int64_t ld_out, int out_units, const void* table,

@@ -80,6 +80,7 @@ SIGNATURES = {
                                      _I, _P]),
     "jinf_probe_stream": (_I, [_P, _P, _P, _P, ctypes.c_int64, _I, _I, _P]),
     "jinf_probe_stream_layout": (_I, [_P, _P, _P, _P, ctypes.c_int64, _I, _I, _I, _I, _P]),
+    "jinf_probe_read_layout": (_I, [_P, ctypes.c_int64, _P, _I, _I, _I, _P]),
     "jinf_probe_gather": (_I, [_P, ctypes.c_int64, _I, _P, ctypes.c_int64, _I, _I, _P, _I, _I,
                                _I, _P]),
     "jinf_probe_rows_ragged": (_I, [_P, ctypes.c_int64, _P, ctypes.c_int64, _I, _P, _I, _I,

@@ -481,6 +481,15 @@ def probe_stream_layout(out0, in0, out1=None, in1=None, units_per_lane=1, exchan
            "jinf_probe_stream_layout")
 
 
+def probe_read_layout(inp, sink, units_per_lane=1, block_lanes=256, max_groups=0):
+    """A read-only stream over inp's bytes (16-byte units) in a chosen launch
+    layout; sink: a 4-byte device tensor the probe leaves untouched in practice."""
+    nbytes = inp.numel() * inp.element_size()
+    _check(lib().jinf_probe_read_layout(_ptr(inp), nbytes // 16, _ptr(sink), int(units_per_lane),
+                                        int(block_lanes), int(max_groups), _stream()),
+           "jinf_probe_read_layout")
+
+
 def probe_gather(out, table, ids, in_row_bytes, units_per_lane=1, exchange=True):
     """The gather's traffic: out row r from table row ids[r] (table viewed as
     byte rows; in_row_bytes of each row read)."""
