@@ -295,10 +295,11 @@ __global__ __launch_bounds__(64) void attn_decode_any_kernel(
 // ---- fp16 cache: matrix-core kernel ----
 //
 // For an fp16 cache the GQA group's work per 64-position tile is two small
-// matrix products, done on the matrix cores with v_mfma_f32_16x16x16_f16
-// (A 16x16 rows x k, B 16x16 k x columns, fp32 accumulate; lane l supplies A
-// row l % 16 / B column l % 16 at k = 4 (l / 16) .. + 3, and holds D rows
-// 4 (l / 16) .. + 3 of column l % 16):
+// matrix products, done on the matrix cores with v_mfma_f32_16x16x32_f16
+// (A 16 rows x 32 k, B 32 k x 16 columns, fp32 accumulate; lane l supplies A
+// row l % 16 / B column l % 16 at eight k slots of lane group l / 16, and
+// holds D rows 4 (l / 16) .. + 3 of column l % 16; the products only need the
+// same k slots in A and B):
 //   S^T[t][c] = sum_d K[t][d] Q'[d][c]   A = K rows (fp16, exact),
 //                                          B = columns c = 8 head slots x {hi, lo}
 //   O[c][d]  += sum_t P'[c][t] V[t][d]   A = P' (hi / lo rows), B = V
@@ -306,13 +307,16 @@ __global__ __launch_bounds__(64) void attn_decode_any_kernel(
 // (hi = fp16(x), lo = fp16(x - hi)), so the products keep about 22
 // significant bits; the 2^15 keeps the probabilities in fp16's normal range
 // and is divided out exactly at the end.  The score accumulator's layout
-// (lane: column c, rows = 4 positions) is exactly the A layout P needs, so
-// the softmax runs in registers; V goes through LDS (rows padded by 8 bytes,
-// so the four lane groups hit different banks) and each B fragment is four
-// 16-bit reads.  The dot-product index is permuted identically in K and Q'
-// (lane group g, k-step s covers dims (HD/4) g + 4 s .. + 3), so each lane
-// loads its K slice as contiguous 16-byte pieces.
+// (lane: column c, rows = 4 positions) is the A layout P needs, so the
+// softmax runs in registers, and two 16-position blocks' accumulators make
+// one 32-deep A fragment; V goes through LDS and is read back transposed.
+// The dot-product index is permuted identically in K and Q' (lane group g,
+// k-step s covers dims (HD/4) g + 8 s .. + 7), so each lane reads its K
+// slice as whole 16-byte pieces.  (16x16x16 steps, as the one-block-per-wave
+// short-context form still uses for P V, measured 234.1 against 233.0 us on
+// the 70B decode attention.)
 typedef _Float16 am_h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 am_h8 __attribute__((ext_vector_type(8)));
 typedef float am_f4 __attribute__((ext_vector_type(4)));
 
 // A workspace splits contexts into chunks of kAmChunkMin positions or more,
@@ -328,6 +332,9 @@ constexpr int kAmInKernelMerge = 128;
 __device__ __forceinline__ am_h4 am_h4_from(uint32_t lo, uint32_t hi) {
     const uint2 u = make_uint2(lo, hi);
     return __builtin_bit_cast(am_h4, u);
+}
+__device__ __forceinline__ am_h8 am_h8_cat(am_h4 a, am_h4 b) {
+    return am_h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
 __device__ __forceinline__ float ror8(float v) { return dpp_f32<0x128>(v); }  // row_ror:8
@@ -555,6 +562,11 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
             qf[ks] = am_h4{hv[0], hv[1], hv[2], hv[3]};
         }
     }
+    // the score product's B fragments for 32-deep k-steps: the lane's 8 dims
+    // DPG lg + 8 u .. + 7, the order of the K row's 16-byte chunk u
+    am_h8 qf8[KLD];
+#pragma unroll
+    for (int u = 0; u < KLD; ++u) qf8[u] = am_h8_cat(qf[2 * u], qf[2 * u + 1]);
     // A wave stops at the first tile holding none of its rows (with RB a
     // wave's block can end before the tile does), so it never issues loads
     // for a tile it does not process and never sees an all-masked tile.
@@ -574,8 +586,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
             for (int u = 0; u < KLD; ++u) {
                 const int c = (DPG * lg) / 8 + u;  // 16-byte chunk of the row
                 const uint4 w = *reinterpret_cast<const uint4*>(kst + r * PITCH + 16 * (c ^ kswz(r)));
-                S[bi] = __builtin_amdgcn_mfma_f32_16x16x16f16(am_h4_from(w.x, w.y), qf[2 * u], S[bi], 0, 0, 0);
-                S[bi] = __builtin_amdgcn_mfma_f32_16x16x16f16(am_h4_from(w.z, w.w), qf[2 * u + 1], S[bi], 0, 0, 0);
+                S[bi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(am_h8, w), qf8[u], S[bi], 0, 0, 0);
             }
         }
         wave_lds_sync();
@@ -633,22 +644,33 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
         else
             __builtin_amdgcn_s_waitcnt(waitcnt_vm<0>());
         wave_lds_sync();
-#pragma unroll
-        for (int bi = 0; bi < NBK; ++bi) {
-            const int b = RB ? wave : bi;
-            // B fragment V[16 b + 4 lg + i][16 n + col], i = 0..3, through
-            // one transposing LDS read (ds_read_b64_tr_b16: within each 16
-            // lanes, lane c receives element c % 4 of the 8 bytes read by
-            // lanes c / 4 + 4 i): lane c reads row 16 b + 4 lg + c / 4,
-            // columns 16 n + 4 (c % 4) .. + 3
+        // B fragment V[16 b + 4 lg + i][16 n + col], i = 0..3, through one
+        // transposing LDS read (ds_read_b64_tr_b16: within each 16 lanes,
+        // lane c receives element c % 4 of the 8 bytes read by lanes
+        // c / 4 + 4 i): lane c reads row 16 b + 4 lg + c / 4, columns
+        // 16 n + 4 (c % 4) .. + 3
+        auto vfrag = [&](int b, int n) {
             const int vr = 16 * b + 4 * lg + (col >> 2);
             const uint8_t* vrow = vst + vr * PITCH + 8 * (col & 1);
+            const int p = (2 * n + ((col & 3) >> 1)) ^ (2 * (vr & 3));  // swizzled chunk
+            return __builtin_bit_cast(am_h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                 (am_lds_tr4*)(vrow + 16 * p)));
+        };
+        if constexpr (RB) {
 #pragma unroll
-            for (int n = 0; n < NB; ++n) {
-                const int p = (2 * n + ((col & 3) >> 1)) ^ (2 * (vr & 3));  // swizzled chunk
-                const am_tr4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (am_lds_tr4*)(vrow + 16 * p));
-                O[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(P[bi], __builtin_bit_cast(am_h4, t), O[n], 0, 0, 0);
+            for (int n = 0; n < NB; ++n)
+                O[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(P[0], vfrag(wave, n), O[n], 0, 0, 0);
+        } else {
+            // two 16-row blocks per 32-deep k-step: lane group lg's 8 k
+            // slots are positions 16 b + 4 lg + i of blocks b = 2 bp and
+            // 2 bp + 1, in P' (the score accumulators) and in V alike
+#pragma unroll
+            for (int bp = 0; bp < NBK / 2; ++bp) {
+                const am_h8 pa = am_h8_cat(P[2 * bp], P[2 * bp + 1]);
+#pragma unroll
+                for (int n = 0; n < NB; ++n)
+                    O[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        pa, am_h8_cat(vfrag(2 * bp, n), vfrag(2 * bp + 1, n)), O[n], 0, 0, 0);
             }
         }
         wave_lds_sync();
