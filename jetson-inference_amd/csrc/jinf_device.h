@@ -192,6 +192,16 @@ __device__ __forceinline__ float exp_neg(float a) {
     return a < -104.0f ? 0.0f : r;
 }
 
+// exp(a) for a softmax argument a = s - m <= 0 in two VALU ops: 2^fl(a*fl(log2 e))
+// through v_exp_f32 (1 ulp).  The product's rounding and log2 e's shift the
+// exponent by at most |a| * 1.05e-7, so the relative error is at most
+// 7.3e-8 * |a| + 1.2e-7: below 6.5e-6 for every normal fp32 result (a above
+// about -87.3), where exp_neg stays within about 2 ulp.  -inf gives +0;
+// subnormal results may flush to 0 (absolute error < 1.2e-38).
+__device__ __forceinline__ float exp_neg_fast(float a) {
+    return __builtin_amdgcn_exp2f(a * 1.44269502162933349609375f);
+}
+
 // fp64 wave sum, same DPP pattern as wave_sum_f32 (both halves of each value
 // moved by DPP; the four row sums added in row order).  Every lane gets the
 // result.

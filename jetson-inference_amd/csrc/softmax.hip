@@ -16,7 +16,11 @@
 // Every chunk's load is issued before any arithmetic, so a row's loads are in
 // flight together.  Max and sum are DPP wave reductions plus one LDS exchange
 // and one barrier each; each lane's exponentials and then the wave's lanes are
-// summed in fp32, the per-wave sums in fp64.  Chunks past the row's live
+// summed in fp32, the per-wave sums in fp64.  The exponential is the
+// two-operation exp_neg_fast (relative error below 6.5e-6 for every normal
+// result, within the 1e-5 bar; the six-operation, 2-ulp exp_neg took 0.8-1.0
+// us longer at config 5: 26.15-26.32 against 25.11-25.28 us, interleaved,
+// with the ragged-row probe at 24.83-24.92).  Chunks past the row's live
 // length do no arithmetic (whole waves branch over them), so the VALU cost
 // follows the live length, not the padded stride.
 // Grid: (rows per length entry, length entries), so a workgroup finds its
@@ -136,7 +140,7 @@ __global__ __launch_bounds__(BS) void softmax_vec_kernel(
             float part = 0.0f;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float ex = 4 * c + e < L ? exp_neg(v[j][e] - mx) : 0.0f;
+                const float ex = 4 * c + e < L ? exp_neg_fast(v[j][e] - mx) : 0.0f;
                 v[j][e] = ex;
                 part += ex;
             }
@@ -181,10 +185,10 @@ __global__ __launch_bounds__(1024) void softmax_loop_kernel(
     for (int i = threadIdx.x; i < L; i += blockDim.x) m = fmaxf(m, x[i] * scale);
     m = block_max(m, redf);
     double sum = 0.0;
-    for (int i = threadIdx.x; i < L; i += blockDim.x) sum += (double)exp_neg(x[i] * scale - m);
+    for (int i = threadIdx.x; i < L; i += blockDim.x) sum += (double)exp_neg_fast(x[i] * scale - m);
     sum = block_sum(sum, redd);
     const float inv = 1.0f / (float)sum;
-    for (int i = threadIdx.x; i < L; i += blockDim.x) y[i] = exp_neg(x[i] * scale - m) * inv;
+    for (int i = threadIdx.x; i < L; i += blockDim.x) y[i] = exp_neg_fast(x[i] * scale - m) * inv;
 }
 
 static int softmax_dispatch(float* out, int ld_out, const float* in, int ld_in, int n_rows,

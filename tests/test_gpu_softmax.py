@@ -42,6 +42,31 @@ def test_config5_ragged_rows(dev):
     assert tu.bits_equal(host(xd), x)  # input untouched
 
 
+def test_wide_exponent_range(dev):
+    # s - m spread evenly over [-87, 0]: every normal fp32 result, down to
+    # about 1.6e-38, where the two-operation exponential's error bound
+    # (7.3e-8 |a| + 1.2e-7 relative) is largest; offsets move the maxima
+    say("exponent range: s - m over [-87, 0], maxima at 0, 40, -30, 1000")
+    r = tu.rng(91)
+    n = 8192
+    base = np.linspace(-87.0, 0.0, n)
+    x = np.stack([(r.permutation(base) + off).astype(np.float32)
+                  for off in (0.0, 40.0, -30.0, 1000.0)])
+    lens = np.full(4, n, np.int32)
+    ref = oracle.softmax_rows(x, lens, 1, 1.0, out=np.full_like(x, np.nan))
+    xd = to_dev(x)
+    out = torch.full_like(xd, float("nan"))
+    jinf_amd.softmax_rows(xd, to_dev(lens), 1, 1.0, out=out)
+    got = host(out)
+    tu.assert_f32_close(got, ref, 1e-5, 1e-30, "wide range")
+    exact = np.exp(x.astype(np.float64) - x.max(axis=1, keepdims=True).astype(np.float64))
+    exact /= exact.sum(axis=1, keepdims=True)
+    big = exact >= 1e-30
+    err = np.max(np.abs(got[big] - exact[big]) / exact[big])
+    say(f"max relative error against fp64 over results >= 1e-30: {err:.2e}")
+    assert err < 1e-5
+
+
 def test_fixture(dev):
     g = np.load(os.path.join(HERE, "golden", "kernels.npz"))
     xd = to_dev(g["sm_x"])
