@@ -172,32 +172,13 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     return ((r0 + r1) + r2) + r3;
 }
 
-// exp(a) for a softmax argument a = s - m <= 0, accurate to ~2 ulp:
-// Cody-Waite splitting of a*log2(e) into hi + lo (hi the rounded product, lo its
-// exact rounding error plus a times the tail of log2(e)), then
-// 2^hi (v_exp_f32) * (1 + lo*ln2).  |lo| <= 2^-24 |hi| + tiny, so the
-// dropped second-order term is below 1e-13.  Six VALU ops against ~12 for the
-// library expf.  a < -104 (including -inf) returns +0: the true value is below
-// the smallest fp32 subnormal there.  Arguments below about -87.3 give fp32
-// subnormals, which the hardware exp2 may return as 0 (absolute error < 1.2e-38).
-__device__ __forceinline__ float exp_neg(float a) {
-    constexpr float kL2E = 1.44269502162933349609375f;        // fl32(log2 e)
-    constexpr float kL2ELo = 1.925963033500011079e-08f;       // log2 e - kL2E
-    constexpr float kLn2 = 0.693147180559945309f;
-    const float hi = a * kL2E;
-    float lo = fmaf(a, kL2E, -hi);
-    lo = fmaf(a, kL2ELo, lo);
-    const float e = __builtin_amdgcn_exp2f(hi);
-    const float r = fmaf(e, lo * kLn2, e);
-    return a < -104.0f ? 0.0f : r;
-}
-
 // exp(a) for a softmax argument a = s - m <= 0 in two VALU ops: 2^fl(a*fl(log2 e))
 // through v_exp_f32 (1 ulp).  The product's rounding and log2 e's shift the
 // exponent by at most |a| * 1.05e-7, so the relative error is at most
 // 7.3e-8 * |a| + 1.2e-7: below 6.5e-6 for every normal fp32 result (a above
-// about -87.3), where exp_neg stays within about 2 ulp.  -inf gives +0;
-// subnormal results may flush to 0 (absolute error < 1.2e-38).
+// about -87.3); a Cody-Waite split of a*log2(e) into hi + lo with
+// 2^hi * (1 + lo*ln2) would stay within about 2 ulp for four more operations.
+// -inf gives +0; subnormal results may flush to 0 (absolute error < 1.2e-38).
 __device__ __forceinline__ float exp_neg_fast(float a) {
     return __builtin_amdgcn_exp2f(a * 1.44269502162933349609375f);
 }

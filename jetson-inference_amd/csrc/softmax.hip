@@ -18,9 +18,9 @@
 // and one barrier each; each lane's exponentials and then the wave's lanes are
 // summed in fp32, the per-wave sums in fp64.  The exponential is the
 // two-operation exp_neg_fast (relative error below 6.5e-6 for every normal
-// result, within the 1e-5 bar; the six-operation, 2-ulp exp_neg took 0.8-1.0
-// us longer at config 5: 26.15-26.32 against 25.11-25.28 us, interleaved,
-// with the ragged-row probe at 24.83-24.92).  Chunks past the row's live
+// result, within the 1e-5 bar; a six-operation Cody-Waite form, about 2 ulp,
+// took 0.8-1.0 us longer at config 5: 26.15-26.32 against 25.11-25.28 us,
+// interleaved, with the ragged-row probe at 24.83-24.92).  Chunks past the row's live
 // length do no arithmetic (whole waves branch over them), so the VALU cost
 // follows the live length, not the padded stride.
 // Grid: (rows per length entry, length entries), so a workgroup finds its
