@@ -54,6 +54,8 @@ void jinf_cuda_silu_mul(float* output, const float* gate, const float* up,
                         int n, hipStream_t stream);
 
 /* One fp32 row: y = exp(x - max x) / sum exp(x - max x); output may alias input.
+ * Each output within 1e-5 relative of the exact softmax (results below 1e-30
+ * within 1e-30 absolutely).
  * Replaces jinf_cuda_softmax, cuda/softmax_kernel.cu:46-51. */
 void jinf_cuda_softmax(float* output, const float* input, int n, hipStream_t stream);
 

@@ -97,7 +97,10 @@ int jinf_residual_add_rows(void* a, int ld_a, const void* b, int ld_b, int n_row
  * entry; lens then holds ceil(n_rows / rows_per_len) values.  scale must be
  * finite and > 0 (1 for pre-scaled scores).
  * Semantics of cuda/softmax_kernel.cu:8-42 and the attention softmax phase
- * cuda/attention_kernel.cu:59-87 (length n_past = pos + 1). */
+ * cuda/attention_kernel.cu:59-87 (length n_past = pos + 1).  Accuracy: each
+ * exponential within 6.5e-6 relative for every normal fp32 result, each
+ * output within 1e-5 relative of the exact softmax (results below 1e-30 within
+ * 1e-30 absolutely). */
 int jinf_softmax_rows_f32(float* out, int ld_out, const float* in, int ld_in,
                           int n_rows, int n_cols, const int32_t* lens,
                           int rows_per_len, float scale, hipStream_t stream);
