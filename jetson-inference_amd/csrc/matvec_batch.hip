@@ -166,6 +166,22 @@ __device__ __forceinline__ mb_h8 mb_nibbles(uint32_t w, uint32_t hi2, float bias
     return mb_h8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
 }
 
+// Eight 4-bit codes q times an integer sub-block scale g <= 63 as fp16 g q,
+// in the order of mb_nibbles: one packed FMA per pair, (1024 + q) g +
+// (-1024 g), whose exact value g q <= 945 is representable, so its one
+// rounding changes nothing.
+__device__ __forceinline__ mb_h8 mb_nibbles_scaled(uint32_t w, _Float16 g) {
+    const mb_h2 g2 = mb_h2{g, g};
+    const mb_h2 c = mb_h2{(_Float16)-1024.0f, (_Float16)-1024.0f} * g2;  // exact: g < 64
+    mb_h2 p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t v = __builtin_amdgcn_bitop3_b32(w >> (4 * i), 0x000F000Fu, 0x64006400u, 0xEA);
+        p[i] = __builtin_elementwise_fma(as_h2(v), g2, c);
+    }
+    return mb_h8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
+}
+
 // Eight int8 codes (two words) as fp16 in the order (0, 4, 1, 5, 2, 6, 3, 7).
 __device__ __forceinline__ mb_h8 mb_int8(uint32_t w0, uint32_t w1) {
     const mb_h2 b = mb_h2{(_Float16)-1152.0f, (_Float16)-1152.0f};
@@ -816,9 +832,8 @@ __global__ __launch_bounds__(64 * WV, 4 * mb_occ<MT>() / WV) void matvec_batch_k
                     zero(tmp);
 #pragma unroll
                     for (int k = 0; k < KPW; ++k) {
-                        const _Float16 g = f[k >> 1];
-                        const mb_h8 B = mb_nibbles(lds_u32(rb[nt] + 16 + 8 * (k0 + k) + 4 * h), 0u, 0.0f) *
-                                        mb_h8{g, g, g, g, g, g, g, g};  // sc * q <= 945: exact
+                        const mb_h8 B = mb_nibbles_scaled(
+                            lds_u32(rb[nt] + 16 + 8 * (k0 + k) + 4 * h), f[k >> 1]);  // sc * q <= 945
                         mfma_step(k, B, tmp);
                     }
                     const float* xs = meta + 32 * MT;
@@ -827,11 +842,11 @@ __global__ __launch_bounds__(64 * WV, 4 * mb_occ<MT>() / WV) void matvec_batch_k
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
                             const int b = mb_token(mt, r, h);
-                            float mins = 0.0f;
+                            float a = fmaf(d, tmp[mt][r], acc[nt][mt][r]);
 #pragma unroll
                             for (int q = 0; q < NSB; ++q)
-                                mins = fmaf(mn[q], xs[(k0 / 2 + q) * 32 * MT + b], mins);
-                            acc[nt][mt][r] += d * tmp[mt][r] - mins;
+                                a = fmaf(-mn[q], xs[(k0 / 2 + q) * 32 * MT + b], a);
+                            acc[nt][mt][r] = a;
                         }
                 } else {
                     static_assert(QT == kQ6_K, "format");
