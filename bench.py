@@ -290,9 +290,12 @@ KERNEL_MIX = {"rope": "1:1 in place", "residual_rmsnorm": "2:2 in place", "swigl
               "residual_add": "2:1 in place", "masked_softmax": "1:1", "q4_0_gather": "gather",
               "gemv_q": "read", "gemv_k": "read", "gemv_v": "read", "gemv_o": "read",
               "gemv_gate": "read", "gemv_up": "read", "gemv_down": "read"}
-# (units per lane, cross-lane exchange, lanes per workgroup, workgroups: 0 = one
-# pass over the data, else a grid-stride loop over that many)
-FLAT_LAYOUTS = tuple((u, x, b, gr) for u in (1, 2, 4) for x in (True, False)
+# (units per lane, store order, lanes per workgroup, workgroups: 0 = one pass
+# over the data, else a grid-stride loop over that many).  Store order: False,
+# every store after the lane's loads; True, after a cross-lane exchange; 2 (two
+# outputs), the first output straight after its own loads and the second after
+# the exchange, as a row norm stores r' before its reduction and y after it.
+FLAT_LAYOUTS = tuple((u, x, b, gr) for u in (1, 2, 4) for x in (True, False, 2)
                      for b, gr in ((64, 0), (128, 0), (256, 0), (512, 0), (1024, 0),
                                    (256, 2048), (1024, 512)))
 GATHER_LAYOUTS = ((1, True), (2, True), (4, True), (1, False), (2, False), (4, False))
@@ -389,7 +392,8 @@ def stream_curve(torch, jinf, timed, n_launch):
              f"(row gather) or {len(READ_LAYOUTS)} (read only) per point, each timed over "
              f"{n_launch} back-to-back launches in one HIP graph, buffer sets rotated over "
              ">= 512 MiB of touched memory",
-             "layout = (units per lane, cross-lane exchange[, lanes per workgroup, "
+             "layout = (units per lane, store order: False after the loads, True after a "
+             "cross-lane exchange, 2 first output after its own loads[, lanes per workgroup, "
              "workgroups (0 = one pass, else grid-stride)])", ""]
     for mix in list(FLAT_MIXES) + ["gather", "read"]:
         lines.append(f"mix {mix}:")

@@ -44,7 +44,10 @@ int jinf_probe_stream(void* out0, void* out1, const void* in0, const void* in1,
  * geometry-free bandwidth curve): block_lanes (64, 128, 256, 512 or 1024)
  * lanes of units_per_lane units per workgroup; max_groups 0 launches one pass
  * over enough workgroups to cover n_units, max_groups > 0 caps the grid at
- * that many workgroups, which loop over the units with a grid stride. */
+ * that many workgroups, which loop over the units with a grid stride.
+ * exchange: 0, stores after all of a lane's loads; 1, stores after a
+ * cross-lane exchange; 2, out0's units stored straight after their own loads
+ * and out1's after a cross-lane exchange. */
 int jinf_probe_stream_layout(void* out0, void* out1, const void* in0, const void* in1,
                              int64_t n_units, int units_per_lane, int exchange,
                              int block_lanes, int max_groups, hipStream_t stream);

@@ -100,10 +100,16 @@ __global__ __launch_bounds__(kProbeStreamBlock) void probe_stream_kernel(
 // BS lanes of U units per workgroup, either one pass over a grid that covers
 // the units or a grid-stride loop over a capped number of workgroups.  Unit i
 // of every input is read and unit i of every output written by one lane.
-template <int U, bool X, int BS>
+// Store order XM: 0, every store after all of the lane's loads; 1, every
+// store after a cross-lane exchange; 2, the first output's unit stored as
+// soon as that unit's loads are in (from them alone), the second output
+// after a cross-lane exchange (a row norm's order: r' before the reduction,
+// y after it).
+template <int U, int XM, int BS>
 __global__ __launch_bounds__(BS) void probe_flat_kernel(uint8_t* out0, uint8_t* out1,
                                                        const uint8_t* in0, const uint8_t* in1,
                                                        int64_t n_units) {
+    constexpr bool X = XM != 0;
     const int64_t step = (int64_t)gridDim.x * BS * U;
     for (int64_t i0 = (int64_t)blockIdx.x * BS * U + threadIdx.x; i0 - threadIdx.x < n_units;
          i0 += step) {
@@ -119,6 +125,17 @@ __global__ __launch_bounds__(BS) void probe_flat_kernel(uint8_t* out0, uint8_t* 
                 if (in1) v1[j] = ld16<true>(in1 + i * 16);
             }
         }
+        if constexpr (XM == 2) {
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                const int64_t i = i0 + (int64_t)BS * j;
+                if (i < n_units) {
+                    uint4 o = v0[j];
+                    o.x ^= v1[j].z;
+                    st16<true>(out0 + i * 16, o);
+                }
+            }
+        }
 #pragma unroll
         for (int j = 0; j < U; ++j) acc ^= v0[j].y ^ v1[j].z;
         const uint32_t z = X ? wave_token(acc) : (acc & 1u);
@@ -128,7 +145,7 @@ __global__ __launch_bounds__(BS) void probe_flat_kernel(uint8_t* out0, uint8_t* 
             if (i < n_units) {
                 v0[j].x ^= z;
                 v1[j].x ^= z;
-                st16<true>(out0 + i * 16, v0[j]);
+                if constexpr (XM != 2) st16<true>(out0 + i * 16, v0[j]);
                 if (out1) st16<true>(out1 + i * 16, v1[j]);
             }
         }
@@ -303,7 +320,8 @@ extern "C" int jinf_probe_stream_layout(void* out0, void* out1, const void* in0,
     const int U = units_per_lane;
     const int B = block_lanes;
     if (n_units < 0 || (U != 1 && U != 2 && U != 4) || max_groups < 0 ||
-        (B != 64 && B != 128 && B != 256 && B != 512 && B != 1024))
+        (B != 64 && B != 128 && B != 256 && B != 512 && B != 1024) || exchange < 0 ||
+        exchange > 2)
         return JINF_HIP_ERR_INVALID;
     if (n_units == 0) return JINF_HIP_OK;
     if (!out0 || !in0 || !al16(out0) || !al16(in0) || (out1 && !al16(out1)) ||
@@ -317,13 +335,12 @@ extern "C" int jinf_probe_stream_layout(void* out0, void* out1, const void* in0,
                       static_cast<uint8_t*>(out1), static_cast<const uint8_t*>(in0),
                       static_cast<const uint8_t*>(in1), n_units);
     };
+#define JINF_PROBE_FLAT_X(XM, BS)                                                           \
+    (U == 1 ? go(probe_flat_kernel<1, XM, BS>)                                              \
+            : U == 2 ? go(probe_flat_kernel<2, XM, BS>) : go(probe_flat_kernel<4, XM, BS>))
 #define JINF_PROBE_FLAT(BS)                                                                 \
-    (exchange ? (U == 1 ? go(probe_flat_kernel<1, true, BS>)                                \
-                        : U == 2 ? go(probe_flat_kernel<2, true, BS>)                       \
-                                 : go(probe_flat_kernel<4, true, BS>))                      \
-              : (U == 1 ? go(probe_flat_kernel<1, false, BS>)                               \
-                        : U == 2 ? go(probe_flat_kernel<2, false, BS>)                      \
-                                 : go(probe_flat_kernel<4, false, BS>)))
+    (exchange == 2 ? JINF_PROBE_FLAT_X(2, BS)                                               \
+                   : exchange ? JINF_PROBE_FLAT_X(1, BS) : JINF_PROBE_FLAT_X(0, BS))
     switch (B) {
         case 64: return JINF_PROBE_FLAT(64);
         case 128: return JINF_PROBE_FLAT(128);
@@ -332,6 +349,7 @@ extern "C" int jinf_probe_stream_layout(void* out0, void* out1, const void* in0,
         default: return JINF_PROBE_FLAT(1024);
     }
 #undef JINF_PROBE_FLAT
+#undef JINF_PROBE_FLAT_X
 }
 
 extern "C" int jinf_probe_read_layout(const void* in, int64_t n_units, void* sink,

@@ -473,10 +473,12 @@ def probe_stream(out0, in0, out1=None, in1=None, units_per_lane=1, exchange=True
 def probe_stream_layout(out0, in0, out1=None, in1=None, units_per_lane=1, exchange=True,
                         block_lanes=256, max_groups=0):
     """probe_stream in a chosen launch layout: block_lanes lanes per workgroup,
-    one pass (max_groups 0) or a grid-stride loop over max_groups workgroups."""
+    one pass (max_groups 0) or a grid-stride loop over max_groups workgroups;
+    exchange False / True, or 2: out0 stored straight after its own loads,
+    out1 after the cross-lane exchange."""
     nbytes = out0.numel() * out0.element_size()
     _check(lib().jinf_probe_stream_layout(_ptr(out0), _ptr(out1), _ptr(in0), _ptr(in1),
-                                          nbytes // 16, int(units_per_lane), int(bool(exchange)),
+                                          nbytes // 16, int(units_per_lane), int(exchange),
                                           int(block_lanes), int(max_groups), _stream()),
            "jinf_probe_stream_layout")
 
