@@ -926,7 +926,7 @@ def cpu_baseline(ks, threads, budget_s):
             t0 = time.perf_counter()
             fn()
             times.append(time.perf_counter() - t0)
-            if time.perf_counter() > t_end and len(times) >= 3:
+            if time.perf_counter() > t_end and len(times) >= 10:
                 break
         out[k.key] = (sorted(times)[len(times) // 2], len(times))
     oracle.set_threads(1)
@@ -965,17 +965,25 @@ def cpu_baseline_both(ks, ks70, args):
     def per(t):
         return {k.key: round(k.nbytes / runs[t][k.key][0] / 1e9, 3) for k in ks + ks70}
 
+    def per_us(t):
+        return {k.key: round(runs[t][k.key][0] * 1e6, 1) for k in ks + ks70}
+
+    def per_rows(t):
+        return {k.key: round(k.rows / runs[t][k.key][0], 1) for k in ks + ks70}
+
     v_all, s_all = rate(ks, n_all)
     v_one, s_one = rate(ks, 1)
     out = {"value": v_all, "unit": "GB/s", "cores": n_all, "kind": "port",
-           "s_per_step": s_all, "per_kernel_GBs": per(n_all),
+           "s_per_step": s_all, "per_kernel_GBs": per(n_all), "per_kernel_us": per_us(n_all),
+           "per_kernel_rows_per_s": per_rows(n_all),
            "single_thread": {"value": v_one, "unit": "GB/s", "cores": 1, "s_per_step": s_one,
-                             "per_kernel_GBs": per(1)},
+                             "per_kernel_GBs": per(1), "per_kernel_us": per_us(1),
+                             "per_kernel_rows_per_s": per_rows(1)},
            "runs": {k.key: [runs[1][k.key][1], runs[n_all][k.key][1]] for k in ks + ks70},
            "host_cores": os.cpu_count(), "usable_cores": aff,
            "cpu_model": cpu_model(), "cpu_info": cpu_info(),
            "sample": (f"every kernel of the step (configs 2-4) and of config 5 at full shape on "
-                      f"a host copy of buffer set 0; median of >= 3 runs after a warm-up, about "
+                      f"a host copy of buffer set 0; median of >= 10 runs after a warm-up, about "
                       f"{budget:.0f} s per thread count; oracle C restatement ({oracle_build()}, "
                       f"-O3, no FMA contraction, no fast-math), 1 thread and {n_all} "
                       f"OpenMP threads")}
