@@ -10,7 +10,9 @@
  * units_per_lane (1, 2 or 4) sets how many units each lane moves per array,
  * all loads issued before any store; exchange != 0 makes every store of a
  * wave wait for all of the wave's loads (one cross-lane permute), exchange 0
- * lets each lane store after its own loads.  bench.py takes the fastest
+ * lets each lane store after its own loads (jinf_probe_stream_layout's
+ * exchange 2: the first output after its own loads, the second after the
+ * permute).  bench.py takes the fastest
  * variant as a kernel's ceiling.  Work is asynchronous on `stream`; nothing
  * allocates.  Return 0, or 5 for an invalid argument (nothing enqueued), or
  * 3 if the launch failed.

@@ -131,7 +131,7 @@ __global__ __launch_bounds__(BS) void probe_flat_kernel(uint8_t* out0, uint8_t* 
                 const int64_t i = i0 + (int64_t)BS * j;
                 if (i < n_units) {
                     uint4 o = v0[j];
-                    o.x ^= v1[j].z;
+                    o.x ^= v1[j].z & 1u;
                     st16<true>(out0 + i * 16, o);
                 }
             }
