@@ -466,7 +466,7 @@ def workload(name, torch, jinf, seed):
                "shapes": "Llama-3-8B layer projections at batch 1 (decode): "
                "q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096, down 4096x14336, Q4_0 "
                "weights, fp32 x/y", "storage": "Q4_0 weights, f32 vectors",
-               "baseline_configs": [], "note": "SURVEY 8(f) f1, next component"}
+               "baseline_configs": [], "note": "batch-1 dequant-GEMVs, beside the hot path"}
     elif name in ("llama3-8b-gemv-q4_k_m", "llama3-8b-gemv-q8_0"):
         H, F, KV = 4096, 14336, 1024
         if name.endswith("q8_0"):
@@ -483,7 +483,7 @@ def workload(name, torch, jinf, seed):
                "shapes": "Llama-3-8B layer projections at batch 1 (decode): "
                "q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096, down 4096x14336, " + desc,
                "storage": desc + ", f32 vectors", "baseline_configs": [],
-               "note": "SURVEY 8(f) f1, next component"}
+               "note": "batch-1 dequant-GEMVs, beside the hot path"}
     elif name == "llama3-70b-attention":
         pos = torch.randint(0, 8192, (64,), generator=g, device="cuda", dtype=torch.int32)
         ks = [build_attention(torch, jinf, g, "gqa_attention", 64, 8192, 64, 8, 128, pos + 1,
@@ -492,7 +492,7 @@ def workload(name, torch, jinf, seed):
                "shapes": "Llama-3-70B decode attention, 64 sequences: 64/8 heads x 128, "
                "KV cache [64, 8192, 8 x 128] fp16, len = pos + 1, pos ~ U[0, 8192)",
                "storage": "f16 KV cache", "baseline_configs": [5],
-               "note": "SURVEY 8(f) f2, next component (config 5's sequences and lengths)"}
+               "note": "decode attention at config 5's sequences and lengths"}
     elif name == "llama3-8b-attention-b1":
         lens = torch.full((1,), 4096, dtype=torch.int32, device="cuda")
         ks = [build_attention(torch, jinf, g, "gqa_attention_b1", 1, 4096, 32, 8, 128, lens,
@@ -501,7 +501,7 @@ def workload(name, torch, jinf, seed):
                "shapes": "Llama-3-8B decode attention through the reference's drop-in "
                "jinf_cuda_attention: one sequence, 32/8 heads x 128, fp32 cache, n_past 4096",
                "storage": "f32 KV cache", "baseline_configs": [],
-               "note": "SURVEY 8(f) f2, batch 1"}
+               "note": "decode attention, batch 1, the reference's drop-in"}
     elif name == "llama3-8b-attention-b1-f16":
         lens = torch.full((1,), 8192, dtype=torch.int32, device="cuda")
         ks = [build_attention(torch, jinf, g, "gqa_attention_b1_f16", 1, 8192, 32, 8, 128, lens,
@@ -511,7 +511,7 @@ def workload(name, torch, jinf, seed):
                "with a workspace (context split over 1024-position chunks): 32/8 heads x 128, "
                "fp16 cache, 8192 positions",
                "storage": "f16 KV cache", "baseline_configs": [],
-               "note": "SURVEY 8(f) f2, batch 1 with split contexts"}
+               "note": "decode attention, batch 1, split contexts"}
     elif name in ("rope", "norm", "swiglu", "gather", "softmax"):
         b = {"rope": lambda: build_rope(torch, jinf, g, 512, 32, 8, 128,
                                         torch.arange(512, dtype=torch.int32, device="cuda"), keep),
@@ -704,7 +704,7 @@ def batch_bench(args, torch, jinf_amd, spec):
                    "weight_bytes_per_step": wbytes,
                    "kv_bytes_per_step_mean": int(kv_bytes),
                    "context": [start_pos, start_pos + args.steps],
-                   "note": "SURVEY 8(f) f4, the engine forward loop with a batched-decode KV cache"},
+                   "note": "the engine's batched decode loop, batched KV cache"},
         "frac_of_peak": round(gbs / PEAK_GBS, 4),
         "launch": "eager stream" if args.no_graph else "HIP graph per step",
         "wall_s_timed": round(dec_s, 4),
@@ -889,7 +889,7 @@ def engine_bench(args, torch, jinf_amd):
                    "weight_bytes_per_token": wbytes,
                    "kv_bytes_per_token_mean": int(kv_bytes),
                    "context": [start_pos, start_pos + args.steps],
-                   "baseline_configs": [], "note": "SURVEY 8(f) f4, the engine forward loop"},
+                   "baseline_configs": [], "note": "the engine forward loop"},
         "frac_of_peak": round(gbs / PEAK_GBS, 4),
         "launch": "eager stream" if args.no_graph else "HIP graph per token",
         "wall_s_timed": round(dec_s, 4),

@@ -5,7 +5,7 @@
  * resident-weight engine of engine_hip.h.  Linkage differs: the reference
  * declares these functions with C++ linkage (mangled names), this library
  * exports them extern "C", so a caller compiles against this header or a
- * stand-in engine.h that declares them extern "C" (INTEGRATION.md shows one),
+ * stand-in engine.h that declares the same prototypes inside extern "C",
  * not against the reference's engine.h unchanged.  Status returns are the
  * reference's jinf_status values (an int-sized enum there, int here), 0 OK,
  * 1 I/O, 2 parse, 3 device, 4 out of memory, 5 invalid.
