@@ -432,13 +432,17 @@ __device__ __forceinline__ void am_merge_last(float* __restrict__ out, int64_t l
 // zero between calls) or, counters == nullptr, attn_combine_kernel does.
 typedef short am_tr4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) am_tr4 am_lds_tr4;
+// The parameters the prologue needs before the first K / V loads lead the
+// list: the first 14 dwords arrive preloaded in SGPRs, so those loads wait
+// for one scalar round trip (the sequence's length), not for several.  (q's
+// loads, which need later arguments, stay in flight behind K's.)
 template <int HD, bool MERGE, bool RB>
 __global__ __launch_bounds__(256) void attn_mfma_kernel(
-    float* __restrict__ out, int64_t ld_out, const float* __restrict__ q, int64_t ld_q,
+    const int32_t* __restrict__ lens, int n_past, int chunk, int G, int group,
     const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t ld_pos,
-    int64_t ld_seq, const int32_t* __restrict__ lens, int n_past, int group, int G,
-    int n_heads, float scale, float* __restrict__ ws, unsigned* __restrict__ counters,
-    int chunk, uint8_t* __restrict__ xrec, int xmt) {
+    int64_t ld_seq, const float* __restrict__ q, int64_t ld_q, int n_heads, float scale,
+    float* __restrict__ out, int64_t ld_out, float* __restrict__ ws,
+    unsigned* __restrict__ counters, uint8_t* __restrict__ xrec, int xmt) {
     constexpr int KS = HD / 16;        // k-steps of the score product
     constexpr int DPG = HD / 4;        // dims per lane group in the score product
     constexpr int KLD = DPG / 8;       // 16-byte K loads per position block
@@ -467,6 +471,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     const int s = blockIdx.y;
     const int cix = blockIdx.z;
     const int h0 = blockIdx.x * G;
+    // The sequence's length is the one load ahead of the K / V loads (their
+    // bounds need it); every argument they need arrives preloaded.
     const int j = h0 / group;
     const int len = lens ? min(max(lens[s], 0), n_past) : n_past;
     const int c0 = cix * chunk;
@@ -479,17 +485,6 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     const uint16_t* kb = kc + (int64_t)s * ld_seq + (int64_t)j * HD;
     const uint16_t* vb = vc + (int64_t)s * ld_seq + (int64_t)j * HD;
 
-    // Q' fragments of this lane's column (zero for unused head slots): the
-    // lane's DPG contiguous q values, loaded unconditionally.  The loads are
-    // issued here and converted after the first tile's K / V loads have been
-    // issued (below), so the q and K / V fetches are in flight together.
-    float4 qraw[KS];
-    {
-        const float4* qp = reinterpret_cast<const float4*>(
-            q + (int64_t)s * ld_q + (int64_t)(h0 + (slot < G ? slot : 0)) * HD + DPG * lg);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qraw[ks] = qp[ks];
-    }
 
     float m = -INFINITY, lsum = 0.0f;
     am_f4 O[NB];
@@ -530,14 +525,16 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
         koff[ii] = (uint32_t)row * rowb + 16u * (uint32_t)((slot_i % VCH) ^ kswz(row));
         voff[ii] = (uint32_t)row * rowb + 16u * (uint32_t)((slot_i % VCH) ^ (2 * (row & 3)));
     }
-    auto load_k = [&](int t0) {
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only: K buffer reads are done
+    // (first: nothing has read the buffers yet, so no wait; that wait would
+    // also take in the scalar loads of later kernel arguments)
+    auto load_k = [&](int t0, bool first = false) {
+        if (!first) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only: K buffer reads are done
         const uint32_t so = (uint32_t)(t0 - c0) * rowb;
 #pragma unroll
         for (int ii = 0; ii < VLDW; ++ii) lds_load16_buf(krs, koff[ii], so, kst + 1024 * (i0 + ii));
     };
-    auto load_v = [&](int t0) {
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only: V buffer reads are done
+    auto load_v = [&](int t0, bool first = false) {
+        if (!first) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only: V buffer reads are done
         const uint32_t so = (uint32_t)(t0 - c0) * rowb;
 #pragma unroll
         for (int ii = 0; ii < VLDW; ++ii) lds_load16_buf(vrs, voff[ii], so, vst + 1024 * (i0 + ii));
@@ -547,8 +544,19 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     const int tfirst = RB ? c0 : c0 + wave * kAtTile;
     const int wrow = RB ? 16 * wave : 0;
     if (tfirst + wrow < c1) {
-        load_k(tfirst);
-        load_v(tfirst);
+        load_k(tfirst, true);
+        load_v(tfirst, true);
+    }
+    // Q' fragments of this lane's column (zero for unused head slots): the
+    // lane's DPG contiguous q values, loaded unconditionally after the first
+    // tile's K / V loads (q's arguments are not among the preloaded ones, and
+    // its loads stay in flight behind K's) and converted below.
+    float4 qraw[KS];
+    {
+        const float4* qp = reinterpret_cast<const float4*>(
+            q + (int64_t)s * ld_q + (int64_t)(h0 + (slot < G ? slot : 0)) * HD + DPG * lg);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qraw[ks] = qp[ks];
     }
     // q' = q * scale as fp16 hi / lo parts (the compiler's wait for the q
     // loads also covers the K / V loads issued after them: in-order counts)
@@ -926,10 +934,10 @@ static int am_launch(float* out, int64_t ld_out, const float* q, int64_t ld_q, c
     if (xr && xr->rec && !split && xr->chunk_cols == G * HD && (xr->mt == 1 || xr->mt == 2) &&
         n_seq <= 32 * xr->mt)
         xrec = xr->rec;
-    const int st = launch(kern, dim3(n_heads / G, n_seq, nch), dim3(256), shmem, stream, out,
-                          ld_out, q, ld_q, static_cast<const uint16_t*>(k),
-                          static_cast<const uint16_t*>(v), ld_pos, ld_seq, lens, n_past, group,
-                          G, n_heads, scale, ws, counters, chunk, xrec, xr ? xr->mt : 1);
+    const int st = launch(kern, dim3(n_heads / G, n_seq, nch), dim3(256), shmem, stream, lens,
+                          n_past, chunk, G, group, static_cast<const uint16_t*>(k),
+                          static_cast<const uint16_t*>(v), ld_pos, ld_seq, q, ld_q, n_heads,
+                          scale, out, ld_out, ws, counters, xrec, xr ? xr->mt : 1);
     if (xr) xr->wrote = st == JINF_HIP_OK && xrec != nullptr;
     if (st != JINF_HIP_OK || !split || in_kernel) return st;
     return launch(attn_combine_kernel, dim3(n_heads, n_seq), dim3(HD), 0, stream, out, ld_out,
