@@ -89,15 +89,18 @@ template <> struct MbFmt<kQ6_K> { static constexpr int SB = 210; };
 // a Q6_K slab (210 bytes) starts at an even offset, so 14 chunks cover it.
 template <int QT> constexpr int mb_nch() { return QT == kQ6_K ? 14 : MbFmt<QT>::SB / 16; }
 
+// The fields the GEMV's first weight and x loads need come first: the first
+// 14 dwords of the kernel arguments arrive preloaded in SGPRs.
 struct MbJob {
-    const uint8_t* W[3];   // segment matrices (same format and width)
-    int seg_end[3];        // virtual row where each segment ends
-    int64_t row_bytes;
     int rows;              // virtual rows; kMbEpiSwiGLU: output rows
-    int n_slabs, n_groups, k_splits, slabs_per_split;
+    int n_slabs, n_groups, slabs_per_split;
+    const uint8_t* W[3];   // segment matrices (same format and width)
+    int64_t row_bytes;
+    const uint8_t* xrec;   // prepared x records [n_slabs][mb_rec(MT)]
+    int seg_end[3];        // virtual row where each segment ends
+    int k_splits;
     const float* x;        // [n_batch][ld_x]
     int ld_x, n_batch;
-    const uint8_t* xrec;   // prepared x records [n_slabs][mb_rec(MT)]
     float* y;              // [n_batch][ld_y]
     int ld_y;
     void* kc;              // kMbEpiQKV: caches [n_batch][ld_seq], rows [max_ctx][kv_dim]
@@ -534,9 +537,9 @@ __device__ __forceinline__ void mb_qkv_store(const MbJob& j, const RopeTheta& th
 // and v may each have their own), finished by one epilogue launch: (sequence,
 // row pair) items [pairs[g - 1], pairs[g]) belong to job g.
 struct MbQkvJobs {
-    MbJob j[3];
-    int pairs[3];
+    int pairs[3];  // first: each lane's first test needs them
     int n;
+    MbJob j[3];
 };
 
 // The Q / K / V epilogue after deferred column splits: one lane per row pair
