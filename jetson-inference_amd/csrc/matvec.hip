@@ -411,15 +411,18 @@ __device__ __forceinline__ int mv_xslot(int tile, int l, int j) {
 enum MvPro { kProNone = 0, kProNorm = 1 };
 enum MvEpi { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2, kEpiQKV = 3 };
 
+// The fields the first loads (x, the norm weight, the first weight rows)
+// need come first: the first 14 dwords of the kernel arguments arrive
+// preloaded in SGPRs.
 struct MvJob {
+    const float* x;         // x, or h for kProNorm
+    const void* norm_w;     // kProNorm: g (fp32 or fp16)
     const uint8_t* W[3];    // segment matrices (same format and width)
-    int seg_end[3];         // kEpiQKV: virtual row where each segment ends
     int64_t row_bytes;
     int rows;               // virtual rows; kEpiSwiGLU: output rows
     int nb;                 // blocks per row
     int nt;                 // column tiles
-    const float* x;         // x, or h for kProNorm
-    const void* norm_w;     // kProNorm: g (fp32 or fp16)
+    int seg_end[3];         // kEpiQKV: virtual row where each segment ends
     int norm_f16;
     float eps;
     float* y;
