@@ -819,15 +819,25 @@ __global__ __launch_bounds__(64 * WV, 4 * mb_occ<MT>() / WV) void matvec_batch_k
                     constexpr int NSB = KPW / 2;  // sub-blocks of this wave
                     const float d = h2f((uint16_t)lds_u16(rb[nt]));
                     const float dmin = h2f((uint16_t)lds_u16(rb[nt] + 2));
-                    uint32_t sw[3];
-#pragma unroll
-                    for (int k = 0; k < 3; ++k) sw[k] = lds_u32(rb[nt] + 4 + 4 * k);
+                    // the wave's sub-blocks' 6-bit scale and minimum (the
+                    // q4_K_scale_min packing) from the bytes that hold them:
+                    // the sub-block index is wave-uniform, so each is one
+                    // byte read rather than a select among the 12 bytes
+                    const uint8_t* sb8 = rb[nt] + 4;
                     float mn[NSB];
                     _Float16 f[NSB];
 #pragma unroll
                     for (int q = 0; q < NSB; ++q) {
+                        const int sb = k0 / 2 + q;
                         int sc, m;
-                        q4_K_scale_min(sw, k0 / 2 + q, sc, m);
+                        if (sb < 4) {
+                            sc = sb8[sb] & 0x3F;
+                            m = sb8[sb + 4] & 0x3F;
+                        } else {
+                            const int hi = sb8[sb + 4];
+                            sc = ((hi & 0x0F) << 2) | (sb8[sb - 4] >> 6);
+                            m = ((hi >> 4) << 2) | (sb8[sb] >> 6);
+                        }
                         f[q] = (_Float16)(float)sc;
                         mn[q] = dmin * (float)m;
                     }
