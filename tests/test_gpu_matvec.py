@@ -61,6 +61,22 @@ def test_llama_shapes(dev, qtype, rows, cols):
     check(y, ref, a, f"{NAMES[qtype]} {rows}x{cols}")
 
 
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("rows,cols", [(1024, 4096), (512, 14336), (40000, 4096), (9, 2048)])
+def test_extreme_codes(dev, qtype, rows, cols):
+    """Every code and sub-block scale at its limit (Q4_0 nibbles 0 / 15, Q8_0
+    -128 / 127, Q4_K scales and minimums 63, Q6_K codes -32 / 31 under
+    sub-block scales -128 / 127): one-tile, multi-tile, tall and generic
+    kernels."""
+    say(f"{NAMES[qtype]} matvec extreme codes rows={rows} cols={cols}")
+    r = tu.rng(977 + rows + cols + qtype)
+    W = tu.extreme_quant_table(r, qtype, rows, cols)
+    x = tu.normal(r, (cols,), 0.0, 1.0, np.float32)
+    ref, a = _oracle(qtype, W, x)
+    y = host(jinf_amd.matvec(to_dev(W), to_dev(x), qtype))
+    check(y, ref, a, f"{NAMES[qtype]} extreme {rows}x{cols}")
+
+
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (20000, 4096), (7, 128), (1, 64)])
 def test_q4_0_entry_point(dev, rows, cols):
     say(f"jinf_matvec_q4_0 rows={rows} cols={cols}")

@@ -86,6 +86,22 @@ def test_matvec_batch(dev, qtype, rows, cols, n_batch):
         assert np.all(y[1] == 0.0)
 
 
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: NAMES[q])
+@pytest.mark.parametrize("rows,cols,n_batch", [(256, 4096, 32), (4096, 4096, 40),
+                                               (64, 14336, 7)])
+def test_matvec_batch_extreme_codes(dev, qtype, rows, cols, n_batch):
+    """Every code and sub-block scale at its limit: the decodes into the
+    matrix-core operands (one M-tile, two M-tiles, split columns) stay exact."""
+    say(f"matvec_batch extreme codes {NAMES[qtype]} {rows}x{cols} batch {n_batch}")
+    r = tu.rng(911 + qtype + rows + n_batch)
+    W = tu.extreme_quant_table(r, qtype, rows, cols)
+    X = batch_x(r, n_batch, cols)
+    ref, a = mv_rows(qtype, W, X)
+    ws = jinf_amd.matvec_batch_workspace(rows, cols, n_batch)
+    y = host(jinf_amd.matvec_batch(to_dev(W), to_dev(X), qtype, workspace=ws))
+    check(y, ref, 1e-5 * a, "extreme codes")
+
+
 def test_matvec_batch_row_stride_and_one_token_agrees(dev):
     """Rows of x and y with padding between them; batch row b equals the
     batch-of-one result for x[b] up to the GEMV bar."""

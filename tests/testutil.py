@@ -50,6 +50,34 @@ def quant_table(r, qtype, n_rows, n_cols, scale_sigma=0.01):
     return blk.reshape(n_rows, nb * nbytes)
 
 
+def extreme_quant_table(r, qtype, n_rows, n_cols):
+    """quant_table rows whose codes and sub-block scales sit at their format's
+    limits: Q4_0 nibbles 0 / 15; Q8_0 codes -128 / 127; Q4_K 6-bit scales and
+    minimums all 63 (scale bytes 0xFF) with nibbles 0 / 15 (sc * q reaches
+    945); Q6_K codes 0 / 63 (q - 32 = -32 / 31, high bits 00 / 11) under int8
+    sub-block scales -128 / 127.  The fp16 block scales stay quant_table's."""
+    W = quant_table(r, qtype, n_rows, n_cols).copy()
+    elems, nbytes = {2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}[qtype]
+    B = W.reshape(n_rows, n_cols // elems, nbytes)
+
+    def pick(choices, n):
+        idx = r.integers(0, len(choices), size=B.shape[:2] + (n,))
+        return np.asarray(choices, np.uint8)[idx]
+
+    if qtype == 2:
+        B[:, :, 2:18] = pick([0x00, 0xFF, 0x0F, 0xF0], 16)
+    elif qtype == 8:
+        B[:, :, 2:34] = pick([0x80, 0x7F], 32)
+    elif qtype == 12:
+        B[:, :, 4:16] = 0xFF
+        B[:, :, 16:144] = pick([0x00, 0xFF, 0x0F, 0xF0], 128)
+    else:
+        B[:, :, 0:128] = pick([0x00, 0xFF, 0x0F, 0xF0], 128)
+        B[:, :, 128:192] = pick([0x00, 0xFF, 0x33, 0xCC], 64)
+        B[:, :, 192:208] = pick([0x80, 0x7F], 16)
+    return B.reshape(n_rows, -1)
+
+
 def q4_0_blocks(d_bits, qs):
     """Build blocks from fp16 scale bit patterns [n] and nibble bytes [n, 16]."""
     d_bits = np.asarray(d_bits, dtype=np.uint16)
