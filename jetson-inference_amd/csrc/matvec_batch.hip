@@ -1109,8 +1109,17 @@ constexpr MbShape kMbNarrow{2, 4, 4};
 // 28672 x 4096: 47.6 against 59.7 us) and smaller targets (4096 x 14336:
 // 26.4 us at 512 workgroups, 35.9 at 256).
 constexpr int kMbSplitTarget = 512;
-int mb_split(int n_groups, int n_slabs, int* slabs_per_split) {
-    int k = kMbSplitTarget / n_groups;
+// The Q / K / V launch at two M-tiles (more than 32 sequences): two splits of
+// the 4096 columns instead of four, at most one 8-wave workgroup per CU (Llama-3-8B,
+// batch 64: step 5.48 -> 5.31 ms; at 32 sequences two splits measured 3.23
+// against 3.24 ms for Q4_0 and 4.17 against 4.07 for Q4_K_M, so one M-tile
+// keeps the common target; 8 or 16 splits, or none, were slower).
+constexpr int kMbQkvWideSplitTarget = 192;
+constexpr int mb_split_target(int epi, int n_batch) {
+    return epi == kMbEpiQKV && n_batch > 32 ? kMbQkvWideSplitTarget : kMbSplitTarget;
+}
+int mb_split(int n_groups, int n_slabs, int* slabs_per_split, int target = kMbSplitTarget) {
+    int k = target / n_groups;
     if (k > n_slabs) k = n_slabs;
     if (k < 1) k = 1;
     const int per = (n_slabs + k - 1) / k;
@@ -1137,7 +1146,7 @@ size_t mb_ctr_bytes(int n_groups) {
 size_t mb_ws_bytes(const MbShape& sh, int epi, int out_rows, int n_slabs, int mt) {
     const int groups = (out_rows + sh.rows_per_group(epi) - 1) / sh.rows_per_group(epi);
     int per;
-    const int k = mb_split(groups, n_slabs, &per);
+    const int k = mb_split(groups, n_slabs, &per, mb_split_target(epi, 32 * mt));
     const size_t parts = k > 1 ? (size_t)groups * k * sh.nt * mt * 1024 * 4 : 0;
     return mb_ctr_bytes(groups) + (size_t)n_slabs * mb_rec(mt) + parts;
 }
@@ -1284,7 +1293,8 @@ int mb_prepare(MbJob& j, MbShape& sh, int qtype, int epi, int rows, int cols, in
                  "jinf_matvec_batch_workspace_bytes()");
         return JINF_HIP_ERR_INVALID;
     }
-    j.k_splits = mb_split(j.n_groups, j.n_slabs, &j.slabs_per_split);
+    j.k_splits =
+        mb_split(j.n_groups, j.n_slabs, &j.slabs_per_split, mb_split_target(epi, n_batch));
     char* w = static_cast<char*>(ws);
     j.counters = reinterpret_cast<uint32_t*>(w);
     j.xrec = reinterpret_cast<uint8_t*>(w + mb_ctr_bytes(j.n_groups));
@@ -1320,7 +1330,7 @@ size_t matvec_batch_ws_bytes(int rows, int cols, int n_batch) {
         return 0;
     const int mt = n_batch > 32 ? 2 : 1, n_slabs = cols / kMbCols;
     size_t most = 0;
-    for (int epi : {kMbEpiStore, kMbEpiSwiGLU}) {
+    for (int epi : {kMbEpiStore, kMbEpiSwiGLU, kMbEpiQKV}) {
         const size_t b = mb_ws_bytes(mb_shape(), epi, rows, n_slabs, mt);
         most = b > most ? b : most;
     }
@@ -1552,6 +1562,21 @@ int rmsnorm_qkv_rope_batch_mixed(const void* const w[3], const int types[3], flo
                   stream, js, th);
 }
 
+// Deferred partial sums of a launch with epilogue epi (kMbEpiAdd or
+// kMbEpiQKV, both 64-row groups): the splits' partials, then the residual
+// merge's slice statistics (fp64 sums, fp32 maxima).
+static size_t mb_defer_bytes(int rows, int cols, int n_batch, int epi) {
+    if (rows <= 0 || cols <= 0 || cols % kMbCols != 0 || cols > kMbMaxCols || n_batch <= 0 ||
+        n_batch > kMbMaxBatch)
+        return 0;
+    const MbShape sh = mb_shape();
+    const int groups = (rows + sh.rows_per_group(epi) - 1) / sh.rows_per_group(epi);
+    int per;
+    const int k = mb_split(groups, cols / kMbCols, &per, mb_split_target(epi, n_batch));
+    const size_t slices = (size_t)(rows + kMbSliceCols - 1) / kMbSliceCols;
+    return (size_t)k * n_batch * rows * sizeof(float) + slices * n_batch * (8 + 4);
+}
+
 size_t qkv_defer_bytes(const int types[3], int q_dim, int kv_dim, int n_embd, int n_batch) {
     const int dims[3] = {q_dim, kv_dim, kv_dim};
     bool done[3] = {false, false, false};
@@ -1564,8 +1589,7 @@ size_t qkv_defer_bytes(const int types[3], int q_dim, int kv_dim, int n_embd, in
                 rows += dims[k];
                 done[k] = true;
             }
-        // (matvec_batch_defer_bytes counts the same 64-row groups and splits)
-        total += mb_qkv_part_span(matvec_batch_defer_bytes(rows, n_embd, n_batch));
+        total += mb_qkv_part_span(mb_defer_bytes(rows, n_embd, n_batch, kMbEpiQKV));
     }
     return total;
 }
@@ -1587,16 +1611,7 @@ uint8_t* matvec_batch_add_xrec(void* workspace, int qtype, int rows, int cols, i
 }
 
 size_t matvec_batch_defer_bytes(int rows, int cols, int n_batch) {
-    if (rows <= 0 || cols <= 0 || cols % kMbCols != 0 || cols > kMbMaxCols || n_batch <= 0 ||
-        n_batch > kMbMaxBatch)
-        return 0;
-    const MbShape sh = mb_shape();
-    const int groups = (rows + sh.rows_per_group(kMbEpiAdd) - 1) / sh.rows_per_group(kMbEpiAdd);
-    int per;
-    const int k = mb_split(groups, cols / kMbCols, &per);
-    // the partials, then the merge's slice statistics (fp64 sums, fp32 maxima)
-    const size_t slices = (size_t)(rows + kMbSliceCols - 1) / kMbSliceCols;
-    return (size_t)k * n_batch * rows * sizeof(float) + slices * n_batch * (8 + 4);
+    return mb_defer_bytes(rows, cols, n_batch, kMbEpiAdd);
 }
 
 int matvec_batch_add_defer(const void* weight, int qtype, const float* x, int ld_x, int rows,
