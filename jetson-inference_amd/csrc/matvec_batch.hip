@@ -1109,14 +1109,16 @@ constexpr MbShape kMbNarrow{2, 4, 4};
 // 28672 x 4096: 47.6 against 59.7 us) and smaller targets (4096 x 14336:
 // 26.4 us at 512 workgroups, 35.9 at 256).
 constexpr int kMbSplitTarget = 512;
-// The Q / K / V launch at two M-tiles (more than 32 sequences): two splits of
-// the 4096 columns instead of four, at most one 8-wave workgroup per CU (Llama-3-8B,
-// batch 64: step 5.48 -> 5.31 ms; at 32 sequences two splits measured 3.23
-// against 3.24 ms for Q4_0 and 4.17 against 4.07 for Q4_K_M, so one M-tile
-// keeps the common target; 8 or 16 splits, or none, were slower).
-constexpr int kMbQkvWideSplitTarget = 192;
-constexpr int mb_split_target(int epi, int n_batch) {
-    return epi == kMbEpiQKV && n_batch > 32 ? kMbQkvWideSplitTarget : kMbSplitTarget;
+// One launch over two M-tiles (more than 32 sequences, every format but
+// Q6_K): its 8-wave workgroups take a CU each, so at most 256 of them, one
+// round, and fewer partials to merge (Llama-3-8B at batch 64: Q4_0 step 5.48
+// -> 5.07 ms, Q4_K_M 7.37 -> 7.14).  Q6_K's two one-tile launches keep the
+// common target (at 256: Q4_K_M 7.93 against 7.40 ms).  The sizes reported
+// for workspaces and deferred partials use the common target, which gives
+// the most splits.
+constexpr int kMbSplitTarget2 = 256;
+int mb_split_target(int qtype, int n_batch) {
+    return n_batch > 32 && qtype != kQ6_K ? kMbSplitTarget2 : kMbSplitTarget;
 }
 int mb_split(int n_groups, int n_slabs, int* slabs_per_split, int target = kMbSplitTarget) {
     int k = target / n_groups;
@@ -1146,7 +1148,7 @@ size_t mb_ctr_bytes(int n_groups) {
 size_t mb_ws_bytes(const MbShape& sh, int epi, int out_rows, int n_slabs, int mt) {
     const int groups = (out_rows + sh.rows_per_group(epi) - 1) / sh.rows_per_group(epi);
     int per;
-    const int k = mb_split(groups, n_slabs, &per, mb_split_target(epi, 32 * mt));
+    const int k = mb_split(groups, n_slabs, &per);  // the most splits of any format
     const size_t parts = k > 1 ? (size_t)groups * k * sh.nt * mt * 1024 * 4 : 0;
     return mb_ctr_bytes(groups) + (size_t)n_slabs * mb_rec(mt) + parts;
 }
@@ -1294,7 +1296,7 @@ int mb_prepare(MbJob& j, MbShape& sh, int qtype, int epi, int rows, int cols, in
         return JINF_HIP_ERR_INVALID;
     }
     j.k_splits =
-        mb_split(j.n_groups, j.n_slabs, &j.slabs_per_split, mb_split_target(epi, n_batch));
+        mb_split(j.n_groups, j.n_slabs, &j.slabs_per_split, mb_split_target(qtype, n_batch));
     char* w = static_cast<char*>(ws);
     j.counters = reinterpret_cast<uint32_t*>(w);
     j.xrec = reinterpret_cast<uint8_t*>(w + mb_ctr_bytes(j.n_groups));
@@ -1330,7 +1332,7 @@ size_t matvec_batch_ws_bytes(int rows, int cols, int n_batch) {
         return 0;
     const int mt = n_batch > 32 ? 2 : 1, n_slabs = cols / kMbCols;
     size_t most = 0;
-    for (int epi : {kMbEpiStore, kMbEpiSwiGLU, kMbEpiQKV}) {
+    for (int epi : {kMbEpiStore, kMbEpiSwiGLU}) {
         const size_t b = mb_ws_bytes(mb_shape(), epi, rows, n_slabs, mt);
         most = b > most ? b : most;
     }
@@ -1562,21 +1564,6 @@ int rmsnorm_qkv_rope_batch_mixed(const void* const w[3], const int types[3], flo
                   stream, js, th);
 }
 
-// Deferred partial sums of a launch with epilogue epi (kMbEpiAdd or
-// kMbEpiQKV, both 64-row groups): the splits' partials, then the residual
-// merge's slice statistics (fp64 sums, fp32 maxima).
-static size_t mb_defer_bytes(int rows, int cols, int n_batch, int epi) {
-    if (rows <= 0 || cols <= 0 || cols % kMbCols != 0 || cols > kMbMaxCols || n_batch <= 0 ||
-        n_batch > kMbMaxBatch)
-        return 0;
-    const MbShape sh = mb_shape();
-    const int groups = (rows + sh.rows_per_group(epi) - 1) / sh.rows_per_group(epi);
-    int per;
-    const int k = mb_split(groups, cols / kMbCols, &per, mb_split_target(epi, n_batch));
-    const size_t slices = (size_t)(rows + kMbSliceCols - 1) / kMbSliceCols;
-    return (size_t)k * n_batch * rows * sizeof(float) + slices * n_batch * (8 + 4);
-}
-
 size_t qkv_defer_bytes(const int types[3], int q_dim, int kv_dim, int n_embd, int n_batch) {
     const int dims[3] = {q_dim, kv_dim, kv_dim};
     bool done[3] = {false, false, false};
@@ -1589,7 +1576,8 @@ size_t qkv_defer_bytes(const int types[3], int q_dim, int kv_dim, int n_embd, in
                 rows += dims[k];
                 done[k] = true;
             }
-        total += mb_qkv_part_span(mb_defer_bytes(rows, n_embd, n_batch, kMbEpiQKV));
+        // (matvec_batch_defer_bytes counts the same 64-row groups and splits)
+        total += mb_qkv_part_span(matvec_batch_defer_bytes(rows, n_embd, n_batch));
     }
     return total;
 }
@@ -1603,7 +1591,7 @@ uint8_t* matvec_batch_add_xrec(void* workspace, int qtype, int rows, int cols, i
     const MbShape sh = mb_shape();
     const int groups = (rows + sh.rows_per_group(kMbEpiAdd) - 1) / sh.rows_per_group(kMbEpiAdd);
     int per;
-    const int k = mb_split(groups, cols / kMbCols, &per);
+    const int k = mb_split(groups, cols / kMbCols, &per, mb_split_target(qtype, n_batch));
     // (Q6_K at two M-tiles runs as two one-tile launches, each preparing its own)
     if (k > 1 && (cols / kMbCols) % per == 0 && (n_batch <= 32 || qtype != kQ6_K))
         *chunk_cols = per * kMbCols;
@@ -1611,7 +1599,16 @@ uint8_t* matvec_batch_add_xrec(void* workspace, int qtype, int rows, int cols, i
 }
 
 size_t matvec_batch_defer_bytes(int rows, int cols, int n_batch) {
-    return mb_defer_bytes(rows, cols, n_batch, kMbEpiAdd);
+    if (rows <= 0 || cols <= 0 || cols % kMbCols != 0 || cols > kMbMaxCols || n_batch <= 0 ||
+        n_batch > kMbMaxBatch)
+        return 0;
+    const MbShape sh = mb_shape();
+    const int groups = (rows + sh.rows_per_group(kMbEpiAdd) - 1) / sh.rows_per_group(kMbEpiAdd);
+    int per;
+    const int k = mb_split(groups, cols / kMbCols, &per);  // the most splits of any format
+    // the partials, then the merge's slice statistics (fp64 sums, fp32 maxima)
+    const size_t slices = (size_t)(rows + kMbSliceCols - 1) / kMbSliceCols;
+    return (size_t)k * n_batch * rows * sizeof(float) + slices * n_batch * (8 + 4);
 }
 
 int matvec_batch_add_defer(const void* weight, int qtype, const float* x, int ld_x, int rows,
