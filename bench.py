@@ -1229,7 +1229,8 @@ def main():
                          "holding STEPS steps")
     ap.add_argument("--no-f4", action="store_true",
                     help="default workload: skip the engine figures (batch-1 and batch-32 "
-                         "decode of the Q4_0 Llama-3-8B-shaped model)")
+                         "decode of the Q4_0 Llama-3-8B-shaped model) and the GEMV and "
+                         "attention figures (f1, f2)")
     ap.add_argument("--stream-curve", action="store_true",
                     help="print the geometry-free attainable stream rate per read:write mix "
                          "over transfer sizes 2-512 MB (a text table) and exit")
@@ -1417,6 +1418,35 @@ def main():
             f"{f4['batch1']['ms_per_token']} ms/token, batch 32 "
             f"{f4['batch32']['ms_per_step']} ms/step")
 
+    # the GEMV and attention rows: the seven batch-1 projections of
+    # --workload llama3-8b-gemv (each beside the read-only stream of its bytes)
+    # and the config-5-shaped decode attention of --workload
+    # llama3-70b-attention, each kernel alone over its rotating sets as above
+    f1 = f2 = None
+    if args.workload == "llama3-8b-layer" and not args.no_f4:
+        t0 = time.perf_counter()
+        ksg, cfg_g, keep_g = workload("llama3-8b-gemv", torch, jinf_amd, args.seed)
+        ksa, cfg_a, keep_a = workload("llama3-70b-attention", torch, jinf_amd, args.seed)
+        for k in ksg + ksa:
+            k.run()
+        torch.cuda.synchronize()
+        for k in ksg + ksa:
+            k.ms = timed(n_launch, [k])
+            k.n = n_launch
+        if not args.no_ceilings:
+            for k in ksg:
+                k.att_us, k.att_lay = attainable(torch, jinf_amd, timed, KERNEL_MIX[k.name],
+                                                 k.nbytes, n_launch)
+        f1 = {"workload": cfg_g["workload"], "shapes": cfg_g["shapes"],
+              "layer_us": round(sum(k.ms / k.n for k in ksg) * 1e3, 3),
+              "kernels": per_kernel(ksg, "llama3-8b-gemv")}
+        f2 = {"workload": cfg_a["workload"], "shapes": cfg_a["shapes"],
+              "kernels": per_kernel(ksa, "llama3-70b-attention")}
+        del ksg, ksa, keep_g, keep_a
+        log(f"GEMV and attention figures in {time.perf_counter() - t0:.1f} s: seven batch-1 "
+            f"GEMVs {f1['layer_us']} us, 70B-shape attention "
+            f"{f2['kernels']['gqa_attention']['us']} us")
+
     out = {
         "metric": METRIC,
         "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
@@ -1434,6 +1464,8 @@ def main():
         "wall_s_timed": round(wall, 4),
         "kernels": per,
         "config5": c5,
+        "f1": f1,
+        "f2": f2,
         "f4": f4,
         "roofline": roofline,
         "cpu_baseline": cpu,
