@@ -33,6 +33,7 @@
 // Anything the tiled kernel does not serve (unaligned pointers, widths that
 // are not a multiple of the format's tile granule, more than 7 tiles) takes a
 // one-wave-per-row kernel that decodes every weight exactly (quant_device.h).
+#include <atomic>
 #include <type_traits>
 
 #include "jinf_device.h"
@@ -937,6 +938,30 @@ __global__ __launch_bounds__(256) void matvec_any_kernel(MvJob job, MvTheta<EPI>
     if (lane == 0) mv_epilogue<QT, EPI>(job, th, g, v, nullptr, EPI == kEpiQKV ? job.pos[0] : 0);
 }
 
+// Workgroups of the tall one-tile kernel (these template arguments, `threads`
+// lanes, `shmem` bytes) that the device holds at once: its occupancy per CU
+// times the CUs.  Such a launch streams tens of items per wave, so it takes
+// every resident slot (the RMSNorm + Q6_K output head, 128256 x 4096, three
+// workgroups per CU: 80.0 -> 76.0-76.9 us at 768 workgroups against 512).
+// Queried once per kernel (metadata queries only, so also under stream
+// capture); 512 if a query fails.  The grid changes no row's arithmetic.
+template <int QT, int PRO, int EPI, int WV1>
+static int mv_tall_grid_cap(int threads, size_t shmem) {
+    static std::atomic<int> cap{0};
+    int c = cap.load(std::memory_order_relaxed);
+    if (c > 0) return c;
+    int per_cu = 0, dev = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, matvec_kernel<QT, true, PRO, EPI, WV1, true>, threads, shmem) != hipSuccess ||
+        per_cu < 1 || hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus < 1)
+        return 512;
+    c = per_cu * cus;
+    cap.store(c, std::memory_order_relaxed);
+    return c;
+}
+
 // Launch a job: the tiled kernel with at most 512 workgroups when the shape
 // and alignment allow it (single-tile matrices use 4 independent waves per
 // workgroup; wider ones 8 waves sharing one copy of x), else the
@@ -979,9 +1004,13 @@ static int mv_run(MvJob job, int cols, const MvTheta<EPI>& th, hipStream_t strea
             grid = (int)(((int64_t)n_groups + waves * kWave - 1) / (waves * kWave));
         const size_t shmem = ((size_t)job.nt * xt16 + (size_t)waves * stage_chunks) * 16;
         if constexpr (kTallable) {
-            if (tall)
-                return launch(matvec_kernel<QT, true, PRO, EPI, WV1, true>, dim3(grid),
-                              dim3(waves * kWave), shmem, stream, job, th);
+            if (tall) {
+                const int cap = mv_tall_grid_cap<QT, PRO, EPI, WV1>(waves * kWave, shmem);
+                const int want = (n_groups + waves - 1) / waves;
+                return launch(matvec_kernel<QT, true, PRO, EPI, WV1, true>,
+                              dim3(want < cap ? want : cap), dim3(waves * kWave), shmem, stream,
+                              job, th);
+            }
         }
         if (job.nt == 1)
             return launch(matvec_kernel<QT, true, PRO, EPI, WV1>, dim3(grid), dim3(waves * kWave),
