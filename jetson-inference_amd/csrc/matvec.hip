@@ -943,8 +943,10 @@ __global__ __launch_bounds__(256) void matvec_any_kernel(MvJob job, MvTheta<EPI>
 // times the CUs.  Such a launch streams tens of items per wave, so it takes
 // every resident slot (the RMSNorm + Q6_K output head, 128256 x 4096, three
 // workgroups per CU: 80.0 -> 76.0-76.9 us at 768 workgroups against 512).
-// Queried once per kernel (metadata queries only, so also under stream
-// capture); 512 if a query fails.  The grid changes no row's arithmetic.
+// Queried once per kernel and process, on the current device (metadata
+// queries only, so also under stream capture; a process whose devices differ
+// uses the first one's figure); 512 if a query fails.  The grid changes no
+// row's arithmetic, so no result depends on it.
 template <int QT, int PRO, int EPI, int WV1>
 static int mv_tall_grid_cap(int threads, size_t shmem) {
     static std::atomic<int> cap{0};
