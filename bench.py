@@ -715,6 +715,8 @@ def batch_bench(args, torch, jinf_amd, spec):
                      "traffic": traffic_from_profiles("decode_step", args.workload)},
         "cpu_baseline": cpu,
     }
+    if args.calibrate_copy:
+        calibrate_copy(torch)
     print(json.dumps(out_line), flush=True)
 
 
@@ -900,6 +902,8 @@ def engine_bench(args, torch, jinf_amd):
                      "traffic": traffic_from_profiles("decode_step", args.workload)},
         "cpu_baseline": cpu,
     }
+    if args.calibrate_copy:
+        calibrate_copy(torch)
     print(json.dumps(out_line), flush=True)
 
 
