@@ -72,3 +72,38 @@ def test_all_kernels_replay_bit_identical(dev):
         torch.cuda.synchronize()
         for n, b in bufs.items():
             assert tu.bits_equal(host(b), eager[n]), f"replay {rep}: {n}"
+
+
+@pytest.mark.parametrize("norm", [False, True], ids=["plain", "rmsnorm"])
+def test_tall_gemv_replays_bit_identical(dev, norm):
+    """The tall one-tile GEMV (rows >= 32768, Q6_K; its grid is the device's
+    resident workgroup count, queried once per process, also under capture)
+    captured in a graph: every replay, between eager launches of its own,
+    gives the eager bits."""
+    import oracle
+    r = tu.rng(93 + norm)
+    rows, cols = 40000, 4096
+    W = to_dev(tu.quant_table(r, oracle.Q6_K, rows, cols))
+    x = to_dev(tu.normal(r, (cols,), 0.0, 1.0, np.float32))
+    g = to_dev(tu.normal(r, (cols,), 1.0, 0.1, np.float32))
+    y = torch.empty(rows, dtype=torch.float32, device=dev)
+
+    def run(out):
+        if norm:
+            jinf_amd.rmsnorm_matvec(W, x, oracle.Q6_K, norm_w=g, eps=1e-5, y=out)
+        else:
+            jinf_amd.matvec(W, x, oracle.Q6_K, y=out)
+
+    # captured before any eager launch: in a process with no earlier tall
+    # launch the grid query runs under the capture
+    graph = _graph(lambda: run(y))
+    want = torch.empty_like(y)
+    run(want)
+    for i in range(3):
+        y.fill_(-1.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        say(f"tall gemv replay {i} ({'rmsnorm' if norm else 'plain'})")
+        assert tu.bits_equal(host(y), host(want)), f"replay {i}"
+        run(want)  # eager work between the replays
+        torch.cuda.synchronize()
