@@ -42,6 +42,10 @@ MODELS = {
     "hd96": dict(n_embd=384, n_heads=4, n_heads_kv=2, n_ff=768,
                  types={k: (mu.Q4_0, mu.Q8_0) for k in mu.MIXED}, embd_type=mu.F32,
                  out_type=mu.Q8_0, output_norm=False),
+    # q and k of one format, v of another (the Q4_K_M pattern): one Q/K/V
+    # launch per format, the second writing only the V rows
+    "qk-v-two-formats": dict(types=dict(mu.MIXED, attn_q=(mu.Q4_0, mu.Q4_K),
+                                        attn_k=(mu.Q4_0, mu.Q4_K), attn_v=(mu.Q8_0, mu.Q6_K))),
 }
 TOKENS = [5, 17, 999, 0, 42, 17, 3, 500]
 
