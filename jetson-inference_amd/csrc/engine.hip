@@ -217,11 +217,21 @@ int enqueue_embed(jinf_hip_engine* e) {
 }
 
 // Q, K and V projections of one layer with their RMSNorm, RoPE and cache
-// stores; matrices of one weight format share a launch.
+// stores; matrices of one weight format share a launch, and q and k of one
+// format with v of another (Q4_K_M) share one as well where the shapes allow.
 int enqueue_qkv(jinf_hip_engine* e, const jinf_hip_layer_weights& w, void* kc, void* vc) {
     const jinf_hip_engine_desc& d = e->d;
     const void* W[3] = {w.attn_q, w.attn_k, w.attn_v};
     const int T[3] = {w.attn_q_type, w.attn_k_type, w.attn_v_type};
+    if (T[0] == T[1] && T[2] != T[0] && w.attn_norm) {
+        bool launched = false;
+        ENG_TRY(rmsnorm_qkv_rope_two(W[0], W[1], T[0], W[2], T[2], e->hidden, w.attn_norm,
+                                     w.attn_norm_type, d.rms_norm_eps, d.n_embd, e->q, kc, vc,
+                                     d.kv_type, e->state + kPos, d.max_context, e->head_dim,
+                                     d.n_heads, d.n_heads_kv, d.rope_freq_base, e->stream,
+                                     &launched));
+        if (launched) return JINF_HIP_OK;
+    }
     bool done[3] = {false, false, false};
     for (int i = 0; i < 3; ++i) {
         if (done[i]) continue;

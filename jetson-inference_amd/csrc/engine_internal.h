@@ -25,4 +25,15 @@ void batch_set_pos(jinf_hip_batch* b, int pos);
 // Device word holding the borrowed sequence's last prefill argmax.
 const int32_t* batch_argmax(const jinf_hip_batch* b);
 
+// jinf_rmsnorm_qkv_rope (an RMSNorm weight required) for q and k of weight
+// format qtype_qk and v of format qtype_v in one launch.  *launched false
+// (status 0, nothing enqueued) when the shapes, alignments or format pair
+// need one launch per format.
+int rmsnorm_qkv_rope_two(const void* wq, const void* wk, int qtype_qk, const void* wv,
+                         int qtype_v, const float* h, const void* norm_w, int norm_type,
+                         float eps, int cols, float* q_out, void* k_cache, void* v_cache,
+                         int kv_type, const int32_t* pos, int max_ctx, int head_dim,
+                         int n_heads, int n_heads_kv, float freq_base, hipStream_t stream,
+                         bool* launched);
+
 }  // namespace jinf

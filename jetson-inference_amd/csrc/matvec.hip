@@ -546,343 +546,11 @@ constexpr bool mv_defers(int epi) { return epi == kEpiSwiGLU; }
 template <int QT, bool ONE_TILE, int PRO, int EPI, int WV1, bool TALL = false, int XW = 28>
 __global__ __launch_bounds__(ONE_TILE ? 64 * WV1 : 512) void matvec_kernel(MvJob job,
                                                                            MvTheta<EPI> th) {
-    using F = MvFmt<QT>;
-    constexpr bool WIDE = !ONE_TILE || TALL;
-    using G = MvGroup<QT, EPI, WIDE>;
-    constexpr int R = G::R;
-    using T = MvTile<QT, R>;
-    constexpr int CPL = T::kCPL;
-    extern __shared__ uint4 lds[];
-    float4* xl = reinterpret_cast<float4*>(lds);
-    const int waves = blockDim.x / kWave;
-    // wave index in a scalar register: the walk over items below is then
-    // wave-uniform control flow (no exec-masked paths whose merged wait
-    // counts would hold the next prefetch until the current one has landed)
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int lane = threadIdx.x & (kWave - 1);
-    const int nb = job.nb;
-    int nt = job.nt;
-    // x region: per tile 1024 float4 (MvXFloat formats) or 64 plane records
-    constexpr int XT16 = F::kPlanes ? kMvRecTile16 : 1024;
-    uint32_t* xrec = reinterpret_cast<uint32_t*>(lds);
-    uint4* stage = lds + nt * XT16 + wave * T::kStageChunks;
-    const int n_groups = G::groups(job);
-    const int stride = gridDim.x * waves;
-    if (ONE_TILE) nt = 1;
-
-    using Buf = uint4[R][CPL];
-    // kEpiAdd: the group's y values ride with each item's weights (loaded
-    // ahead, so the residual add does not wait for a load after the dot
-    // product; only the owning wave reads or writes a row of y)
-    using YBuf = float[R];
-    auto fetch = [&](int g, int t, Buf& buf, YBuf& yb) {
-        if constexpr (EPI == kEpiAdd) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int row = g * R + r < job.rows ? g * R + r : job.rows - 1;
-                yb[r] = job.y[row];
-            }
-        } else {
-            (void)yb;
-        }
-        const int tb = t * T::kTileBlocks;
-        const int nbt = nb - tb < T::kTileBlocks ? nb - tb : T::kTileBlocks;
-        const int nchunk = nbt * F::kBytes / 16;  // whole by the width granule
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint8_t* src = mv_row<QT, EPI, WIDE>(job, g, r) + (int64_t)tb * F::kBytes;
-#pragma unroll
-            for (int k = 0; k < CPL; ++k) {
-                // Lanes past the tile's end re-read its last chunk (never used).
-                const int c = lane + kWave * k < nchunk ? lane + kWave * k : nchunk - 1;
-                buf[r][k] = ld16<true>(src + 16 * c);
-            }
-        }
-    };
-    auto advance = [&](int& g, int& t) {
-        if (ONE_TILE) {
-            g += stride;
-        } else if (++t == nt) {
-            t = 0;
-            g += stride;
-        }
-    };
-
-    int g0 = blockIdx.x * waves + wave, t0 = 0;
-    uint4 bufA[R][CPL];
-    uint4 bufB[R][CPL];
-    float yA[R], yB[R];
-
-    // Operands of the prologue are loaded before the first weight prefetch:
-    // vector loads complete in order, so a load issued after the prefetch
-    // would make the x staging, the norm and the RoPE table wait for the
-    // weights' HBM latency instead of overlapping it.  x (zero past the last
-    // value): XPT float4 per thread cover the staged tiles (one tile: 1024
-    // float4 over 64 WV1 threads; wide: XW, chosen by the launcher for the
-    // tile count: unneeded slots would each cost a branch and 4 registers,
-    // and the 4-tile down projection stages in 9.4 against 10.2 us with 8
-    // slots instead of 28).
-    constexpr int XPT = ONE_TILE ? 16 / WV1 : XW;
-    // float4 number of slot k: plane formats take word groups of two
-    // consecutive float4 (group threadIdx.x + (k / 2) blockDim.x)
-    auto fi = [&](int k) {
-        return F::kPlanes ? 2 * ((int)threadIdx.x + (k >> 1) * (int)blockDim.x) + (k & 1)
-                          : (int)threadIdx.x + k * (int)blockDim.x;
-    };
-    const float4* x4 = reinterpret_cast<const float4*>(job.x);
-    const int nx4 = nb * (F::kElems / 4);
-    const int nxs = nt << 10;
-    float4 xr[XPT];
-#pragma unroll
-    for (int k = 0; k < XPT; ++k) {
-        const int f = fi(k);
-        xr[k] = f < nx4 ? x4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    // norm weights g of the same slots (fp32, or fp16 in the low 8 bytes),
-    // early for single-tile matrices only (held with x, the multi-tile
-    // kernel's registers would spill; it reads g after the reduction)
-    constexpr bool NW_EARLY = PRO == kProNorm && ONE_TILE;
-    uint4 nwr[NW_EARLY ? XPT : 1];
-    auto load_nw = [&](int k) {
-        const int f = fi(k);
-        uint4 r = make_uint4(0, 0, 0, 0);
-        if (f < nx4) {
-            if (job.norm_f16) {
-                const uint2 u = reinterpret_cast<const uint2*>(job.norm_w)[f];
-                r = make_uint4(u.x, u.y, 0, 0);
-            } else {
-                r = reinterpret_cast<const uint4*>(job.norm_w)[f];
-            }
-        }
-        return r;
-    };
-    if constexpr (NW_EARLY) {
-#pragma unroll
-        for (int k = 0; k < XPT; ++k) nwr[k] = load_nw(k);
-    }
-    // RoPE: the position and this lane's theta
-    int rpos = 0;
-    float rth = 0.0f;
-    if constexpr (EPI == kEpiQKV) {
-        rpos = job.pos[0];
-        if (threadIdx.x < job.head_dim / 2) rth = th.t[threadIdx.x];
-    }
-    // first weight item (a wave past the last group fetches the last row's
-    // bytes and never uses them: the load count stays the same on every path)
-    fetch(g0, t0, bufA, yA);
-
-    // RoPE: the position's (cos, sin) for every pair index, computed once per
-    // workgroup (one sin/cos per lane) instead of once per finished pair in
-    // the finishing lane
-    __shared__ float2 rcs[EPI == kEpiQKV ? kRopeMaxHalf : 1];
-    if constexpr (EPI == kEpiQKV) {
-        if (threadIdx.x < job.head_dim / 2) rcs[threadIdx.x] = rope_cs(rpos, rth);
-    }
-
-    // Stage x while the first weights are in flight.
-    if constexpr (PRO == kProNorm) {
-        __shared__ double red[8];
-        double ss = 0.0;
-#pragma unroll
-        for (int k = 0; k < XPT; ++k) {
-            const float4 v = xr[k];
-            ss = fma((double)v.x, (double)v.x, ss);
-            ss = fma((double)v.y, (double)v.y, ss);
-            ss = fma((double)v.z, (double)v.z, ss);
-            ss = fma((double)v.w, (double)v.w, ss);
-        }
-        // DPP wave sums, one LDS exchange and one barrier (`red` is not reused)
-        ss = wave_sum_f64(ss);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        ss = red[0];
-        for (int i = 1; i < waves; ++i) ss += red[i];
-        const float rs = rms_scale(ss, nb * F::kElems, job.eps);
-        // x_j = fl32(fl32(h_j * rs) * g_j), written once
-#pragma unroll
-        for (int k = 0; k < XPT; ++k) {
-            const int f = fi(k);
-            if (f < nxs) {
-                float4 v = xr[k];
-                if (f < nx4) {
-                    uint4 nw;
-                    if constexpr (NW_EARLY)
-                        nw = nwr[k];
-                    else
-                        nw = load_nw(k);
-                    float w[4];
-                    if (job.norm_f16) {
-                        w[0] = h2f((uint16_t)(nw.x & 0xFFFFu));
-                        w[1] = h2f((uint16_t)(nw.x >> 16));
-                        w[2] = h2f((uint16_t)(nw.y & 0xFFFFu));
-                        w[3] = h2f((uint16_t)(nw.y >> 16));
-                    } else {
-                        w[0] = __builtin_bit_cast(float, nw.x);
-                        w[1] = __builtin_bit_cast(float, nw.y);
-                        w[2] = __builtin_bit_cast(float, nw.z);
-                        w[3] = __builtin_bit_cast(float, nw.w);
-                    }
-                    {
-#pragma clang fp contract(off)
-                        v.x = (v.x * rs) * w[0];
-                        v.y = (v.y * rs) * w[1];
-                        v.z = (v.z * rs) * w[2];
-                        v.w = (v.w * rs) * w[3];
-                    }
-                }
-                if constexpr (F::kPlanes)
-                    xr[k] = v;
-                else
-                    xl[mv_xslot(f >> 10, (f >> 4) & 63, f & 15)] = v;
-            }
-        }
-    }
-    if constexpr (F::kPlanes) {
-        // 2 g < nxs holds for whole waves (nxs is a multiple of 1024), so the
-        // four lanes of a block stage it together
-#pragma unroll
-        for (int k = 0; k < XPT; k += 2) {
-            const int g = threadIdx.x + (k >> 1) * blockDim.x;
-            if (2 * g < nxs) mv_stage_planes(xrec, g, xr[k], xr[k + 1]);
-        }
-    } else if constexpr (PRO != kProNorm) {
-#pragma unroll
-        for (int k = 0; k < XPT; ++k) {
-            const int f = fi(k);
-            if (f < nxs) xl[mv_xslot(f >> 10, (f >> 4) & 63, f & 15)] = xr[k];
-        }
-    }
-    __syncthreads();
-    if (g0 >= n_groups) return;
-
-    typename F::XReg xw;
-    auto load_x = [&](int t) {
-        if constexpr (F::kPlanes) {
-            const uint4* rp = reinterpret_cast<const uint4*>(xrec + (t * kWave + lane) * kMvRecWords);
-#pragma unroll
-            for (int i = 0; i < 12; ++i) {
-                const uint4 u = rp[i];
-                xw.p[4 * i] = u.x; xw.p[4 * i + 1] = u.y; xw.p[4 * i + 2] = u.z; xw.p[4 * i + 3] = u.w;
-            }
-            const uint4 u = rp[12];
-            xw.inv[0] = __uint_as_float(u.x);
-            xw.inv[1] = __uint_as_float(u.y);
-            xw.sx[0] = (int)u.z;
-            xw.sx[1] = (int)u.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const float4 v = xl[mv_xslot(t, lane, j)];
-                xw.v[4 * j] = v.x; xw.v[4 * j + 1] = v.y; xw.v[4 * j + 2] = v.z; xw.v[4 * j + 3] = v.w;
-            }
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                float s = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) s += xw.v[16 * k + i];
-                xw.s[k] = s;
-            }
-            F::prep(xw.v);
-        }
-    };
-    if (ONE_TILE) load_x(0);
-
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-
-    // kEpiSwiGLU: lane k keeps the k-th finished group's gate and up sums
-    // (every lane holds the wave sums), and the lanes evaluate silu(gate) * up
-    // and store together at the end, instead of one lane per group while the
-    // wave waits; the epilogue's registers are then not live in the loop.  A
-    // wave finishes at most 64 groups (mv_run sizes the grid so).
-    constexpr bool DEFER = mv_defers(EPI);
-    int dk_g = -1, dk_n = 0;
-    float dk_v[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) dk_v[r] = 0.0f;
-    auto dk_flush = [&]() {
-        if (dk_g >= 0) mv_epilogue<QT, EPI, WIDE>(job, th, dk_g, dk_v, nullptr, rpos, rcs);
-        dk_g = -1;
-    };
-
-    auto process = [&](int g, int t, const Buf& buf, const YBuf& yb) {
-        if (!ONE_TILE) load_x(t);
-        const bool live = t * kMvTileElems + lane * kMvLaneElems < nb * F::kElems;
-        // Every lane writes every chunk (no branch, so no load is left pending
-        // on a skipped path).  The last pass goes first: its slots past
-        // kChunks land on the next row's first chunks, which the first pass
-        // then overwrites (a wave's LDS writes complete in order), and the
-        // last row's on the pad.
-#pragma unroll
-        for (int r = 0; r < R; ++r) stage[r * T::kChunks + lane + (CPL - 1) * kWave] = buf[r][CPL - 1];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int k = 0; k < CPL - 1; ++k) stage[r * T::kChunks + lane + kWave * k] = buf[r][k];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint32_t* rowp = reinterpret_cast<const uint32_t*>(stage + r * T::kChunks);
-            if (live) acc[r] += F::dot(rowp, lane, xw);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (t == nt - 1) {  // group complete: reduce and finish its rows
-            float v[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                v[r] = wave_sum_f32(acc[r]);
-                acc[r] = 0.0f;
-            }
-            if constexpr (DEFER) {
-                if (lane == dk_n) {
-                    dk_g = g;  // below n_groups
-#pragma unroll
-                    for (int r = 0; r < R; ++r) dk_v[r] = v[r];
-                }
-                ++dk_n;
-            } else if (lane == 0) {
-                mv_epilogue<QT, EPI, WIDE>(job, th, g, v, yb, rpos, rcs);
-            }
-        }
-    };
-
-    // The wave's items (its groups g0, g0 + stride, ... below n_groups, each
-    // over its tiles), counted up front: the loop below has no exit but its
-    // own test, so every fetch in it is unconditional and the compiler's wait
-    // counts at the loop head see exactly the one item in flight (an exit
-    // taken from inside the loop, or a conditional fetch, merges paths on
-    // which other buffers look pending, and the next prefetch then waits for
-    // the current one).  The last one or two items follow the loop.
-    const int n_items = ((n_groups - 1 - g0) / stride + 1) * nt;
-    int g = g0, t = t0;  // the item held in bufA
-    int rem = n_items;
-    while (rem > 2) {
-        int g1 = g, t1 = t;
-        advance(g1, t1);
-        fetch(g1, t1, bufB, yB);
-        process(g, t, bufA, yA);
-        g = g1;
-        t = t1;
-        advance(g, t);
-        fetch(g, t, bufA, yA);
-        process(g1, t1, bufB, yB);
-        rem -= 2;
-    }
-    if (rem == 2) {
-        int g1 = g, t1 = t;
-        advance(g1, t1);
-        fetch(g1, t1, bufB, yB);
-        process(g, t, bufA, yA);
-        process(g1, t1, bufB, yB);
-    } else {
-        process(g, t, bufA, yA);
-    }
-    if constexpr (DEFER) dk_flush();
+#define MV_BID blockIdx.x
+#define MV_NBLK gridDim.x
+#include "matvec_body.inc"
+#undef MV_BID
+#undef MV_NBLK
 }
 
 // Any width / alignment: one wave per group of R rows; each lane takes
@@ -937,6 +605,88 @@ __global__ __launch_bounds__(256) void matvec_any_kernel(MvJob job, MvTheta<EPI>
     for (int r = 0; r < R; ++r) v[r] = wave_sum_f32(acc[r]);
     if (lane == 0) mv_epilogue<QT, EPI>(job, th, g, v, nullptr, EPI == kEpiQKV ? job.pos[0] : 0);
 }
+
+// Host checks shared with the two-format Q/K/V launch (matvec_qkv2.hip).
+static int q_elems(int qtype) {
+    switch (qtype) {
+        case kQ4_0: case kQ8_0: return 32;
+        case kQ4_K: case kQ6_K: return 256;
+        default: return 0;
+    }
+}
+
+// Common checks: a served qtype, whole blocks, 4-byte aligned vectors.
+static int mv_check(int qtype, int rows, int cols, const float* x, const float* y) {
+    const int e = q_elems(qtype);
+    if (e == 0 || rows < 0 || cols < 0) return JINF_HIP_ERR_INVALID;
+    if (rows == 0 || cols == 0) return -1;  // nothing to do
+    if (!x || !y || cols % e != 0) return JINF_HIP_ERR_INVALID;
+    if (!aligned(x, 4) || !aligned(y, 4)) return JINF_HIP_ERR_INVALID;
+    return JINF_HIP_OK;
+}
+
+static int norm_setup(MvJob& j, const void* norm_w, int norm_type, float eps) {
+    j.norm_w = norm_w;
+    j.norm_f16 = norm_type == JINF_HIP_F16;
+    j.eps = eps;
+    if (!norm_w) return JINF_HIP_OK;
+    if (norm_type != JINF_HIP_F32 && norm_type != JINF_HIP_F16) return JINF_HIP_ERR_INVALID;
+    if (!aligned(norm_w, norm_type == JINF_HIP_F16 ? 2 : 4) || !(eps >= 0.0f))
+        return JINF_HIP_ERR_INVALID;
+    return JINF_HIP_OK;
+}
+
+// The Q/K/V job of jinf_rmsnorm_qkv_rope after its checks; *none when there
+// is nothing to compute.
+static int qkv_job(MvJob& j, bool* none, const void* wq, const void* wk, const void* wv,
+                   int qtype, const float* h, const void* norm_w, int norm_type, float eps,
+                   int cols, float* q_out, void* k_cache, void* v_cache, int kv_type,
+                   const int32_t* pos, int max_ctx, int head_dim, int n_heads, int n_heads_kv,
+                   float freq_base) {
+    *none = true;
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim / 2 > kRopeMaxHalf || n_heads < 0 ||
+        n_heads_kv < 0 || max_ctx < 0)
+        return JINF_HIP_ERR_INVALID;
+    if (kv_type != JINF_HIP_F32 && kv_type != JINF_HIP_F16) return JINF_HIP_ERR_INVALID;
+    if (!(freq_base > 0.0f)) return JINF_HIP_ERR_INVALID;
+    const int64_t qd = (int64_t)n_heads * head_dim, kvd = (int64_t)n_heads_kv * head_dim;
+    const int64_t rq = wq ? qd : 0, rk = wk ? kvd : 0, rv = wv ? kvd : 0;
+    if (rq + rk + rv > 0x7FFFFFFF) return JINF_HIP_ERR_INVALID;
+    const int rows = (int)(rq + rk + rv);
+    if (rows == 0) return JINF_HIP_OK;
+    if ((wq && !q_out) || (wk && !k_cache) || (wv && !v_cache) || !pos)
+        return JINF_HIP_ERR_INVALID;
+    if (q_out && !aligned(q_out, 4)) return JINF_HIP_ERR_INVALID;
+    const int es = kv_type == JINF_HIP_F16 ? 2 : 4;
+    if ((k_cache && !aligned(k_cache, es)) || (v_cache && !aligned(v_cache, es)))
+        return JINF_HIP_ERR_INVALID;
+    const int c = mv_check(qtype, rows, cols, h, q_out ? q_out : h);
+    if (c != JINF_HIP_OK) return c < 0 ? JINF_HIP_OK : c;
+    j = MvJob{};
+    if (norm_setup(j, norm_w, norm_type, eps) != JINF_HIP_OK) return JINF_HIP_ERR_INVALID;
+    // q, k, v segments in that order; an absent one is empty
+    const void* first = wq ? wq : wk ? wk : wv;
+    j.W[0] = static_cast<const uint8_t*>(wq ? wq : first);
+    j.W[1] = static_cast<const uint8_t*>(wk ? wk : first);
+    j.W[2] = static_cast<const uint8_t*>(wv ? wv : first);
+    j.seg_end[0] = (int)rq;
+    j.seg_end[1] = (int)(rq + rk);
+    j.seg_end[2] = rows;
+    j.rows = rows;
+    j.x = h;
+    j.y = q_out;
+    j.kc = k_cache;
+    j.vc = v_cache;
+    j.pos = pos;
+    j.kv_f16 = kv_type == JINF_HIP_F16;
+    j.kv_dim = (int)kvd;
+    j.head_dim = head_dim;
+    j.max_ctx = max_ctx;
+    *none = false;
+    return JINF_HIP_OK;
+}
+
+#ifndef JINF_MATVEC_KERNELS_ONLY
 
 // Workgroups of the tall one-tile kernel (these template arguments, `threads`
 // lanes, `shmem` bytes) that the device holds at once: its occupancy per CU
@@ -1049,35 +799,6 @@ static int mv_dispatch(int qtype, const MvJob& job, int cols, const MvTheta<EPI>
     }
 }
 
-static int q_elems(int qtype) {
-    switch (qtype) {
-        case kQ4_0: case kQ8_0: return 32;
-        case kQ4_K: case kQ6_K: return 256;
-        default: return 0;
-    }
-}
-
-// Common checks: a served qtype, whole blocks, 4-byte aligned vectors.
-static int mv_check(int qtype, int rows, int cols, const float* x, const float* y) {
-    const int e = q_elems(qtype);
-    if (e == 0 || rows < 0 || cols < 0) return JINF_HIP_ERR_INVALID;
-    if (rows == 0 || cols == 0) return -1;  // nothing to do
-    if (!x || !y || cols % e != 0) return JINF_HIP_ERR_INVALID;
-    if (!aligned(x, 4) || !aligned(y, 4)) return JINF_HIP_ERR_INVALID;
-    return JINF_HIP_OK;
-}
-
-static int norm_setup(MvJob& j, const void* norm_w, int norm_type, float eps) {
-    j.norm_w = norm_w;
-    j.norm_f16 = norm_type == JINF_HIP_F16;
-    j.eps = eps;
-    if (!norm_w) return JINF_HIP_OK;
-    if (norm_type != JINF_HIP_F32 && norm_type != JINF_HIP_F16) return JINF_HIP_ERR_INVALID;
-    if (!aligned(norm_w, norm_type == JINF_HIP_F16 ? 2 : 4) || !(eps >= 0.0f))
-        return JINF_HIP_ERR_INVALID;
-    return JINF_HIP_OK;
-}
-
 static int matvec(const void* w, int qtype, const float* x, float* y, int rows, int cols,
                   hipStream_t stream) {
     const int c = mv_check(qtype, rows, cols, x, y);
@@ -1143,51 +864,23 @@ static int rmsnorm_qkv_rope(const void* wq, const void* wk, const void* wv, int 
                             int cols, float* q_out, void* k_cache, void* v_cache, int kv_type,
                             const int32_t* pos, int max_ctx, int head_dim, int n_heads,
                             int n_heads_kv, float freq_base, hipStream_t stream) {
-    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim / 2 > kRopeMaxHalf || n_heads < 0 ||
-        n_heads_kv < 0 || max_ctx < 0)
-        return JINF_HIP_ERR_INVALID;
-    if (kv_type != JINF_HIP_F32 && kv_type != JINF_HIP_F16) return JINF_HIP_ERR_INVALID;
-    if (!(freq_base > 0.0f)) return JINF_HIP_ERR_INVALID;
-    const int64_t qd = (int64_t)n_heads * head_dim, kvd = (int64_t)n_heads_kv * head_dim;
-    const int64_t rq = wq ? qd : 0, rk = wk ? kvd : 0, rv = wv ? kvd : 0;
-    if (rq + rk + rv > 0x7FFFFFFF) return JINF_HIP_ERR_INVALID;
-    const int rows = (int)(rq + rk + rv);
-    if (rows == 0) return JINF_HIP_OK;
-    if ((wq && !q_out) || (wk && !k_cache) || (wv && !v_cache) || !pos)
-        return JINF_HIP_ERR_INVALID;
-    if (q_out && !aligned(q_out, 4)) return JINF_HIP_ERR_INVALID;
-    const int es = kv_type == JINF_HIP_F16 ? 2 : 4;
-    if ((k_cache && !aligned(k_cache, es)) || (v_cache && !aligned(v_cache, es)))
-        return JINF_HIP_ERR_INVALID;
-    const int c = mv_check(qtype, rows, cols, h, q_out ? q_out : h);
-    if (c != JINF_HIP_OK) return c < 0 ? JINF_HIP_OK : c;
-    MvJob j{};
-    if (norm_setup(j, norm_w, norm_type, eps) != JINF_HIP_OK) return JINF_HIP_ERR_INVALID;
-    // q, k, v segments in that order; an absent one is empty
-    const void* first = wq ? wq : wk ? wk : wv;
-    j.W[0] = static_cast<const uint8_t*>(wq ? wq : first);
-    j.W[1] = static_cast<const uint8_t*>(wk ? wk : first);
-    j.W[2] = static_cast<const uint8_t*>(wv ? wv : first);
-    j.seg_end[0] = (int)rq;
-    j.seg_end[1] = (int)(rq + rk);
-    j.seg_end[2] = rows;
-    j.rows = rows;
-    j.x = h;
-    j.y = q_out;
-    j.kc = k_cache;
-    j.vc = v_cache;
-    j.pos = pos;
-    j.kv_f16 = kv_type == JINF_HIP_F16;
-    j.kv_dim = (int)kvd;
-    j.head_dim = head_dim;
-    j.max_ctx = max_ctx;
+    MvJob j;
+    bool none;
+    const int rc = qkv_job(j, &none, wq, wk, wv, qtype, h, norm_w, norm_type, eps, cols, q_out,
+                           k_cache, v_cache, kv_type, pos, max_ctx, head_dim, n_heads,
+                           n_heads_kv, freq_base);
+    if (rc != JINF_HIP_OK || none) return rc;
     RopeTheta th;
     theta_table(th, head_dim, freq_base);
     if (!norm_w) return mv_dispatch<kProNone, kEpiQKV>(qtype, j, cols, th, stream);
     return mv_dispatch<kProNorm, kEpiQKV>(qtype, j, cols, th, stream);
 }
 
+#endif  // JINF_MATVEC_KERNELS_ONLY
+
 }  // namespace jinf
+
+#ifndef JINF_MATVEC_KERNELS_ONLY
 
 extern "C" int jinf_matvec_q4_0(const void* weight, const float* x, float* y, int rows,
                                 int cols, hipStream_t stream) {
@@ -1243,3 +936,5 @@ extern "C" int jinf_rmsnorm_qkv_rope(const void* w_q, const void* w_k, const voi
                                   k_cache, v_cache, kv_type, pos, max_ctx, head_dim, n_heads,
                                   n_heads_kv, freq_base, stream);
 }
+
+#endif  // JINF_MATVEC_KERNELS_ONLY
